@@ -1,0 +1,351 @@
+// Fused backward: midpoint-trajectory replay + discrete adjoint + cell moments
+// (cpab_ops_1d.cu:331-422, cpab_ops_2d.cu:384-513, cpab_ops_3d.cu:405-532).
+//
+// Per trajectory (one lane):
+//   phase 1  T explicit-midpoint steps from p0, keeping a checkpoint every kSeg
+//            steps.  The checkpoint array lives in VGPRs: phase 1 is unrolled
+//            over segments so every store has a static index, and phase 2 reads
+//            a checkpoint with a uniform select chain (no scratch memory).
+//   phase 2  segments last to first: replay kSeg steps from the checkpoint into
+//            a register buffer, then walk them backwards propagating lambda and
+//            accumulating the 2x3 (1x2, 3x4) moment of the current cell; the
+//            moment is flushed whenever the cell changes, exactly as the
+//            reference groups its flushes.
+//
+// Moment accumulation on MI355X: each workgroup serves ONE theta, and when the
+// nC x ppc table fits it keeps a private copy of that theta's moments in LDS
+// (ds_add_f32, no HBM atomics).  At the end the workgroup writes its table as
+// one partial (plain coalesced stores); a separate pass sums the partials in a
+// fixed order.  When the table does not fit (3D at 10x10x10: 234 KiB) flushes
+// go to HBM with global_atomic_add_f32, pre-aggregated across the wave for
+// lanes that share a cell.
+#include <hip/hip_runtime.h>
+#include "cpab_device.hpp"
+#include "cpab_launch.hpp"
+
+namespace cpab {
+namespace {
+
+template <int D> struct Dim;
+template <> struct Dim<1> { static constexpr int P = 2; };
+template <> struct Dim<2> { static constexpr int P = 6; };
+template <> struct Dim<3> { static constexpr int P = 12; };
+
+struct Cells { int nx, ny, nz; };
+
+template <int D> __device__ __forceinline__ int lookup(const float (&p)[D], const Cells& g);
+template <> __device__ __forceinline__ int lookup<1>(const float (&p)[1], const Cells& g) {
+  return cell_1d(p[0], g.nx);
+}
+template <> __device__ __forceinline__ int lookup<2>(const float (&p)[2], const Cells& g) {
+  return cell_2d(p[0], p[1], g.nx, g.ny);
+}
+template <> __device__ __forceinline__ int lookup<3>(const float (&p)[3], const Cells& g) {
+  return cell_3d(p[0], p[1], p[2], g.nx, g.ny, g.nz);
+}
+
+template <int D, typename Ptr> __device__ __forceinline__ Aff<D> fetch(Ptr tab, int c);
+template <> __device__ __forceinline__ Aff<1> fetch<1>(const float* tab, int c) { return load_aff1(tab, c); }
+template <> __device__ __forceinline__ Aff<2> fetch<2>(const float* tab, int c) { return load_aff2(tab, c); }
+template <> __device__ __forceinline__ Aff<3> fetch<3>(const float* tab, int c) { return load_aff3(tab, c); }
+
+__device__ __forceinline__ void velocity(const Aff<1>& A, const float (&p)[1], float (&v)[1]) {
+  v[0] = fmaf(A.a, p[0], A.b);
+}
+__device__ __forceinline__ void velocity(const Aff<2>& A, const float (&p)[2], float (&v)[2]) {
+  apply2(A, p[0], p[1], v[0], v[1]);
+}
+__device__ __forceinline__ void velocity(const Aff<3>& A, const float (&p)[3], float (&v)[3]) {
+  apply3(A, p[0], p[1], p[2], v[0], v[1], v[2]);
+}
+
+__device__ __forceinline__ void midpoint(const Aff<1>& A, float (&p)[1], float h, float hh) {
+  p[0] = midpoint1(A, p[0], h, hh);
+}
+__device__ __forceinline__ void midpoint(const Aff<2>& A, float (&p)[2], float h, float hh) {
+  midpoint2(A, p[0], p[1], h, hh);
+}
+__device__ __forceinline__ void midpoint(const Aff<3>& A, float (&p)[3], float h, float hh) {
+  midpoint3(A, p[0], p[1], p[2], h, hh);
+}
+
+__device__ __forceinline__ void adjoint(const Aff<1>& A, const float (&p)[1], float h, float hh,
+                                        float hhh, float (&m)[2], float (&l)[1]) {
+  adjoint1(A, p[0], h, hh, hhh, m, l[0]);
+}
+__device__ __forceinline__ void adjoint(const Aff<2>& A, const float (&p)[2], float h, float hh,
+                                        float hhh, float (&m)[6], float (&l)[2]) {
+  adjoint2(A, p[0], p[1], h, hh, hhh, m, l[0], l[1]);
+}
+__device__ __forceinline__ void adjoint(const Aff<3>& A, const float (&p)[3], float h, float hh,
+                                        float hhh, float (&m)[12], float (&l)[3]) {
+  adjoint3(A, p[0], p[1], p[2], h, hh, hhh, m, l[0], l[1], l[2]);
+}
+
+// One replay step from p in cell c (already looked up): explicit midpoint, or
+// with adaptive_substeps the Heun correction when the step leaves the cell
+// (cpab_ops_2d.cu:294-332).
+template <int D, bool ADAPTIVE>
+__device__ __forceinline__ void replay_step(const float* tab, int c, float (&p)[D], float h,
+                                            float hh, const Cells& g) {
+  const Aff<D> A = fetch<D>(tab, c);
+  if (!ADAPTIVE) {
+    midpoint(A, p, h, hh);
+    return;
+  }
+  float q[D];
+#pragma unroll
+  for (int k = 0; k < D; ++k) q[k] = p[k];
+  midpoint(A, q, h, hh);
+  const int ce = lookup<D>(q, g);
+  if (ce == c) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) p[k] = q[k];
+    return;
+  }
+  float v0[D], v1[D];
+  velocity(A, p, v0);
+  velocity(fetch<D>(tab, ce), q, v1);
+#pragma unroll
+  for (int k = 0; k < D; ++k) p[k] = fmaf(hh, v0[k] + v1[k], p[k]);
+}
+
+// Checkpoint stack in VGPRs.  Phase 2 consumes checkpoints in exactly the
+// reverse order phase 1 produces them, so a shift register with static
+// indices suffices: push shifts every entry up one slot, pop shifts down.
+// (A select chain over a runtime index gets turned into a scratch-memory
+// table by the compiler; shifting keeps everything in registers.)
+template <int N>
+__device__ __forceinline__ void stack_push(float (&a)[N], float v) {
+#pragma unroll
+  for (int k = N - 1; k > 0; --k) a[k] = a[k - 1];
+  a[0] = v;
+}
+template <int N>
+__device__ __forceinline__ float stack_pop(float (&a)[N]) {
+  const float v = a[0];
+#pragma unroll
+  for (int k = 0; k < N - 1; ++k) a[k] = a[k + 1];
+  return v;
+}
+
+template <int P>
+__device__ __forceinline__ void flush_lds(float* bins, int c, const float (&m)[P]) {
+  float* q = bins + P * c;
+#pragma unroll
+  for (int k = 0; k < P; ++k)
+    __hip_atomic_fetch_add(q + k, m[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Global flush for a converged wave (all 64 lanes active; `need` marks the
+// lanes that flush).  Lanes flushing the same cell are summed with a
+// wave-wide butterfly and the lowest of them issues the atomics, which is
+// what cpab_ops_2d.cu:6-59 does with __match_any_sync.  A readfirstlane /
+// ballot loop peels one cell group at a time; once the next group is small
+// (incoherent points) every remaining lane adds its own values instead.
+template <int P>
+__device__ __forceinline__ void flush_global(float* __restrict__ mom, bool need, int c,
+                                             const float (&m)[P]) {
+  const int lane = __lane_id();
+  uint64_t todo = __ballot(need);
+  while (todo) {
+    const int leader = __ffsll((unsigned long long)todo) - 1;
+    const int lc = __shfl(c, leader);
+    const bool in = need && c == lc;
+    const uint64_t grp = __ballot(in) & todo;
+    if (__popcll(grp) < 4) {
+      if ((todo >> lane) & 1) {
+#pragma unroll
+        for (int k = 0; k < P; ++k) unsafeAtomicAdd(mom + (size_t)P * c + k, m[k]);
+      }
+      break;
+    }
+    todo &= ~grp;
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+      float v = in ? m[k] : 0.0f;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+      if (lane == leader) unsafeAtomicAdd(mom + (size_t)P * lc + k, v);
+    }
+  }
+}
+
+template <int D, bool ADAPTIVE, bool LDS_A, bool LDS_BINS>
+__global__ __launch_bounds__(512) void backward_kernel(
+    int nP, int batched, int T, Cells g, int nC, const float* __restrict__ points,
+    const float* __restrict__ As, const float* __restrict__ grad_out,
+    float* __restrict__ moments, float* __restrict__ partials, float* __restrict__ grad_points) {
+  constexpr int P = Dim<D>::P;
+  extern __shared__ float lds[];
+  const int b = blockIdx.y;
+  const int R = nC * P;
+  const float* __restrict__ Ag = As + (size_t)b * R;
+  float* ldsA = lds;
+  float* bins = lds + (LDS_A ? R : 0);
+  if (LDS_A) {
+    const float2* s2 = reinterpret_cast<const float2*>(Ag);
+    float2* d2 = reinterpret_cast<float2*>(ldsA);
+    for (int i = threadIdx.x; i < R / 2; i += blockDim.x) d2[i] = s2[i];
+  }
+  if (LDS_BINS) {
+    for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
+  }
+  if (LDS_A || LDS_BINS) __syncthreads();
+  const float* tab = LDS_A ? static_cast<const float*>(ldsA) : Ag;
+  float* __restrict__ mom_b = moments + (size_t)b * R;
+
+  const float h = 1.0f / (float)T;
+  const float hh = h * 0.5f;
+  const float hhh = hh * h;
+  const int nseg = (T + kSeg - 1) / kSeg;
+  const float* __restrict__ pts = points + (batched ? (size_t)b * D * nP : 0);
+  const float* __restrict__ gout = grad_out + (size_t)b * D * nP;
+
+  // The loop bound is uniform so every wave stays converged (the global flush
+  // needs all 64 lanes); lanes past nP replay a clamped point and contribute nothing.
+  for (int base = blockIdx.x * blockDim.x; base < nP; base += gridDim.x * blockDim.x) {
+    const int pi0 = base + (int)threadIdx.x;
+    const bool valid = pi0 < nP;
+    const int pi = valid ? pi0 : nP - 1;
+    float p[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) p[k] = pts[pi + (size_t)k * nP];
+
+    // Phase 1: checkpoint (position before step seg*kSeg) pushed per segment.
+    float ck[D][kMaxSeg];
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+#pragma unroll
+      for (int i = 0; i < kMaxSeg; ++i) ck[k][i] = 0.0f;
+    for (int seg = 0; seg < nseg; ++seg) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) stack_push(ck[k], p[k]);
+      const int len = min(kSeg, T - seg * kSeg);
+      for (int s = 0; s < len; ++s) replay_step<D, ADAPTIVE>(tab, lookup<D>(p, g), p, h, hh, g);
+    }
+
+    // Phase 2: reverse sweep.
+    float lam[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) lam[k] = gout[pi + (size_t)k * nP];
+    float m[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) m[k] = 0.0f;
+    int prev = -1;
+    for (int seg = nseg - 1; seg >= 0; --seg) {
+      const int len = min(kSeg, T - seg * kSeg);
+      float q[D];
+#pragma unroll
+      for (int k = 0; k < D; ++k) q[k] = stack_pop(ck[k]);
+      float sp[kSeg][D];
+      int sc[kSeg];
+#pragma unroll
+      for (int s = 0; s < kSeg; ++s) {
+        if (s < len) {
+          const int c = lookup<D>(q, g);
+          sc[s] = c;
+#pragma unroll
+          for (int k = 0; k < D; ++k) sp[s][k] = q[k];
+          replay_step<D, ADAPTIVE>(tab, c, q, h, hh, g);
+        }
+      }
+#pragma unroll
+      for (int s = kSeg - 1; s >= 0; --s) {
+        if (s < len) {
+          const int c = sc[s];
+          const bool need = valid && c != prev && prev >= 0;
+          if (LDS_BINS) {
+            if (need) flush_lds<P>(bins, prev, m);
+          } else {
+            flush_global<P>(mom_b, need, prev, m);
+          }
+          if (c != prev) {
+#pragma unroll
+            for (int k = 0; k < P; ++k) m[k] = 0.0f;
+            prev = c;
+          }
+          adjoint(fetch<D>(tab, c), sp[s], h, hh, hhh, m, lam);
+        }
+      }
+    }
+    if (LDS_BINS) {
+      if (valid) flush_lds<P>(bins, prev, m);
+    } else {
+      flush_global<P>(mom_b, valid, prev, m);
+    }
+    if (grad_points && valid) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) grad_points[(size_t)b * D * nP + pi + (size_t)k * nP] = lam[k];
+    }
+  }
+
+  if (LDS_BINS) {
+    __syncthreads();
+    float* dst = partials + ((size_t)b * gridDim.x + blockIdx.x) * R;
+    for (int i = threadIdx.x; i < R; i += blockDim.x) dst[i] = bins[i];
+  }
+}
+
+template <int D, bool ADAPTIVE, bool LDS_A, bool LDS_BINS>
+hipError_t go(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int T,
+              const float* points, const float* As, const float* grad_out, float* moments,
+              float* partials, float* grad_points, const LaunchCfg& cfg, hipStream_t s) {
+  auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, LDS_BINS>;
+  const size_t R = (size_t)geo.nC * Dim<D>::P;
+  const size_t lds = R * sizeof(float) * ((LDS_A ? 1 : 0) + (LDS_BINS ? 1 : 0));
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  const Cells g{geo.nx, geo.ny, geo.nz};
+  hipLaunchKernelGGL(kernel, dim3((unsigned)cfg.chunks, (unsigned)n_theta), dim3(cfg.block), lds,
+                     s, (int)nP, batched, T, g, geo.nC, points, As, grad_out, moments, partials,
+                     grad_points);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t dispatch(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int T,
+                    int adaptive, const float* points, const float* As, const float* grad_out,
+                    float* moments, float* partials, float* grad_points, const LaunchCfg& cfg,
+                    hipStream_t s) {
+#define CPAB_GO(AD, LA, LB)                                                                  \
+  return go<D, AD, LA, LB>(geo, nP, n_theta, batched, T, points, As, grad_out, moments,     \
+                           partials, grad_points, cfg, s)
+  const int key = (adaptive ? 4 : 0) | (cfg.lds_table ? 2 : 0) | (cfg.lds_bins ? 1 : 0);
+  switch (key) {
+    case 0: CPAB_GO(false, false, false);
+    case 1: CPAB_GO(false, false, true);
+    case 2: CPAB_GO(false, true, false);
+    case 3: CPAB_GO(false, true, true);
+    case 4: CPAB_GO(true, false, false);
+    case 5: CPAB_GO(true, false, true);
+    case 6: CPAB_GO(true, true, false);
+    default: CPAB_GO(true, true, true);
+  }
+#undef CPAB_GO
+}
+
+}  // namespace
+
+hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
+                           int adaptive, const float* points, const float* As,
+                           const float* grad_out, float* moments, float* partials,
+                           float* grad_points, const LaunchCfg& cfg, hipStream_t s) {
+  if (nP <= 0 || n_theta <= 0) return hipSuccess;
+  switch (g.ndim) {
+    case 1:
+      return dispatch<1>(g, nP, n_theta, batched, T, adaptive, points, As, grad_out, moments,
+                         partials, grad_points, cfg, s);
+    case 2:
+      return dispatch<2>(g, nP, n_theta, batched, T, adaptive, points, As, grad_out, moments,
+                         partials, grad_points, cfg, s);
+    default:
+      return dispatch<3>(g, nP, n_theta, batched, T, adaptive, points, As, grad_out, moments,
+                         partials, grad_points, cfg, s);
+  }
+}
+
+}  // namespace cpab

@@ -1,0 +1,316 @@
+// Small per-theta kernels around the integrator:
+//   affine   A = B theta          (replaces torch.sparse.mm, cpab/pytorch/transformer.py:84)
+//   expm     Trels = expm(dT A)   (cpab_ops_1d.cu:404-429, 2d.cu:537-653, 3d.cu:538-674)
+//   project  dtheta = B^T vec(M)  (replaces torch.sparse.mm, transformer.py:165-166)
+//   reduce   moments = sum of per-workgroup partial moment tables
+//   sum      grad_points.sum(0)   (transformer.py:151-152)
+// These are latency-sized (µs) next to the integrator; they exist so the
+// whole path stays on HIP with fixed, reproducible summation orders.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include "cpab_device.hpp"
+#include "cpab_launch.hpp"
+
+namespace cpab {
+
+namespace {
+
+__global__ void fill_kernel(float* __restrict__ dst, int64_t n, float value) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = value;
+}
+
+// One thread per (theta, row of B): As[b, r] = sum_k B[r, col_k] * theta[b, col_k],
+// summed in ascending column order (the order of a coalesced CSR row).
+__global__ void affine_kernel(int64_t n_theta, int rows, int d, const float* __restrict__ theta,
+                              const int32_t* __restrict__ row_ptr,
+                              const int32_t* __restrict__ col_idx,
+                              const float* __restrict__ vals, float* __restrict__ As) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n_theta * rows) return;
+  const int64_t b = i / rows;
+  const int r = (int)(i - b * rows);
+  const float* th = theta + b * d;
+  float acc = 0.0f;
+  for (int k = row_ptr[r]; k < row_ptr[r + 1]; ++k) acc = fmaf(vals[k], th[col_idx[k]], acc);
+  As[i] = acc;
+}
+
+// One thread per (theta, column j of B): grad[b, j] = sum_k B[row_k, j] * M[b, row_k],
+// in ascending row order.
+__global__ void project_kernel(int64_t n_theta, int D, int d, const float* __restrict__ M,
+                               const int32_t* __restrict__ col_ptr,
+                               const int32_t* __restrict__ row_idx,
+                               const float* __restrict__ vals, float* __restrict__ grad) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n_theta * d) return;
+  const int64_t b = i / d;
+  const int j = (int)(i - b * d);
+  const float* m = M + b * D;
+  float acc = 0.0f;
+  for (int k = col_ptr[j]; k < col_ptr[j + 1]; ++k) acc = fmaf(vals[k], m[row_idx[k]], acc);
+  grad[i] = acc;
+}
+
+// moments[b, r] = sum_w partials[b, w, r], w ascending (deterministic).
+__global__ void reduce_partials_kernel(int64_t n_theta, int nparts, int R,
+                                       const float* __restrict__ partials,
+                                       float* __restrict__ moments) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n_theta * R) return;
+  const int64_t b = i / R;
+  const int r = (int)(i - b * R);
+  const float* src = partials + b * (int64_t)nparts * R + r;
+  float acc = 0.0f;
+  for (int w = 0; w < nparts; ++w) acc += src[(int64_t)w * R];
+  moments[i] = acc;
+}
+
+// dst[i] = sum_b src[b, i], b ascending.
+__global__ void sum_batch_kernel(int64_t n_theta, int64_t n, const float* __restrict__ src,
+                                 float* __restrict__ dst) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float acc = 0.0f;
+    for (int64_t b = 0; b < n_theta; ++b) acc += src[b * n + i];
+    dst[i] = acc;
+  }
+}
+
+// ---- matrix exponentials of dT*[A; 0] (affine, last row zero) -------------
+
+__global__ void expm2_kernel(int64_t n, float dT, const float* __restrict__ As,
+                             float* __restrict__ out) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float m00 = dT * As[2 * i], m01 = dT * As[2 * i + 1];
+  float exprel;
+  if (fabsf(m00) > 1e-6f) {
+    exprel = expm1_cr(m00) / m00;
+  } else {
+    const float m2 = m00 * m00;
+    exprel = fmaf((1.0f / 24.0f) * m2, m00, fmaf(1.0f / 6.0f, m2, fmaf(0.5f, m00, 1.0f)));
+  }
+  out[2 * i] = exp_cr(m00);
+  out[2 * i + 1] = m01 * exprel;
+}
+
+__device__ __forceinline__ int n_squarings(float norm) {
+  return (norm > 0.5f) ? (int)ceilf(log2f(norm * 2.0f)) : 0;
+}
+
+// Pade(3,3) with scaling and squaring: R = Q^{-1} P, P/Q = I +- M/2 + M^2/12.
+__global__ void expm3_kernel(int64_t n, float dT, const float* __restrict__ As,
+                             float* __restrict__ out) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float* A = As + 6 * i;
+  const float a00 = dT * A[0], a01 = dT * A[1], a02 = dT * A[2];
+  const float a10 = dT * A[3], a11 = dT * A[4], a12 = dT * A[5];
+  float nsq = fmaf(a00, a00, a01 * a01);
+  nsq = fmaf(a02, a02, nsq);
+  nsq = fmaf(a10, a10, nsq);
+  nsq = fmaf(a11, a11, nsq);
+  nsq = fmaf(a12, a12, nsq);
+  const int ns = n_squarings(sqrtf(nsq));
+  float sc = 1.0f;
+  for (int k = 0; k < ns; ++k) sc *= 0.5f;
+  const float m00 = a00 * sc, m01 = a01 * sc, m02 = a02 * sc;
+  const float m10 = a10 * sc, m11 = a11 * sc, m12 = a12 * sc;
+  const float s00 = fmaf(m00, m00, m01 * m10), s01 = fmaf(m00, m01, m01 * m11);
+  const float s02 = fmaf(m00, m02, m01 * m12), s10 = fmaf(m10, m00, m11 * m10);
+  const float s11 = fmaf(m10, m01, m11 * m11), s12 = fmaf(m10, m02, m11 * m12);
+  const float c12 = 1.0f / 12.0f;
+  const float p00 = fmaf(c12, s00, fmaf(0.5f, m00, 1.0f)), p01 = fmaf(0.5f, m01, c12 * s01);
+  const float p02 = fmaf(0.5f, m02, c12 * s02), p10 = fmaf(0.5f, m10, c12 * s10);
+  const float p11 = fmaf(c12, s11, fmaf(0.5f, m11, 1.0f)), p12 = fmaf(0.5f, m12, c12 * s12);
+  const float q00 = fmaf(c12, s00, fmaf(-0.5f, m00, 1.0f)), q01 = fmaf(-0.5f, m01, c12 * s01);
+  const float q02 = fmaf(-0.5f, m02, c12 * s02), q10 = fmaf(-0.5f, m10, c12 * s10);
+  const float q11 = fmaf(c12, s11, fmaf(-0.5f, m11, 1.0f)), q12 = fmaf(-0.5f, m12, c12 * s12);
+  const float det = fmaf(q00, q11, -(q01 * q10));
+  const float id = 1.0f / det;
+  const float i00 = q11 * id, i01 = (-q01) * id, i10 = (-q10) * id, i11 = q00 * id;
+  const float i02 = -fmaf(i00, q02, i01 * q12);
+  const float i12 = -fmaf(i10, q02, i11 * q12);
+  float r00 = fmaf(i00, p00, i01 * p10), r01 = fmaf(i00, p01, i01 * p11);
+  float r02 = fmaf(i00, p02, i01 * p12) + i02;
+  float r10 = fmaf(i10, p00, i11 * p10), r11 = fmaf(i10, p01, i11 * p11);
+  float r12 = fmaf(i10, p02, i11 * p12) + i12;
+  for (int k = 0; k < ns; ++k) {
+    const float n00 = fmaf(r00, r00, r01 * r10), n01 = fmaf(r00, r01, r01 * r11);
+    const float n02 = fmaf(r00, r02, r01 * r12) + r02;
+    const float n10 = fmaf(r10, r00, r11 * r10), n11 = fmaf(r10, r01, r11 * r11);
+    const float n12 = fmaf(r10, r02, r11 * r12) + r12;
+    r00 = n00; r01 = n01; r02 = n02; r10 = n10; r11 = n11; r12 = n12;
+  }
+  float* o = out + 6 * i;
+  o[0] = r00; o[1] = r01; o[2] = r02; o[3] = r10; o[4] = r11; o[5] = r12;
+}
+
+// (x1*y1 + x2*y2) + x3*y3 with the first product of the pair fused, then the third.
+__device__ __forceinline__ float dot3(float x1, float y1, float x2, float y2, float x3, float y3) {
+  return fmaf(x3, y3, fmaf(x1, y1, x2 * y2));
+}
+// x1*y1 - x2*y2 with the left product fused.
+__device__ __forceinline__ float cross2(float x1, float y1, float x2, float y2) {
+  return fmaf(x1, y1, -(x2 * y2));
+}
+
+__global__ void expm4_kernel(int64_t n, float dT, const float* __restrict__ As,
+                             float* __restrict__ out) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float* A = As + 12 * i;
+  float a[12];
+#pragma unroll
+  for (int k = 0; k < 12; ++k) a[k] = dT * A[k];
+  float nsq = fmaf(a[0], a[0], a[1] * a[1]);
+#pragma unroll
+  for (int k = 2; k < 12; ++k) nsq = fmaf(a[k], a[k], nsq);
+  const int ns = n_squarings(sqrtf(nsq));
+  float sc = 1.0f;
+  for (int k = 0; k < ns; ++k) sc *= 0.5f;
+  float m[3][4];
+#pragma unroll
+  for (int r = 0; r < 3; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) m[r][c] = a[4 * r + c] * sc;
+  // M^2: linear block and translation column.
+  float s[3][3], t[3];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+      s[r][c] = dot3(m[r][0], m[0][c], m[r][1], m[1][c], m[r][2], m[2][c]);
+    t[r] = dot3(m[r][0], m[0][3], m[r][1], m[1][3], m[r][2], m[2][3]);
+  }
+  const float c12 = 1.0f / 12.0f;
+  float p[3][3], q[3][3], pt[3], qt[3];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      if (r == c) {
+        p[r][c] = fmaf(c12, s[r][c], fmaf(0.5f, m[r][c], 1.0f));
+        q[r][c] = fmaf(c12, s[r][c], fmaf(-0.5f, m[r][c], 1.0f));
+      } else {
+        p[r][c] = fmaf(0.5f, m[r][c], c12 * s[r][c]);
+        q[r][c] = fmaf(-0.5f, m[r][c], c12 * s[r][c]);
+      }
+    }
+    pt[r] = fmaf(0.5f, m[r][3], c12 * t[r]);
+    qt[r] = fmaf(-0.5f, m[r][3], c12 * t[r]);
+  }
+  // Adjugate / determinant of the 3x3 block of Q.
+  const float c00 = cross2(q[1][1], q[2][2], q[1][2], q[2][1]);
+  const float c10 = cross2(q[1][0], q[2][2], q[1][2], q[2][0]);
+  const float c20 = cross2(q[1][0], q[2][1], q[1][1], q[2][0]);
+  const float det = fmaf(q[0][2], c20, fmaf(q[0][0], c00, -(q[0][1] * c10)));
+  const float id = 1.0f / det;
+  float qi[3][3];
+  qi[0][0] = c00 * id;
+  qi[0][1] = cross2(q[0][2], q[2][1], q[0][1], q[2][2]) * id;
+  qi[0][2] = cross2(q[0][1], q[1][2], q[0][2], q[1][1]) * id;
+  qi[1][0] = cross2(q[1][2], q[2][0], q[1][0], q[2][2]) * id;
+  qi[1][1] = cross2(q[0][0], q[2][2], q[0][2], q[2][0]) * id;
+  qi[1][2] = cross2(q[0][2], q[1][0], q[0][0], q[1][2]) * id;
+  qi[2][0] = c20 * id;
+  qi[2][1] = cross2(q[0][1], q[2][0], q[0][0], q[2][1]) * id;
+  qi[2][2] = cross2(q[0][0], q[1][1], q[0][1], q[1][0]) * id;
+  float qit[3];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) qit[r] = -dot3(qi[r][0], qt[0], qi[r][1], qt[1], qi[r][2], qt[2]);
+  float R[3][4];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+      R[r][c] = dot3(qi[r][0], p[0][c], qi[r][1], p[1][c], qi[r][2], p[2][c]);
+    R[r][3] = dot3(qi[r][0], pt[0], qi[r][1], pt[1], qi[r][2], pt[2]) + qit[r];
+  }
+  for (int k = 0; k < ns; ++k) {
+    float N[3][4];
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+#pragma unroll
+      for (int c = 0; c < 3; ++c)
+        N[r][c] = dot3(R[r][0], R[0][c], R[r][1], R[1][c], R[r][2], R[2][c]);
+      N[r][3] = dot3(R[r][0], R[0][3], R[r][1], R[1][3], R[r][2], R[2][3]) + R[r][3];
+    }
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) R[r][c] = N[r][c];
+  }
+  float* o = out + 12 * i;
+#pragma unroll
+  for (int r = 0; r < 3; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[4 * r + c] = R[r][c];
+}
+
+inline unsigned grid_for(int64_t n, int block) {
+  int64_t g = (n + block - 1) / block;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+}  // namespace
+
+hipError_t launch_fill(float* dst, int64_t n, float value, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)g), dim3(256), 0, s, dst, n, value);
+  return hipGetLastError();
+}
+
+hipError_t launch_affine(int64_t n_theta, int rows, int d, const float* theta,
+                         const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
+                         float* As, hipStream_t s) {
+  const int64_t n = n_theta * rows;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(affine_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, n_theta, rows, d,
+                     theta, row_ptr, col_idx, vals, As);
+  return hipGetLastError();
+}
+
+hipError_t launch_expm(int ndim, int64_t n, float dT, const float* As, float* Trels,
+                       hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const dim3 g(grid_for(n, 256)), b(256);
+  if (ndim == 1) hipLaunchKernelGGL(expm2_kernel, g, b, 0, s, n, dT, As, Trels);
+  else if (ndim == 2) hipLaunchKernelGGL(expm3_kernel, g, b, 0, s, n, dT, As, Trels);
+  else hipLaunchKernelGGL(expm4_kernel, g, b, 0, s, n, dT, As, Trels);
+  return hipGetLastError();
+}
+
+hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
+                          const int32_t* col_ptr, const int32_t* row_idx, const float* vals,
+                          float* grad_theta, hipStream_t s) {
+  const int64_t n = n_theta * d;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(project_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, n_theta, D, d,
+                     moments, col_ptr, row_idx, vals, grad_theta);
+  return hipGetLastError();
+}
+
+hipError_t launch_reduce_partials(int64_t n_theta, int nparts, int R, const float* partials,
+                                  float* moments, hipStream_t s) {
+  const int64_t n = n_theta * R;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, n_theta,
+                     nparts, R, partials, moments);
+  return hipGetLastError();
+}
+
+hipError_t launch_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst,
+                            hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  hipLaunchKernelGGL(sum_batch_kernel, dim3((unsigned)g), dim3(256), 0, s, n_theta, n, src, dst);
+  return hipGetLastError();
+}
+
+}  // namespace cpab

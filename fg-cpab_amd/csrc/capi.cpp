@@ -1,0 +1,402 @@
+// extern "C" boundary of libcpab_hip.so (declared in include/cpab_hip.h).
+//
+// Responsibilities: validate every argument before touching HIP (the
+// reference's TORCH_CHECK / AT_ASSERTM set, transformer_cuda.cpp:25-52 and
+// transformer_cuda.cu:38-48,183-197, plus the size limits of this
+// implementation), pick the launch shape for the device, enqueue, and turn any
+// HIP failure into an error code + thread-local message instead of exit().
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/cpab_hip.h"
+#include "cpab_device.hpp"
+#include "cpab_launch.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return CPAB_OK;
+  return fail(CPAB_ERR_DEVICE, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+int env_int(const char* name, int dflt) {
+  const char* s = std::getenv(name);
+  return (s && *s) ? std::atoi(s) : dflt;
+}
+
+struct DeviceInfo {
+  int cus = 0;
+  int lds = 0;
+};
+
+DeviceInfo device_info() {
+  static std::mutex mu;
+  static DeviceInfo cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  DeviceInfo& d = cache[dev];
+  if (d.cus == 0) {
+    int v = 0;
+    d.cus = (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v : 256;
+    // LDS a single workgroup may allocate (dynamic shared memory budget).
+    v = 0;
+    d.lds = (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
+                ? v
+                : 64 * 1024;
+    d.lds = env_int("CPAB_LDS_BUDGET", d.lds);
+  }
+  return d;
+}
+
+int64_t div_up(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int check_geometry(int ndim, int ncx, int ncy, int ncz, cpab::Geometry* g) {
+  if (ndim < 1 || ndim > 3) return fail(CPAB_ERR_INVALID, "ndim must be 1, 2 or 3, got %d", ndim);
+  if (ncx < 1 || (ndim >= 2 && ncy < 1) || (ndim == 3 && ncz < 1))
+    return fail(CPAB_ERR_INVALID, "invalid tessellation %d x %d x %d", ncx, ncy, ncz);
+  g->ndim = ndim;
+  g->nx = ncx;
+  g->ny = ndim >= 2 ? ncy : 1;
+  g->nz = ndim == 3 ? ncz : 1;
+  const int64_t nC = ndim == 1 ? (int64_t)ncx
+                     : ndim == 2 ? 4LL * ncx * ncy
+                                 : 5LL * ncx * ncy * ncz;
+  if (nC * g->ppc() >= (1LL << 30)) return fail(CPAB_ERR_INVALID, "tessellation too large (nC=%lld)", (long long)nC);
+  g->nC = (int)nC;
+  return CPAB_OK;
+}
+
+int check_steps(int T) {
+  if (T <= 0) return fail(CPAB_ERR_INVALID, "Invalid nstepsolver=%d. Expected nstepsolver > 0.", T);
+  if (T > cpab::kMaxSteps)
+    return fail(CPAB_ERR_INVALID,
+                "Invalid nstepsolver=%d. The backward supports at most CPAB_MAX_STEPS=%d; "
+                "reduce params.nstepsolver.",
+                T, cpab::kMaxSteps);
+  return CPAB_OK;
+}
+
+int check_points(int64_t nP, int64_t n_theta, int ndim) {
+  if (nP < 0 || n_theta < 0) return fail(CPAB_ERR_INVALID, "negative size (nP=%lld, n_theta=%lld)", (long long)nP, (long long)n_theta);
+  if (nP >= (1LL << 31) / 3) return fail(CPAB_ERR_INVALID, "nP=%lld exceeds the 32-bit point index", (long long)nP);
+  if (n_theta >= 65536) return fail(CPAB_ERR_INVALID, "n_theta=%lld exceeds the grid limit 65535", (long long)n_theta);
+  (void)ndim;
+  return CPAB_OK;
+}
+
+#define CPAB_REQUIRE(ptr) \
+  do { if (!(ptr)) return fail(CPAB_ERR_INVALID, "%s must not be NULL", #ptr); } while (0)
+
+// ---- launch-shape policy ---------------------------------------------------
+
+cpab::LaunchCfg forward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta) {
+  const DeviceInfo dev = device_info();
+  const int64_t table = (int64_t)g.nC * g.ppc() * 4;
+  cpab::LaunchCfg c{};
+  c.lds_table = table <= dev.lds ? env_int("CPAB_FWD_LDS", 1) : 0;
+  int wg_per_cu = c.lds_table ? (int)std::min<int64_t>(8, std::max<int64_t>(1, dev.lds / std::max<int64_t>(table, 1))) : 4;
+  int block = 1024 / wg_per_cu;
+  block = std::max(256, std::min(1024, block / 64 * 64));
+  block = env_int("CPAB_FWD_BLOCK", block);
+  c.block = block;
+  const int64_t want = (int64_t)dev.cus * wg_per_cu * env_int("CPAB_FWD_WAVES", 1);
+  int64_t chunks = std::max<int64_t>(1, div_up(want, std::max<int64_t>(n_theta, 1)));
+  chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, block)));
+  c.chunks = (int)env_int("CPAB_FWD_CHUNKS", (int)chunks);
+  c.lds_bins = 0;
+  return c;
+}
+
+cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta) {
+  const DeviceInfo dev = device_info();
+  const int64_t table = (int64_t)g.nC * g.ppc() * 4;
+  cpab::LaunchCfg c{};
+  c.block = env_int("CPAB_BWD_BLOCK", 512);
+  c.lds_bins = (table <= dev.lds) ? env_int("CPAB_BWD_LDS_BINS", 1) : 0;
+  const int64_t used = c.lds_bins ? table : 0;
+  c.lds_table = (used + table <= dev.lds) ? env_int("CPAB_BWD_LDS_TABLE", 1) : 0;
+  const int64_t lds = table * (c.lds_bins + c.lds_table);
+  const int max_wg_threads = 2048;  // 32 waves per CU
+  int wg_per_cu = std::max(1, max_wg_threads / c.block);
+  if (lds > 0) wg_per_cu = (int)std::max<int64_t>(1, std::min<int64_t>(wg_per_cu, dev.lds / lds));
+  const int64_t want = (int64_t)dev.cus * wg_per_cu;
+  int64_t chunks = std::max<int64_t>(1, div_up(want, std::max<int64_t>(n_theta, 1)));
+  chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
+  c.chunks = env_int("CPAB_BWD_CHUNKS", (int)chunks);
+  return c;
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- optional kernel timing (HIP events recorded on the launch stream) -----
+struct Timed {
+  const char* name;
+  hipEvent_t start, stop;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<Timed> g_prof_pending;
+
+bool prof_begin(hipStream_t s, hipEvent_t* a) {
+  if (!g_prof_on) return false;
+  if (hipEventCreate(a) != hipSuccess) return false;
+  if (hipEventRecord(*a, s) != hipSuccess) {
+    (void)hipEventDestroy(*a);
+    return false;
+  }
+  return true;
+}
+void prof_end(bool on, hipEvent_t a, const char* name, hipStream_t s) {
+  if (!on) return;
+  hipEvent_t b;
+  if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return; }
+  (void)hipEventRecord(b, s);
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  g_prof_pending.push_back({name, a, b});
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cpab_last_error_string(void) { return g_last_error.c_str(); }
+
+int cpab_abi_version(void) { return 100; }
+
+int cpab_affine(int ndim, int64_t n_theta, int nC, int d, const float* theta,
+                const int32_t* row_ptr, const int32_t* col_idx, const float* vals, float* As,
+                void* stream) {
+  if (ndim < 1 || ndim > 3) return fail(CPAB_ERR_INVALID, "ndim must be 1, 2 or 3, got %d", ndim);
+  if (n_theta < 0 || nC < 0 || d < 0) return fail(CPAB_ERR_INVALID, "negative size");
+  if (n_theta == 0 || nC == 0) return CPAB_OK;
+  CPAB_REQUIRE(row_ptr); CPAB_REQUIRE(As);
+  if (d > 0) { CPAB_REQUIRE(theta); CPAB_REQUIRE(col_idx); CPAB_REQUIRE(vals); }
+  const int rows = nC * ndim * (ndim + 1);
+  return check_hip(cpab::launch_affine(n_theta, rows, d, theta, row_ptr, col_idx, vals, As,
+                                       as_stream(stream)),
+                   "cpab_affine");
+}
+
+int cpab_expm(int ndim, int64_t n_matrices, float dT, const float* As, float* Trels,
+              void* stream) {
+  if (ndim < 1 || ndim > 3) return fail(CPAB_ERR_INVALID, "As_in must have ndim=1,2,3, got %d", ndim);
+  if (n_matrices < 0) return fail(CPAB_ERR_INVALID, "negative n_matrices");
+  if (n_matrices == 0) return CPAB_OK;
+  CPAB_REQUIRE(As); CPAB_REQUIRE(Trels);
+  return check_hip(cpab::launch_expm(ndim, n_matrices, dT, As, Trels, as_stream(stream)),
+                   "cpab_expm");
+}
+
+int cpab_forward_1d_closed_form(int64_t nP, int64_t n_theta, int batched, int ncx,
+                                const float* points, const float* As, float* out, void* stream) {
+  cpab::Geometry g{};
+  int rc = check_geometry(1, ncx, 1, 1, &g);
+  if (rc) return rc;
+  if ((rc = check_points(nP, n_theta, 1))) return rc;
+  if (nP == 0 || n_theta == 0) return CPAB_OK;
+  CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(out);
+  return check_hip(cpab::launch_forward_1d(g, nP, n_theta, batched ? 1 : 0, points, As, out,
+                                           as_stream(stream)),
+                   "cpab_forward_1d_closed_form");
+}
+
+int cpab_forward(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver, int ncx,
+                 int ncy, int ncz, int adaptive, const float* points, const float* Trels,
+                 const float* As, float* out, void* stream) {
+  if (ndim == 1)
+    return cpab_forward_1d_closed_form(nP, n_theta, batched, ncx, points, As, out, stream);
+  cpab::Geometry g{};
+  int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
+  if (rc) return rc;
+  if ((rc = check_steps(nstepsolver))) return rc;
+  if ((rc = check_points(nP, n_theta, ndim))) return rc;
+  if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
+  if (nP == 0 || n_theta == 0) return CPAB_OK;
+  CPAB_REQUIRE(points); CPAB_REQUIRE(Trels); CPAB_REQUIRE(As); CPAB_REQUIRE(out);
+  const cpab::LaunchCfg cfg = forward_cfg(g, nP, n_theta);
+  hipEvent_t ev;
+  const bool timed = prof_begin(as_stream(stream), &ev);
+  rc = check_hip(cpab::launch_forward(g, nP, n_theta, batched ? 1 : 0, nstepsolver, adaptive,
+                                      points, Trels, As, out, cfg, as_stream(stream)),
+                 "cpab_forward");
+  prof_end(timed, ev, "forward", as_stream(stream));
+  return rc;
+}
+
+int cpab_trace_cells(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
+                     int ncx, int ncy, int ncz, int adaptive, const float* points,
+                     const float* Trels, const float* As, int32_t* cells, void* stream) {
+  if (ndim != 2 && ndim != 3) return fail(CPAB_ERR_INVALID, "cell tracing covers the 2D/3D fixed-step forward, got ndim=%d", ndim);
+  cpab::Geometry g{};
+  int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
+  if (rc) return rc;
+  if ((rc = check_steps(nstepsolver))) return rc;
+  if ((rc = check_points(nP, n_theta, ndim))) return rc;
+  if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
+  if (nP == 0 || n_theta == 0) return CPAB_OK;
+  CPAB_REQUIRE(points); CPAB_REQUIRE(Trels); CPAB_REQUIRE(As); CPAB_REQUIRE(cells);
+  return check_hip(cpab::launch_trace_cells(g, nP, n_theta, batched ? 1 : 0, nstepsolver, adaptive,
+                                            points, Trels, As, cells, as_stream(stream)),
+                   "cpab_trace_cells");
+}
+
+int64_t cpab_backward_workspace_size(int ndim, int64_t nP, int64_t n_theta, int nC) {
+  if (ndim < 1 || ndim > 3 || nP <= 0 || n_theta <= 0 || nC <= 0) return 0;
+  cpab::Geometry g{};
+  g.ndim = ndim;
+  g.nC = nC;
+  const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_theta);
+  if (!cfg.lds_bins) return 0;
+  return (int64_t)n_theta * cfg.chunks * nC * g.ppc() * (int64_t)sizeof(float);
+}
+
+int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver, int ncx,
+                  int ncy, int ncz, int adaptive, const float* points, const float* As,
+                  const float* grad_out, float* moments, float* grad_points, void* workspace,
+                  int64_t workspace_bytes, void* stream) {
+  cpab::Geometry g{};
+  int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
+  if (rc) return rc;
+  if ((rc = check_steps(nstepsolver))) return rc;
+  if ((rc = check_points(nP, n_theta, ndim))) return rc;
+  if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
+  if (n_theta == 0) return CPAB_OK;
+  CPAB_REQUIRE(moments);
+  hipStream_t s = as_stream(stream);
+  const int R = g.nC * g.ppc();
+  if (nP == 0) return check_hip(cpab::launch_fill(moments, n_theta * R, 0.0f, s), "cpab_backward");
+  CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(grad_out);
+  const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_theta);
+  const int64_t need = cfg.lds_bins ? (int64_t)n_theta * cfg.chunks * R * (int64_t)sizeof(float) : 0;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld", (long long)need,
+                (long long)workspace_bytes);
+  float* partials = static_cast<float*>(workspace);
+  if (!cfg.lds_bins) {
+    rc = check_hip(cpab::launch_fill(moments, n_theta * R, 0.0f, s), "cpab_backward(zero)");
+    if (rc) return rc;
+  }
+  hipEvent_t ev;
+  const bool timed = prof_begin(s, &ev);
+  rc = check_hip(cpab::launch_backward(g, nP, n_theta, batched ? 1 : 0, nstepsolver, adaptive,
+                                       points, As, grad_out, moments, partials, grad_points, cfg, s),
+                 "cpab_backward");
+  prof_end(timed, ev, "backward", s);
+  if (rc) return rc;
+  if (cfg.lds_bins)
+    rc = check_hip(cpab::launch_reduce_partials(n_theta, cfg.chunks, R, partials, moments, s),
+                   "cpab_backward(reduce)");
+  return rc;
+}
+
+int cpab_project(int64_t n_theta, int D, int d, const float* moments, const int32_t* col_ptr,
+                 const int32_t* row_idx, const float* vals, float* grad_theta, void* stream) {
+  if (n_theta < 0 || D < 0 || d < 0) return fail(CPAB_ERR_INVALID, "negative size");
+  if (n_theta == 0 || d == 0) return CPAB_OK;
+  CPAB_REQUIRE(moments); CPAB_REQUIRE(col_ptr); CPAB_REQUIRE(row_idx); CPAB_REQUIRE(vals);
+  CPAB_REQUIRE(grad_theta);
+  return check_hip(cpab::launch_project(n_theta, D, d, moments, col_ptr, row_idx, vals,
+                                        grad_theta, as_stream(stream)),
+                   "cpab_project");
+}
+
+int cpab_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, void* stream) {
+  if (n_theta < 0 || n < 0) return fail(CPAB_ERR_INVALID, "negative size");
+  if (n == 0) return CPAB_OK;
+  CPAB_REQUIRE(dst);
+  if (n_theta > 0) CPAB_REQUIRE(src);
+  return check_hip(cpab::launch_sum_batch(n_theta, n, src, dst, as_stream(stream)),
+                   "cpab_sum_batch");
+}
+
+void cpab_profile_enable(int on) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  g_prof_on = on != 0;
+}
+
+int cpab_profile_read(const char* kernel, double* total_ms, int64_t* launches) {
+  CPAB_REQUIRE(kernel); CPAB_REQUIRE(total_ms); CPAB_REQUIRE(launches);
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  double tot = 0.0;
+  int64_t n = 0;
+  std::vector<Timed> keep;
+  for (const Timed& t : g_prof_pending) {
+    if (std::strcmp(t.name, kernel) != 0) { keep.push_back(t); continue; }
+    float ms = 0.0f;
+    hipError_t e = hipEventSynchronize(t.stop);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, t.start, t.stop);
+    (void)hipEventDestroy(t.start);
+    (void)hipEventDestroy(t.stop);
+    if (e != hipSuccess) return check_hip(e, "cpab_profile_read");
+    tot += ms;
+    ++n;
+  }
+  g_prof_pending.swap(keep);
+  *total_ms = tot;
+  *launches = n;
+  return CPAB_OK;
+}
+
+static int check_interp(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                        const int64_t* out_size) {
+  if (ndim < 1 || ndim > 3) return fail(CPAB_ERR_INVALID, "interpolation supports ndim 1, 2, 3, got %d", ndim);
+  CPAB_REQUIRE(in_size); CPAB_REQUIRE(out_size);
+  if (B < 0 || C < 0) return fail(CPAB_ERR_INVALID, "negative batch or channel count");
+  int64_t n = 1;
+  for (int k = 0; k < ndim; ++k) {
+    if (in_size[k] < 1) return fail(CPAB_ERR_INVALID, "input size %d must be >= 1", k);
+    if (out_size[k] < 0) return fail(CPAB_ERR_INVALID, "output size %d must be >= 0", k);
+    if (out_size[k] >= (1LL << 31) || in_size[k] >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "size too large");
+    n *= out_size[k];
+  }
+  if (B * n * (C > 0 ? C : 1) >= (1LL << 40)) return fail(CPAB_ERR_INVALID, "problem too large");
+  if (ndim >= 2 && B * (ndim == 3 ? out_size[1] : 1) >= 65536)
+    return fail(CPAB_ERR_INVALID, "n_batch * mid size exceeds the grid limit");
+  return CPAB_OK;
+}
+
+int cpab_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                        const int64_t* out_size, const float* data, const float* grid, float* out,
+                        void* stream) {
+  int rc = check_interp(ndim, B, C, in_size, out_size);
+  if (rc) return rc;
+  CPAB_REQUIRE(data); CPAB_REQUIRE(grid); CPAB_REQUIRE(out);
+  return check_hip(cpab::launch_interp_forward(ndim, B, C, in_size, out_size, data, grid, out,
+                                               as_stream(stream)),
+                   "cpab_interp_forward");
+}
+
+int cpab_interp_backward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                         const int64_t* out_size, const float* data, const float* grid,
+                         const float* grad_out, float* grad_grid, float* grad_data,
+                         void* stream) {
+  int rc = check_interp(ndim, B, C, in_size, out_size);
+  if (rc) return rc;
+  CPAB_REQUIRE(data); CPAB_REQUIRE(grid); CPAB_REQUIRE(grad_out);
+  return check_hip(cpab::launch_interp_backward(ndim, B, C, in_size, out_size, data, grid,
+                                                grad_out, grad_grid, grad_data, as_stream(stream)),
+                   "cpab_interp_backward");
+}
+
+}  // extern "C"

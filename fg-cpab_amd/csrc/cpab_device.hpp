@@ -1,0 +1,282 @@
+// Device-side building blocks of the CPAB integrator for gfx950 (CDNA4).
+//
+// Everything here is a __forceinline__ helper used by the kernels in
+// integrate.hip / adjoint.hip.  Floating-point operation order is fixed on
+// purpose: the whole library is compiled with -ffp-contract=off, every fused
+// multiply-add is written as fmaf(), and the oracle under oracle/ performs the
+// same sequence so the two agree bit for bit.
+//
+// Where the reference (cpab/core/cpab_ops_{1d,2d,3d}.cu) writes __fmaf_rn the
+// fma is copied.  Where it writes a plain `a*b + c` nvcc contracts it by
+// default (--fmad=true); we contract those the way LLVM's FMA combiner does:
+// the left product of a sum is fused, `(a*b + c*d)` -> fmaf(a, b, c*d), and a
+// further `+ e*f` is fused around the partial sum.  Which product nvcc fuses is
+// not observable without an NVIDIA GPU, so those last bits are a documented
+// tolerance, not a parity claim.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cpab {
+
+// Same cap as CPAB_MAX_STEPS in the reference (cpab/core/cpab_ops_2d.cuh:8).
+constexpr int kMaxSteps = 100;
+// Trajectory checkpoint spacing for the backward replay.  Any value gives
+// identical results (the replay is deterministic); 8 keeps the per-segment
+// position buffer in 26 VGPRs.
+constexpr int kSeg = 8;
+constexpr int kMaxSeg = (kMaxSteps + kSeg - 1) / kSeg;
+
+// Correctly rounded float exp / log / expm1: evaluated in double and rounded
+// once.  The reference calls CUDA's expf/logf (a few ulp, implementation
+// specific); rounding the double result gives the nearest float, so device
+// and host (oracle) agree and both stay within an ulp of the exact value.
+__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+__device__ __forceinline__ float log_cr(float x) { return (float)log((double)x); }
+__device__ __forceinline__ float expm1_cr(float x) { return (float)expm1((double)x); }
+
+__device__ __forceinline__ int floor_to_int(float x) {
+  // __float2int_rd: round toward -inf, then convert.
+  return (int)__builtin_floorf(x);
+}
+
+// ---------------------------------------------------------------------------
+// Cell lookup.  Indexing and tie-breaking follow
+//   1D: cpab_ops_1d.cu:52-59   2D: cpab_ops_2d.cu:71-128   3D: cpab_ops_3d.cu:67-131
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int cell_1d(float px, int nx) {
+  const float xc = fminf(fmaxf(px, 0.0f), 1.0f - 1e-7f);
+  return min(floor_to_int(xc * (float)nx), nx - 1);
+}
+
+// Square (cx, cy) holds triangles 4*(cx + cy*nx) + {0 top, 1 right, 2 bottom, 3 left}.
+__device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
+  const float fx = (float)nx, fy = (float)ny;
+  const float xc = fminf(fmaxf(px, 0.0f), 1.0f - 1e-7f);
+  const float yc = fminf(fmaxf(py, 0.0f), 1.0f - 1e-7f);
+  const int cx = min(floor_to_int(xc * fx), nx - 1);
+  const int cy = min(floor_to_int(yc * fy), ny - 1);
+  const float lx = fmaf(xc, fx, -(float)cx);
+  const float ly = fmaf(yc, fy, -(float)cy);
+  const int base = (cx + cy * nx) * 4;
+  // Outside [0,1]^2 the point takes the boundary triangle of the nearest
+  // square; beyond a corner the diagonal through the corner decides.
+  if (px <= 0.0f || px >= 1.0f || py <= 0.0f || py >= 1.0f) {
+    if (px <= 0.0f) {
+      if (py <= 0.0f && py * fy < px * fx) return base;
+      if (py >= 1.0f && fmaf(py, fy, -fy) > (-px) * fx) return base + 2;
+      return base + 3;
+    }
+    if (px >= 1.0f) {
+      if (py <= 0.0f && (-py) * fy > fmaf(px, fx, -fx)) return base;
+      if (py >= 1.0f && fmaf(py, fy, -fy) > fmaf(px, fx, -fx)) return base + 2;
+      return base + 1;
+    }
+    return (py <= 0.0f) ? base : base + 2;
+  }
+  // Inside: the two diagonals of the square pick the triangle.
+  const int above_main = lx < ly;          // below-left of y = x
+  const int above_anti = (1.0f - lx) < ly; // beyond x + y = 1
+  return base + (above_main ? 3 - above_anti : above_anti);
+}
+
+// Cube (i, j, k) holds tetrahedra 5*(i + j*nx + k*nx*ny) + {0 central, 1..4 corners};
+// odd-parity cubes are mirrored by the local remap (x, y) -> (y, 1 - x).
+__device__ __forceinline__ int cell_3d(float px, float py, float pz, int nx, int ny, int nz) {
+  const float fx = (float)nx, fy = (float)ny, fz = (float)nz;
+  const float ox = (fabsf(px - 0.5f) - 0.5f) * fx;
+  const float oy = (fabsf(py - 0.5f) - 0.5f) * fy;
+  const float oz = (fabsf(pz - 0.5f) - 0.5f) * fz;
+  if (ox > 0.0f && oy > 0.0f && oz > 0.0f) {
+    // Beyond a corner: move the axis with the smallest overshoot half a cell inside.
+    if (ox <= oy && ox <= oz) {
+      px = (px < 0.5f) ? 0.5f / fx : 1.0f - 0.5f / fx;
+    } else if (oy <= oz) {
+      py = (py < 0.5f) ? 0.5f / fy : 1.0f - 0.5f / fy;
+    } else {
+      pz = (pz < 0.5f) ? 0.5f / fz : 1.0f - 0.5f / fz;
+    }
+  }
+  const float xc = fminf(fmaxf(px, 0.0f), 1.0f);
+  const float yc = fminf(fmaxf(py, 0.0f), 1.0f);
+  const float zc = fminf(fmaxf(pz, 0.0f), 1.0f);
+  const int i = min(floor_to_int(xc * fx), nx - 1);
+  const int j = min(floor_to_int(yc * fy), ny - 1);
+  const int k = min(floor_to_int(zc * fz), nz - 1);
+  float x = fmaf(xc, fx, -(float)i);
+  float y = fmaf(yc, fy, -(float)j);
+  const float z = fmaf(zc, fz, -(float)k);
+  int c = 5 * (i + j * nx + k * nx * ny);
+  if ((i ^ j ^ k) & 1) {
+    const float t = x;
+    x = y;
+    y = 1.0f - t;
+  }
+  if (z - (x + y) >= 0.0f) return c + 1;  // ((-x) - y) + z, rounded identically
+  if (((x + y) + z) - 2.0f >= 0.0f) return c + 2;
+  if ((y - x) - z >= 0.0f) return c + 3;  // ((-x) + y) - z
+  if ((x - y) - z >= 0.0f) return c + 4;
+  return c;
+}
+
+// ---------------------------------------------------------------------------
+// Per-cell affine maps.  A cell's row-major [ndim, ndim+1] block (velocity
+// field A or one-step map Trels) is held in registers while it is applied.
+// ---------------------------------------------------------------------------
+
+template <int D> struct Aff;
+template <> struct Aff<1> { float a, b; };
+template <> struct Aff<2> { float m[6]; };
+template <> struct Aff<3> { float m[12]; };
+
+// Loads from LDS or global memory depending on where `tab` points; the caller
+// passes an address-space-specific pointer so the right instructions are used.
+template <typename P>
+__device__ __forceinline__ Aff<1> load_aff1(P tab, int c) {
+  const float2 v = *reinterpret_cast<const float2*>(tab + 2 * c);
+  return {v.x, v.y};
+}
+template <typename P>
+__device__ __forceinline__ Aff<2> load_aff2(P tab, int c) {
+  const float2* q = reinterpret_cast<const float2*>(tab + 6 * c);
+  const float2 a = q[0], b = q[1], d = q[2];
+  return {{a.x, a.y, b.x, b.y, d.x, d.y}};
+}
+template <typename P>
+__device__ __forceinline__ Aff<3> load_aff3(P tab, int c) {
+  const float4* q = reinterpret_cast<const float4*>(tab + 12 * c);
+  const float4 a = q[0], b = q[1], d = q[2];
+  return {{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w}};
+}
+
+// v = M [p; 1] with the reference's nesting fma(m0, x, fma(m1, y, m2)).
+__device__ __forceinline__ void apply2(const Aff<2>& M, float px, float py, float& ox, float& oy) {
+  ox = fmaf(M.m[0], px, fmaf(M.m[1], py, M.m[2]));
+  oy = fmaf(M.m[3], px, fmaf(M.m[4], py, M.m[5]));
+}
+__device__ __forceinline__ void apply3(const Aff<3>& M, float px, float py, float pz,
+                                       float& ox, float& oy, float& oz) {
+  ox = fmaf(M.m[0], px, fmaf(M.m[1], py, fmaf(M.m[2], pz, M.m[3])));
+  oy = fmaf(M.m[4], px, fmaf(M.m[5], py, fmaf(M.m[6], pz, M.m[7])));
+  oz = fmaf(M.m[8], px, fmaf(M.m[9], py, fmaf(M.m[10], pz, M.m[11])));
+}
+
+// One explicit-midpoint step with cell A fixed (cpab_ops_2d.cu:269-292,
+// cpab_ops_1d.cu:249-266, cpab_ops_3d.cu:247-282).
+__device__ __forceinline__ float midpoint1(const Aff<1>& A, float px, float h, float hh) {
+  const float v = fmaf(A.a, px, A.b);
+  const float pm = fmaf(hh, v, px);
+  const float vm = fmaf(A.a, pm, A.b);
+  return fmaf(h, vm, px);
+}
+__device__ __forceinline__ void midpoint2(const Aff<2>& A, float& px, float& py, float h, float hh) {
+  float vx, vy, mx, my;
+  apply2(A, px, py, vx, vy);
+  const float pmx = fmaf(hh, vx, px), pmy = fmaf(hh, vy, py);
+  apply2(A, pmx, pmy, mx, my);
+  px = fmaf(h, mx, px);
+  py = fmaf(h, my, py);
+}
+__device__ __forceinline__ void midpoint3(const Aff<3>& A, float& px, float& py, float& pz,
+                                          float h, float hh) {
+  float vx, vy, vz, mx, my, mz;
+  apply3(A, px, py, pz, vx, vy, vz);
+  const float pmx = fmaf(hh, vx, px), pmy = fmaf(hh, vy, py), pmz = fmaf(hh, vz, pz);
+  apply3(A, pmx, pmy, pmz, mx, my, mz);
+  px = fmaf(h, mx, px);
+  py = fmaf(h, my, py);
+  pz = fmaf(h, mz, pz);
+}
+
+// ---------------------------------------------------------------------------
+// Adjoint step + cell moments for one midpoint step at position p with
+// lambda = lambda_{t+1} (cpab_ops_2d.cu:334-382, 1d:301-329, 3d:331-403):
+//   M[k][q] += h*lam_k*[pmid;1]_q + (h*h/2)*(A^T lam)_k*[p;1]_q
+//   lam     += h*A^T (lam + (h/2) A^T lam)
+// `hhh` is (h/2)*h.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ void adjoint1(const Aff<1>& A, float px, float h, float hh, float hhh,
+                                         float m[2], float& lam) {
+  const float v = fmaf(A.a, px, A.b);
+  const float pm = fmaf(hh, v, px);
+  float at = A.a * lam;
+  const float wm = h * lam;
+  const float wp = hhh * at;
+  m[0] = fmaf(wm, pm, m[0]);
+  m[1] = m[1] + wm;
+  m[0] = fmaf(wp, px, m[0]);
+  m[1] = m[1] + wp;
+  const float lmid = fmaf(hh, at, lam);
+  at = A.a * lmid;
+  lam = fmaf(h, at, lam);
+}
+
+__device__ __forceinline__ void adjoint2(const Aff<2>& A, float px, float py, float h, float hh,
+                                         float hhh, float m[6], float& lx, float& ly) {
+  const float* a = A.m;
+  float vx, vy;
+  apply2(A, px, py, vx, vy);
+  const float pmx = fmaf(hh, vx, px), pmy = fmaf(hh, vy, py);
+  float atx = fmaf(a[0], lx, a[3] * ly);
+  float aty = fmaf(a[1], lx, a[4] * ly);
+  const float wmx = h * lx, wmy = h * ly;
+  const float wpx = hhh * atx, wpy = hhh * aty;
+  m[0] = fmaf(wmx, pmx, m[0]);
+  m[1] = fmaf(wmx, pmy, m[1]);
+  m[2] = m[2] + wmx;
+  m[3] = fmaf(wmy, pmx, m[3]);
+  m[4] = fmaf(wmy, pmy, m[4]);
+  m[5] = m[5] + wmy;
+  m[0] = fmaf(wpx, px, m[0]);
+  m[1] = fmaf(wpx, py, m[1]);
+  m[2] = m[2] + wpx;
+  m[3] = fmaf(wpy, px, m[3]);
+  m[4] = fmaf(wpy, py, m[4]);
+  m[5] = m[5] + wpy;
+  const float mlx = fmaf(hh, atx, lx), mly = fmaf(hh, aty, ly);
+  atx = fmaf(a[0], mlx, a[3] * mly);
+  aty = fmaf(a[1], mlx, a[4] * mly);
+  lx = fmaf(h, atx, lx);
+  ly = fmaf(h, aty, ly);
+}
+
+__device__ __forceinline__ void adjoint3(const Aff<3>& A, float px, float py, float pz, float h,
+                                         float hh, float hhh, float m[12], float& lx, float& ly,
+                                         float& lz) {
+  const float* a = A.m;
+  float vx, vy, vz;
+  apply3(A, px, py, pz, vx, vy, vz);
+  const float pmx = fmaf(hh, vx, px), pmy = fmaf(hh, vy, py), pmz = fmaf(hh, vz, pz);
+  float atx = fmaf(a[8], lz, fmaf(a[0], lx, a[4] * ly));
+  float aty = fmaf(a[9], lz, fmaf(a[1], lx, a[5] * ly));
+  float atz = fmaf(a[10], lz, fmaf(a[2], lx, a[6] * ly));
+  const float w[3] = {h * lx, h * ly, h * lz};
+  const float u[3] = {hhh * atx, hhh * aty, hhh * atz};
+  const float pm[3] = {pmx, pmy, pmz};
+  const float p[3] = {px, py, pz};
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    m[4 * k + 0] = fmaf(w[k], pm[0], m[4 * k + 0]);
+    m[4 * k + 1] = fmaf(w[k], pm[1], m[4 * k + 1]);
+    m[4 * k + 2] = fmaf(w[k], pm[2], m[4 * k + 2]);
+    m[4 * k + 3] = m[4 * k + 3] + w[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    m[4 * k + 0] = fmaf(u[k], p[0], m[4 * k + 0]);
+    m[4 * k + 1] = fmaf(u[k], p[1], m[4 * k + 1]);
+    m[4 * k + 2] = fmaf(u[k], p[2], m[4 * k + 2]);
+    m[4 * k + 3] = m[4 * k + 3] + u[k];
+  }
+  const float mlx = fmaf(hh, atx, lx), mly = fmaf(hh, aty, ly), mlz = fmaf(hh, atz, lz);
+  atx = fmaf(a[8], mlz, fmaf(a[0], mlx, a[4] * mly));
+  aty = fmaf(a[9], mlz, fmaf(a[1], mlx, a[5] * mly));
+  atz = fmaf(a[10], mlz, fmaf(a[2], mlx, a[6] * mly));
+  lx = fmaf(h, atx, lx);
+  ly = fmaf(h, aty, ly);
+  lz = fmaf(h, atz, lz);
+}
+
+}  // namespace cpab

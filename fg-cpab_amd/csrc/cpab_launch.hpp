@@ -1,0 +1,61 @@
+// Internal (C++) launch interface between the C-ABI layer (capi.cpp) and the
+// kernel translation units.  Every launcher assumes its arguments were
+// validated by the caller and only enqueues work on `stream`.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cpab {
+
+struct Geometry {
+  int ndim;
+  int nx, ny, nz;   // cells per axis (unused axes = 1)
+  int nC;           // number of cells (nx | 4*nx*ny | 5*nx*ny*nz)
+  int ppc() const { return ndim * (ndim + 1); }
+};
+
+// Launch-shape knobs (chosen per problem by the C-ABI layer, overridable for tuning).
+struct LaunchCfg {
+  int block;        // threads per workgroup
+  int chunks;       // workgroups per theta (gridDim.x)
+  int lds_table;    // stage the per-theta cell table in LDS
+  int lds_bins;     // accumulate moments in LDS bins (else global atomics)
+};
+
+int device_cu_count();
+int device_max_lds();
+
+hipError_t launch_fill(float* dst, int64_t n, float value, hipStream_t s);
+hipError_t launch_affine(int64_t n_theta, int rows, int d, const float* theta,
+                         const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
+                         float* As, hipStream_t s);
+hipError_t launch_expm(int ndim, int64_t n, float dT, const float* As, float* Trels, hipStream_t s);
+hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
+                          const int32_t* col_ptr, const int32_t* row_idx, const float* vals,
+                          float* grad_theta, hipStream_t s);
+hipError_t launch_reduce_partials(int64_t n_theta, int nparts, int R, const float* partials,
+                                  float* moments, hipStream_t s);
+hipError_t launch_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, hipStream_t s);
+
+hipError_t launch_forward_1d(const Geometry& g, int64_t nP, int64_t n_theta, int batched,
+                             const float* points, const float* As, float* out, hipStream_t s);
+hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
+                          int adaptive, const float* points, const float* Trels, const float* As,
+                          float* out, const LaunchCfg& cfg, hipStream_t s);
+hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
+                              int adaptive, const float* points, const float* Trels,
+                              const float* As, int32_t* cells, hipStream_t s);
+hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
+                           int adaptive, const float* points, const float* As,
+                           const float* grad_out, float* moments, float* partials,
+                           float* grad_points, const LaunchCfg& cfg, hipStream_t s);
+
+hipError_t launch_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                                 const int64_t* out_size, const float* data, const float* grid,
+                                 float* out, hipStream_t s);
+hipError_t launch_interp_backward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                                  const int64_t* out_size, const float* data, const float* grid,
+                                  const float* grad_out, float* grad_grid, float* grad_data,
+                                  hipStream_t s);
+
+}  // namespace cpab

@@ -1,0 +1,340 @@
+// Forward integrators (transform_grid forward pass).
+//
+//   1D: exact closed-form flow with boundary-hit times (cpab_ops_1d.cu:103-243).
+//   2D/3D: T fixed steps p <- Trels[cell(p)] [p; 1] with Trels = expm(A/T)
+//          (cpab_ops_2d.cu:164-230, cpab_ops_3d.cu:169-241), optional Heun
+//          correction on a cell crossing (adaptive_substeps).
+//
+// MI355X layout: one workgroup integrates a contiguous chunk of points for ONE
+// theta, so that theta's whole per-cell table (nC x 6 floats in 2D) is staged
+// once into LDS and every step's table fetch is an LDS read instead of a
+// random L2 gather.  Points are SoA ([ndim, nP] rows) and each lane owns whole
+// trajectories, so global reads and writes are fully coalesced.  The integrator
+// is fp32 VALU-bound; no MFMA is involved.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include "cpab_device.hpp"
+#include "cpab_launch.hpp"
+
+namespace cpab {
+namespace {
+
+// ---------------------------------------------------------------------------
+// 1D closed form
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int sgn(float x) { return (x > 0.0f) - (x < 0.0f); }
+__device__ __forceinline__ bool near0(float x) { return fabsf(x) < 1e-7f; }
+
+// Time to leave cell c from x moving for time t, with the exit point and the
+// next cell (cpab_ops_1d.cu:133-167).
+__device__ float hit_time_1d(float x, float t, int c, float a, float b, int nx, float& xc,
+                             int& cc) {
+  const int s = sgn(t);
+  const float inf_t = INFINITY * (float)s;
+  const float v = fmaf(a, x, b);
+  if (near0(v)) return inf_t;
+  cc = c + sgn(v) * s;
+  if (cc < 0 || cc >= nx) return inf_t;
+  const float right = (float)(c + 1) / (float)nx + 1e-7f;
+  const float left = (float)c / (float)nx - 1e-7f;
+  xc = (t > 0.0f) ? ((v > 0.0f) ? right : left) : ((v > 0.0f) ? left : right);
+  const float vc = fmaf(a, xc, b);
+  if (near0(vc)) return inf_t;
+  if (sgn(v) != sgn(vc)) return inf_t;
+  if (xc <= 0.0f || xc >= 1.0f) return inf_t;
+  if (near0(a)) return (xc - x) / b;
+  return log_cr(vc / v) / a;
+}
+
+__device__ float closed_form_1d(float x, float t, const float* __restrict__ A, int nx) {
+  int c = cell_1d(x, nx);
+  const int contmax = max(c, nx - 1 - c) + 1;
+  const int s = sgn(t);
+  for (int cont = 0;;) {
+    const float a = A[2 * c], b = A[2 * c + 1];
+    float xc = x;
+    int cc = c;
+    const float thit = hit_time_1d(x, t, c, a, b, nx, xc, cc);
+    if ((float)s * thit > (float)s * t) {
+      if (near0(a)) return fmaf(t, b, x);
+      const float boa = b / a;
+      return fmaf(exp_cr(t * a), x + boa, -boa);
+    }
+    x = xc;
+    c = cc;
+    t -= thit;
+    if (++cont > contmax) break;
+  }
+  return x;
+}
+
+__global__ __launch_bounds__(256) void fwd1d_closed_kernel(int nP, int batched, int nx,
+                                                          const float* __restrict__ points,
+                                                          const float* __restrict__ As,
+                                                          float* __restrict__ out) {
+  const int b = blockIdx.y;
+  const float* A = As + (size_t)b * 2 * nx;
+  const float* pts = points + (batched ? (size_t)b * nP : 0);
+  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < nP; p += gridDim.x * blockDim.x)
+    out[(size_t)b * nP + p] = closed_form_1d(pts[p], 1.0f, A, nx);
+}
+
+// ---------------------------------------------------------------------------
+// 2D / 3D fixed-step forward
+// ---------------------------------------------------------------------------
+
+// Cooperative copy of n floats (n % 2 == 0, 8-byte aligned) global -> LDS.
+__device__ __forceinline__ void stage(float* __restrict__ dst, const float* __restrict__ src,
+                                      int n) {
+  const float2* s2 = reinterpret_cast<const float2*>(src);
+  float2* d2 = reinterpret_cast<float2*>(dst);
+  for (int i = threadIdx.x; i < n / 2; i += blockDim.x) d2[i] = s2[i];
+}
+
+// PPT independent trajectories per lane give the scheduler two dependency
+// chains (lookup -> table read -> affine apply) to interleave.
+template <bool ADAPTIVE, bool LDS, int PPT>
+__global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T, int nx, int ny,
+                                                    const float* __restrict__ points,
+                                                    const float* __restrict__ Trels,
+                                                    const float* __restrict__ As,
+                                                    float* __restrict__ out) {
+  extern __shared__ float lds[];
+  const int b = blockIdx.y;
+  const int nC = 4 * nx * ny;
+  const float* __restrict__ Tg = Trels + (size_t)b * nC * 6;
+  const float* __restrict__ Ag = As + (size_t)b * nC * 6;
+  if (LDS) {
+    stage(lds, Tg, nC * 6);
+    __syncthreads();
+  }
+  const float h = 1.0f / (float)T;
+  const float hh = 0.5f * h;
+  const float* __restrict__ pts = points + (batched ? (size_t)b * 2 * nP : 0);
+  float* __restrict__ o = out + (size_t)b * 2 * nP;
+  const int stride = gridDim.x * blockDim.x;
+  for (int p0 = blockIdx.x * blockDim.x + threadIdx.x; p0 < nP; p0 += PPT * stride) {
+    float px[PPT], py[PPT];
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int p = min(p0 + k * stride, nP - 1);
+      px[k] = pts[p];
+      py[k] = pts[p + nP];
+    }
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+      for (int k = 0; k < PPT; ++k) {
+        const int c = cell_2d(px[k], py[k], nx, ny);
+        const Aff<2> M = LDS ? load_aff2(static_cast<const float*>(lds), c) : load_aff2(Tg, c);
+        float sx, sy;
+        apply2(M, px[k], py[k], sx, sy);
+        if (ADAPTIVE) {
+          const int ce = cell_2d(sx, sy, nx, ny);
+          if (ce != c) {
+            float v0x, v0y, v1x, v1y;
+            apply2(load_aff2(Ag, c), px[k], py[k], v0x, v0y);
+            apply2(load_aff2(Ag, ce), sx, sy, v1x, v1y);
+            sx = fmaf(hh, v0x + v1x, px[k]);
+            sy = fmaf(hh, v0y + v1y, py[k]);
+          }
+        }
+        px[k] = sx;
+        py[k] = sy;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int p = p0 + k * stride;
+      if (p < nP) {
+        o[p] = px[k];
+        o[p + nP] = py[k];
+      }
+    }
+  }
+}
+
+template <bool ADAPTIVE, bool LDS>
+__global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T, int nx, int ny,
+                                                    int nz, const float* __restrict__ points,
+                                                    const float* __restrict__ Trels,
+                                                    const float* __restrict__ As,
+                                                    float* __restrict__ out) {
+  extern __shared__ float lds[];
+  const int b = blockIdx.y;
+  const int nC = 5 * nx * ny * nz;
+  const float* __restrict__ Tg = Trels + (size_t)b * nC * 12;
+  const float* __restrict__ Ag = As + (size_t)b * nC * 12;
+  if (LDS) {
+    stage(lds, Tg, nC * 12);
+    __syncthreads();
+  }
+  const float h = 1.0f / (float)T;
+  const float hh = 0.5f * h;
+  const float* __restrict__ pts = points + (batched ? (size_t)b * 3 * nP : 0);
+  float* __restrict__ o = out + (size_t)b * 3 * nP;
+  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < nP; p += gridDim.x * blockDim.x) {
+    float px = pts[p], py = pts[p + nP], pz = pts[p + 2 * (size_t)nP];
+    for (int t = 0; t < T; ++t) {
+      const int c = cell_3d(px, py, pz, nx, ny, nz);
+      const Aff<3> M = LDS ? load_aff3(static_cast<const float*>(lds), c) : load_aff3(Tg, c);
+      float sx, sy, sz;
+      apply3(M, px, py, pz, sx, sy, sz);
+      if (ADAPTIVE) {
+        const int ce = cell_3d(sx, sy, sz, nx, ny, nz);
+        if (ce != c) {
+          float v0x, v0y, v0z, v1x, v1y, v1z;
+          apply3(load_aff3(Ag, c), px, py, pz, v0x, v0y, v0z);
+          apply3(load_aff3(Ag, ce), sx, sy, sz, v1x, v1y, v1z);
+          sx = fmaf(hh, v0x + v1x, px);
+          sy = fmaf(hh, v0y + v1y, py);
+          sz = fmaf(hh, v0z + v1z, pz);
+        }
+      }
+      px = sx;
+      py = sy;
+      pz = sz;
+    }
+    o[p] = px;
+    o[p + nP] = py;
+    o[p + 2 * (size_t)nP] = pz;
+  }
+}
+
+
+// Cell index visited at every step of the fixed-step forward, for parity tests
+// of the visited-cell sequence (same stepping as fwd2d/fwd3d, table read from
+// global memory).  cells: [n_theta, nP, T] int32.
+__global__ __launch_bounds__(256) void trace_cells_kernel(int ndim, int nP, int batched, int T,
+                                                          int nx, int ny, int nz,
+                                                          const float* __restrict__ points,
+                                                          const float* __restrict__ Trels,
+                                                          const float* __restrict__ As,
+                                                          int adaptive, int32_t* __restrict__ cells) {
+  const int b = blockIdx.y;
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= nP) return;
+  const int P = ndim * (ndim + 1);
+  const int nC = ndim == 2 ? 4 * nx * ny : 5 * nx * ny * nz;
+  const float* Tg = Trels + (size_t)b * nC * P;
+  const float* Ag = As + (size_t)b * nC * P;
+  const float* pts = points + (batched ? (size_t)b * ndim * nP : 0);
+  const float h = 1.0f / (float)T, hh = 0.5f * h;
+  int32_t* cl = cells + ((size_t)b * nP + p) * T;
+  if (ndim == 2) {
+    float px = pts[p], py = pts[p + nP];
+    for (int t = 0; t < T; ++t) {
+      const int c = cell_2d(px, py, nx, ny);
+      cl[t] = c;
+      float sx, sy;
+      apply2(load_aff2(Tg, c), px, py, sx, sy);
+      if (adaptive) {
+        const int ce = cell_2d(sx, sy, nx, ny);
+        if (ce != c) {
+          float v0x, v0y, v1x, v1y;
+          apply2(load_aff2(Ag, c), px, py, v0x, v0y);
+          apply2(load_aff2(Ag, ce), sx, sy, v1x, v1y);
+          sx = fmaf(hh, v0x + v1x, px);
+          sy = fmaf(hh, v0y + v1y, py);
+        }
+      }
+      px = sx;
+      py = sy;
+    }
+  } else {
+    float px = pts[p], py = pts[p + nP], pz = pts[p + 2 * (size_t)nP];
+    for (int t = 0; t < T; ++t) {
+      const int c = cell_3d(px, py, pz, nx, ny, nz);
+      cl[t] = c;
+      float sx, sy, sz;
+      apply3(load_aff3(Tg, c), px, py, pz, sx, sy, sz);
+      if (adaptive) {
+        const int ce = cell_3d(sx, sy, sz, nx, ny, nz);
+        if (ce != c) {
+          float v0x, v0y, v0z, v1x, v1y, v1z;
+          apply3(load_aff3(Ag, c), px, py, pz, v0x, v0y, v0z);
+          apply3(load_aff3(Ag, ce), sx, sy, sz, v1x, v1y, v1z);
+          sx = fmaf(hh, v0x + v1x, px);
+          sy = fmaf(hh, v0y + v1y, py);
+          sz = fmaf(hh, v0z + v1z, pz);
+        }
+      }
+      px = sx;
+      py = sy;
+      pz = sz;
+    }
+  }
+}
+
+template <typename K>
+hipError_t launch_with_lds(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                           int nP, int batched, int T, int nx, int ny, const float* points,
+                           const float* Trels, const float* As, float* out) {
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kernel, grid, block, lds, s, nP, batched, T, nx, ny, points, Trels, As, out);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_forward_1d(const Geometry& g, int64_t nP, int64_t n_theta, int batched,
+                             const float* points, const float* As, float* out, hipStream_t s) {
+  if (nP <= 0 || n_theta <= 0) return hipSuccess;
+  int64_t gx = (nP + 255) / 256;
+  if (gx > 4096) gx = 4096;
+  hipLaunchKernelGGL(fwd1d_closed_kernel, dim3((unsigned)gx, (unsigned)n_theta), dim3(256), 0, s,
+                     (int)nP, batched, g.nx, points, As, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
+                          int adaptive, const float* points, const float* Trels, const float* As,
+                          float* out, const LaunchCfg& cfg, hipStream_t s) {
+  if (nP <= 0 || n_theta <= 0) return hipSuccess;
+  const dim3 grid((unsigned)cfg.chunks, (unsigned)n_theta), block((unsigned)cfg.block);
+  const size_t tab = (size_t)g.nC * g.ppc() * sizeof(float);
+  const size_t lds = cfg.lds_table ? tab : 0;
+  if (g.ndim == 2) {
+    if (adaptive) {
+      return cfg.lds_table
+                 ? launch_with_lds(fwd2d_kernel<true, true, 1>, grid, block, lds, s, (int)nP,
+                                   batched, T, g.nx, g.ny, points, Trels, As, out)
+                 : launch_with_lds(fwd2d_kernel<true, false, 1>, grid, block, lds, s, (int)nP,
+                                   batched, T, g.nx, g.ny, points, Trels, As, out);
+    }
+    return cfg.lds_table
+               ? launch_with_lds(fwd2d_kernel<false, true, 2>, grid, block, lds, s, (int)nP,
+                                 batched, T, g.nx, g.ny, points, Trels, As, out)
+               : launch_with_lds(fwd2d_kernel<false, false, 2>, grid, block, lds, s, (int)nP,
+                                 batched, T, g.nx, g.ny, points, Trels, As, out);
+  }
+  // 3D: the kernel takes nz as an extra argument.
+  auto go = [&](auto kernel) -> hipError_t {
+    if (lds > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, (int)nP, batched, T, g.nx, g.ny, g.nz,
+                       points, Trels, As, out);
+    return hipGetLastError();
+  };
+  if (adaptive) return cfg.lds_table ? go(fwd3d_kernel<true, true>) : go(fwd3d_kernel<true, false>);
+  return cfg.lds_table ? go(fwd3d_kernel<false, true>) : go(fwd3d_kernel<false, false>);
+}
+
+hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
+                              int adaptive, const float* points, const float* Trels,
+                              const float* As, int32_t* cells, hipStream_t s) {
+  if (nP <= 0 || n_theta <= 0) return hipSuccess;
+  hipLaunchKernelGGL(trace_cells_kernel, dim3((unsigned)((nP + 255) / 256), (unsigned)n_theta),
+                     dim3(256), 0, s, g.ndim, (int)nP, batched, T, g.nx, g.ny, g.nz, points, Trels,
+                     As, adaptive, cells);
+  return hipGetLastError();
+}
+
+}  // namespace cpab

@@ -1,0 +1,357 @@
+// transform_data gather: border-clamped linear / bilinear / trilinear sampling
+// and its backward (cpab/pytorch/interpolation.py:3-159 plus the torch
+// autograd backward of those ops).
+//
+// Index conventions of the reference: grid coordinate k scales by
+// (data.shape[2+k] - 1) and indexes data axis 2+k; the warped grid lists points
+// with coordinate 0 fastest, p = i0 + o0*(i1 + o1*i2); the output is
+// [B, C, o0, o1(, o2)] with the LAST axis fastest.  So the point order and the
+// output order are transposes of each other.  HBM-bound, so each workgroup
+// takes a 64 x 64 tile over (i0, i_last) at fixed i_mid, reads the grid rows
+// coalesced along i0 into LDS, and computes/writes with i_last across the
+// lanes (coalesced output and, for smooth warps, near-contiguous data rows).
+// The backward does the same transpose in the other direction for grad_grid.
+//
+// Arithmetic follows the reference's eager torch ops one by one (no fused
+// multiply-add): x = g*(W-1); x0 = clamp(floor(x)); xd = x - x0;
+// lerp(a, b, t) = a*(1-t) + b*t with the axes reduced x, then y, then z.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include "cpab_launch.hpp"
+
+namespace cpab {
+namespace {
+
+constexpr int kTile = 64;
+constexpr int kThreads = 256;
+
+struct Axis {
+  int i0, i1;   // clamped corner indices
+  float t;      // fractional weight of i1
+};
+
+__device__ __forceinline__ Axis axis_of(float g, int size) {
+  const float x = g * (float)(size - 1);
+  const float f = floorf(x);
+  const float hi = (float)(size - 1);
+  // floor -> clamp to [0, size-1] (integer semantics of the reference; done in
+  // float first so out-of-range values cannot overflow the conversion).
+  const int a = (int)fminf(fmaxf(f, 0.0f), hi);
+  const int b = (int)fminf(fmaxf(f + 1.0f, 0.0f), hi);
+  return {a, b, x - (float)a};
+}
+
+__device__ __forceinline__ float lerp_ref(float a, float b, float t) {
+  const float u = 1.0f - t;
+  return __fadd_rn(__fmul_rn(a, u), __fmul_rn(b, t));
+}
+
+struct Shape {
+  int ndim;
+  int B, C;
+  int in[3];     // data spatial sizes
+  int o0, omid, olast;
+  int64_t nP;
+};
+
+__device__ __forceinline__ int64_t data_index(const Shape& s, int64_t bc, int x, int y, int z) {
+  if (s.ndim == 2) return (bc * s.in[0] + x) * (int64_t)s.in[1] + y;
+  return ((bc * s.in[0] + x) * (int64_t)s.in[1] + y) * (int64_t)s.in[2] + z;
+}
+
+// Sample data[b, ch] at the three axis weights (z unused in 2D).
+__device__ __forceinline__ float sample(const Shape& s, const float* __restrict__ data, int64_t bc,
+                                        const Axis& ax, const Axis& ay, const Axis& az) {
+  if (s.ndim == 2) {
+    const float c00 = data[data_index(s, bc, ax.i0, ay.i0, 0)];
+    const float c01 = data[data_index(s, bc, ax.i0, ay.i1, 0)];
+    const float c10 = data[data_index(s, bc, ax.i1, ay.i0, 0)];
+    const float c11 = data[data_index(s, bc, ax.i1, ay.i1, 0)];
+    const float c0 = lerp_ref(c00, c10, ax.t);
+    const float c1 = lerp_ref(c01, c11, ax.t);
+    return lerp_ref(c0, c1, ay.t);
+  }
+  float c[2][2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int d = 0; d < 2; ++d)
+        c[a][b][d] = data[data_index(s, bc, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0,
+                                     d ? az.i1 : az.i0)];
+  const float c00 = lerp_ref(c[0][0][0], c[1][0][0], ax.t);
+  const float c01 = lerp_ref(c[0][0][1], c[1][0][1], ax.t);
+  const float c10 = lerp_ref(c[0][1][0], c[1][1][0], ax.t);
+  const float c11 = lerp_ref(c[0][1][1], c[1][1][1], ax.t);
+  const float c0 = lerp_ref(c00, c10, ay.t);
+  const float c1 = lerp_ref(c01, c11, ay.t);
+  return lerp_ref(c0, c1, az.t);
+}
+
+// d out / d (x, y, z) for one channel with upstream gradient g, before the
+// (size-1) chain factor; and the 4 / 8 corner weights for grad_data.
+__device__ __forceinline__ void sample_grad(const Shape& s, const float* __restrict__ data,
+                                            int64_t bc, const Axis& ax, const Axis& ay,
+                                            const Axis& az, float g, float* dxyz,
+                                            float* __restrict__ grad_data) {
+  const float ux = 1.0f - ax.t, uy = 1.0f - ay.t, uz = 1.0f - az.t;
+  if (s.ndim == 2) {
+    const int64_t i00 = data_index(s, bc, ax.i0, ay.i0, 0), i01 = data_index(s, bc, ax.i0, ay.i1, 0);
+    const int64_t i10 = data_index(s, bc, ax.i1, ay.i0, 0), i11 = data_index(s, bc, ax.i1, ay.i1, 0);
+    if (dxyz) {
+      const float c00 = data[i00], c01 = data[i01], c10 = data[i10], c11 = data[i11];
+      const float c0 = lerp_ref(c00, c10, ax.t), c1 = lerp_ref(c01, c11, ax.t);
+      dxyz[0] += g * uy * (c10 - c00) + g * ay.t * (c11 - c01);
+      dxyz[1] += g * (c1 - c0);
+    }
+    if (grad_data) {
+      const float g0 = g * uy, g1 = g * ay.t;
+      unsafeAtomicAdd(grad_data + i00, g0 * ux);
+      unsafeAtomicAdd(grad_data + i10, g0 * ax.t);
+      unsafeAtomicAdd(grad_data + i01, g1 * ux);
+      unsafeAtomicAdd(grad_data + i11, g1 * ax.t);
+    }
+    return;
+  }
+  int64_t idx[2][2][2];
+  float c[2][2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        idx[a][b][d] = data_index(s, bc, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, d ? az.i1 : az.i0);
+        c[a][b][d] = dxyz ? data[idx[a][b][d]] : 0.0f;
+      }
+  if (dxyz) {
+    // Along x: the four (y, z) lines; along y: the two z planes; along z: the two halves.
+    const float wyz[2][2] = {{uy * uz, uy * az.t}, {ay.t * uz, ay.t * az.t}};
+    float gx = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int d = 0; d < 2; ++d) gx += wyz[b][d] * (c[1][b][d] - c[0][b][d]);
+    const float c00 = lerp_ref(c[0][0][0], c[1][0][0], ax.t);
+    const float c01 = lerp_ref(c[0][0][1], c[1][0][1], ax.t);
+    const float c10 = lerp_ref(c[0][1][0], c[1][1][0], ax.t);
+    const float c11 = lerp_ref(c[0][1][1], c[1][1][1], ax.t);
+    const float gy = uz * (c10 - c00) + az.t * (c11 - c01);
+    const float gz = lerp_ref(c01, c11, ay.t) - lerp_ref(c00, c10, ay.t);
+    dxyz[0] += g * gx;
+    dxyz[1] += g * gy;
+    dxyz[2] += g * gz;
+  }
+  if (grad_data) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const float w = (a ? ax.t : ux) * (b ? ay.t : uy) * (d ? az.t : uz);
+          unsafeAtomicAdd(grad_data + idx[a][b][d], g * w);
+        }
+  }
+}
+
+// Tile coordinates: blockIdx.x -> i0 tile, blockIdx.y -> i_last tile,
+// blockIdx.z -> b * omid + i_mid.
+__device__ __forceinline__ void tile_origin(const Shape& s, int& b, int& im, int& t0, int& tl) {
+  b = blockIdx.z / s.omid;
+  im = blockIdx.z - b * s.omid;
+  t0 = blockIdx.x * kTile;
+  tl = blockIdx.y * kTile;
+}
+
+__device__ __forceinline__ int64_t point_of(const Shape& s, int i0, int im, int il) {
+  return i0 + (int64_t)s.o0 * (im + (int64_t)s.omid * il);
+}
+
+__global__ __launch_bounds__(kThreads) void interp_fwd_kernel(Shape s,
+                                                              const float* __restrict__ data,
+                                                              const float* __restrict__ grid,
+                                                              float* __restrict__ out) {
+  __shared__ float crd[3][kTile][kTile + 1];  // [axis][i_last][i0]
+  int b, im, t0, tl;
+  tile_origin(s, b, im, t0, tl);
+  const int n0 = min(kTile, s.o0 - t0), nl = min(kTile, s.olast - tl);
+  // Load: lanes along i0 (contiguous in the grid rows).
+  for (int e = threadIdx.x; e < kTile * kTile; e += kThreads) {
+    const int a0 = e % kTile, al = e / kTile;
+    if (a0 < n0 && al < nl) {
+      const int64_t p = point_of(s, t0 + a0, im, tl + al);
+      for (int k = 0; k < s.ndim; ++k) crd[k][al][a0] = grid[((int64_t)b * s.ndim + k) * s.nP + p];
+    }
+  }
+  __syncthreads();
+  // Compute: lanes along i_last (contiguous in the output rows).
+  for (int e = threadIdx.x; e < kTile * kTile; e += kThreads) {
+    const int al = e % kTile, a0 = e / kTile;
+    if (a0 >= n0 || al >= nl) continue;
+    const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
+    const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
+    const Axis az = (s.ndim == 3) ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
+    const int64_t o = ((int64_t)(t0 + a0) * s.omid + im) * s.olast + tl + al;
+    const int64_t plane = (int64_t)s.o0 * s.omid * s.olast;
+    for (int ch = 0; ch < s.C; ++ch) {
+      const int64_t bc = (int64_t)b * s.C + ch;
+      out[bc * plane + o] = sample(s, data, bc, ax, ay, az);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void interp_bwd_kernel(Shape s,
+                                                              const float* __restrict__ data,
+                                                              const float* __restrict__ grid,
+                                                              const float* __restrict__ grad_out,
+                                                              float* __restrict__ grad_grid,
+                                                              float* __restrict__ grad_data) {
+  __shared__ float crd[3][kTile][kTile + 1];
+  int b, im, t0, tl;
+  tile_origin(s, b, im, t0, tl);
+  const int n0 = min(kTile, s.o0 - t0), nl = min(kTile, s.olast - tl);
+  for (int e = threadIdx.x; e < kTile * kTile; e += kThreads) {
+    const int a0 = e % kTile, al = e / kTile;
+    if (a0 < n0 && al < nl) {
+      const int64_t p = point_of(s, t0 + a0, im, tl + al);
+      for (int k = 0; k < s.ndim; ++k) crd[k][al][a0] = grid[((int64_t)b * s.ndim + k) * s.nP + p];
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < kTile * kTile; e += kThreads) {
+    const int al = e % kTile, a0 = e / kTile;
+    if (a0 >= n0 || al >= nl) continue;
+    const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
+    const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
+    const Axis az = (s.ndim == 3) ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
+    const int64_t o = ((int64_t)(t0 + a0) * s.omid + im) * s.olast + tl + al;
+    const int64_t plane = (int64_t)s.o0 * s.omid * s.olast;
+    float d[3] = {0.0f, 0.0f, 0.0f};
+    for (int ch = 0; ch < s.C; ++ch) {
+      const int64_t bc = (int64_t)b * s.C + ch;
+      sample_grad(s, data, bc, ax, ay, az, grad_out[bc * plane + o], grad_grid ? d : nullptr,
+                  grad_data);
+    }
+    if (grad_grid) {
+      // Chain factor of x = g*(size-1); the result goes back through LDS
+      // (same slot: each thread reads and writes only its own element).
+      for (int k = 0; k < s.ndim; ++k) crd[k][al][a0] = d[k] * (float)(s.in[k] - 1);
+    }
+  }
+  if (!grad_grid) return;
+  __syncthreads();
+  for (int e = threadIdx.x; e < kTile * kTile; e += kThreads) {
+    const int a0 = e % kTile, al = e / kTile;
+    if (a0 < n0 && al < nl) {
+      const int64_t p = point_of(s, t0 + a0, im, tl + al);
+      for (int k = 0; k < s.ndim; ++k)
+        grad_grid[((int64_t)b * s.ndim + k) * s.nP + p] = crd[k][al][a0];
+    }
+  }
+}
+
+// 1D: point order equals output order, one thread per (b, point).
+__global__ __launch_bounds__(kThreads) void interp1d_fwd_kernel(int B, int C, int W, int64_t nP,
+                                                                const float* __restrict__ data,
+                                                                const float* __restrict__ grid,
+                                                                float* __restrict__ out) {
+  for (int64_t e = blockIdx.x * (int64_t)kThreads + threadIdx.x; e < (int64_t)B * nP;
+       e += (int64_t)gridDim.x * kThreads) {
+    const int64_t b = e / nP, p = e - b * nP;
+    const Axis ax = axis_of(grid[e], W);
+    for (int ch = 0; ch < C; ++ch) {
+      const float* d = data + (b * C + ch) * W;
+      out[(b * C + ch) * nP + p] = lerp_ref(d[ax.i0], d[ax.i1], ax.t);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void interp1d_bwd_kernel(int B, int C, int W, int64_t nP,
+                                                                const float* __restrict__ data,
+                                                                const float* __restrict__ grid,
+                                                                const float* __restrict__ grad_out,
+                                                                float* __restrict__ grad_grid,
+                                                                float* __restrict__ grad_data) {
+  for (int64_t e = blockIdx.x * (int64_t)kThreads + threadIdx.x; e < (int64_t)B * nP;
+       e += (int64_t)gridDim.x * kThreads) {
+    const int64_t b = e / nP, p = e - b * nP;
+    const Axis ax = axis_of(grid[e], W);
+    float gx = 0.0f;
+    for (int ch = 0; ch < C; ++ch) {
+      const int64_t bc = b * C + ch;
+      const float g = grad_out[bc * nP + p];
+      const float* d = data + bc * W;
+      gx += g * (d[ax.i1] - d[ax.i0]);
+      if (grad_data) {
+        unsafeAtomicAdd(grad_data + bc * W + ax.i0, g * (1.0f - ax.t));
+        unsafeAtomicAdd(grad_data + bc * W + ax.i1, g * ax.t);
+      }
+    }
+    if (grad_grid) grad_grid[e] = gx * (float)(W - 1);
+  }
+}
+
+Shape make_shape(int ndim, int64_t B, int64_t C, const int64_t* in_size, const int64_t* out_size) {
+  Shape s{};
+  s.ndim = ndim;
+  s.B = (int)B;
+  s.C = (int)C;
+  for (int k = 0; k < 3; ++k) s.in[k] = k < ndim ? (int)in_size[k] : 1;
+  s.o0 = (int)out_size[0];
+  s.omid = ndim == 3 ? (int)out_size[1] : 1;
+  s.olast = (int)out_size[ndim - 1];
+  s.nP = 1;
+  for (int k = 0; k < ndim; ++k) s.nP *= out_size[k];
+  return s;
+}
+
+dim3 tile_grid(const Shape& s) {
+  return dim3((unsigned)((s.o0 + kTile - 1) / kTile), (unsigned)((s.olast + kTile - 1) / kTile),
+              (unsigned)(s.B * s.omid));
+}
+
+}  // namespace
+
+hipError_t launch_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                                 const int64_t* out_size, const float* data, const float* grid,
+                                 float* out, hipStream_t st) {
+  const Shape s = make_shape(ndim, B, C, in_size, out_size);
+  if (s.nP <= 0 || B <= 0) return hipSuccess;
+  if (ndim == 1) {
+    int64_t g = (B * s.nP + kThreads - 1) / kThreads;
+    if (g > 65536) g = 65536;
+    hipLaunchKernelGGL(interp1d_fwd_kernel, dim3((unsigned)g), dim3(kThreads), 0, st, s.B, s.C,
+                       s.in[0], s.nP, data, grid, out);
+  } else {
+    hipLaunchKernelGGL(interp_fwd_kernel, tile_grid(s), dim3(kThreads), 0, st, s, data, grid, out);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_interp_backward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                                  const int64_t* out_size, const float* data, const float* grid,
+                                  const float* grad_out, float* grad_grid, float* grad_data,
+                                  hipStream_t st) {
+  const Shape s = make_shape(ndim, B, C, in_size, out_size);
+  if (grad_data) {
+    int64_t n = B * C;
+    for (int k = 0; k < ndim; ++k) n *= in_size[k];
+    hipError_t e = launch_fill(grad_data, n, 0.0f, st);
+    if (e != hipSuccess) return e;
+  }
+  if (s.nP <= 0 || B <= 0) return hipSuccess;
+  if (ndim == 1) {
+    int64_t g = (B * s.nP + kThreads - 1) / kThreads;
+    if (g > 65536) g = 65536;
+    hipLaunchKernelGGL(interp1d_bwd_kernel, dim3((unsigned)g), dim3(kThreads), 0, st, s.B, s.C,
+                       s.in[0], s.nP, data, grid, grad_out, grad_grid, grad_data);
+  } else {
+    hipLaunchKernelGGL(interp_bwd_kernel, tile_grid(s), dim3(kThreads), 0, st, s, data, grid,
+                       grad_out, grad_grid, grad_data);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace cpab

@@ -1,0 +1,133 @@
+/*
+ * cpab_hip.h -- C ABI of the MI355X CPAB transform library (libcpab_hip.so).
+ *
+ * Drop-in replacement for the reference's pybind11 module `cpab_gpu`
+ * (cpab/pytorch/transformer_cuda.cpp:172-179) and for the two torch.sparse.mm
+ * calls and the torch interpolation ops around it.  Conventions:
+ *
+ *   - every pointer is a device pointer to contiguous float32 (or int32 index)
+ *     memory owned by the caller; nothing is allocated by the library;
+ *   - `stream` is a hipStream_t (pass 0 for the null stream); all work is
+ *     enqueued asynchronously on it;
+ *   - the return value is CPAB_OK or an error code; argument checking happens
+ *     before any HIP call, and cpab_last_error_string() gives the message of
+ *     the calling thread's last failure (the reference raised RuntimeError via
+ *     TORCH_CHECK, or exit()ed on a launch error, transformer_cuda.cu:12-18);
+ *   - `batched` = 1 when points are [n_theta, ndim, nP], 0 when one [ndim, nP]
+ *     set is shared by all thetas (the reference's `broadcast` flag,
+ *     transformer_cuda.cpp:43).
+ *
+ * Layouts: theta [n_theta, d]; As/Trels [n_theta, nC, ndim, ndim+1] row-major;
+ * moments [n_theta, nC, ndim*(ndim+1)]; points/outputs SoA rows [.., ndim, nP].
+ */
+#ifndef CPAB_HIP_H
+#define CPAB_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CPAB_OK 0
+#define CPAB_ERR_INVALID 1 /* bad argument: nothing was enqueued */
+#define CPAB_ERR_DEVICE 2  /* HIP runtime / launch failure */
+
+#define CPAB_MAX_STEPS 100 /* same cap as cpab/core/cpab_ops_2d.cuh:8 */
+
+/* Message for the calling thread's last failed call ("" if none). */
+const char* cpab_last_error_string(void);
+
+/* ABI version (major*100 + minor). */
+int cpab_abi_version(void);
+
+/* A = B theta per theta: As[b, r] = sum_k vals[k] * theta[b, col_idx[k]] over
+ * the CSR row r of B (rows = nC*ndim*(ndim+1)).
+ * Replaces torch.sparse.mm(B, theta^T) in cpab/pytorch/transformer.py:84. */
+int cpab_affine(int ndim, int64_t n_theta, int nC, int d, const float* theta,
+                const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
+                float* As, void* stream);
+
+/* Trels = expm(dT * [A; 0]) for n_matrices affine blocks of shape [ndim, ndim+1].
+ * Replaces cpab_gpu.expm, transformer_cuda.cpp:159-170. */
+int cpab_expm(int ndim, int64_t n_matrices, float dT, const float* As, float* Trels,
+              void* stream);
+
+/* Forward integration: out[b] = phi(points[b or shared]; theta_b), [n_theta, ndim, nP].
+ * ndim 2/3: nstepsolver steps of Trels (+ Heun on crossings if adaptive);
+ * ndim 1: the closed form (Trels unused), as the reference does.
+ * Replaces cpab_gpu.forward, transformer_cuda.cpp:32-61. */
+int cpab_forward(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
+                 int ncx, int ncy, int ncz, int adaptive, const float* points,
+                 const float* Trels, const float* As, float* out, void* stream);
+
+/* 1D closed-form forward.  Replaces cpab_gpu.forward_1d_closed_form,
+ * transformer_cuda.cpp:66-85. */
+int cpab_forward_1d_closed_form(int64_t nP, int64_t n_theta, int batched, int ncx,
+                                const float* points, const float* As, float* out,
+                                void* stream);
+
+/* Debug / parity aid: the cell index visited at each of the nstepsolver steps
+ * of cpab_forward (ndim 2/3) into cells [n_theta, nP, nstepsolver] int32.  No
+ * reference counterpart (the reference exposes no trajectory); it makes the
+ * visited-cell sequence of the fixed-step forward observable for tests. */
+int cpab_trace_cells(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
+                     int ncx, int ncy, int ncz, int adaptive, const float* points,
+                     const float* Trels, const float* As, int32_t* cells, void* stream);
+
+/* Bytes of device workspace cpab_backward needs for this problem (may be 0). */
+int64_t cpab_backward_workspace_size(int ndim, int64_t nP, int64_t n_theta, int nC);
+
+/* Fused backward: cell moments [n_theta, nC, ndim*(ndim+1)] (overwritten, no
+ * need to zero them) and, if grad_points != NULL, the point adjoints
+ * [n_theta, ndim, nP].  `workspace` must hold
+ * cpab_backward_workspace_size(...) bytes (NULL if that is 0).
+ * Replaces cpab_gpu.backward_moments (transformer_cuda.cpp:92-116) and
+ * cpab_gpu.backward_moments_and_points (transformer_cuda.cpp:122-153). */
+int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
+                  int ncx, int ncy, int ncz, int adaptive, const float* points,
+                  const float* As, const float* grad_out, float* moments,
+                  float* grad_points, void* workspace, int64_t workspace_bytes,
+                  void* stream);
+
+/* grad_theta[b, j] = sum_k vals[k] * moments[b, row_idx[k]] over the CSC column
+ * j of B (D = rows of B).  Replaces torch.sparse.mm(B^T, M^T) in
+ * cpab/pytorch/transformer.py:165-166. */
+int cpab_project(int64_t n_theta, int D, int d, const float* moments,
+                 const int32_t* col_ptr, const int32_t* row_idx, const float* vals,
+                 float* grad_theta, void* stream);
+
+/* dst[i] = sum_b src[b, i] (b ascending).  Replaces grad_points.sum(0) for
+ * shared points, cpab/pytorch/transformer.py:151-152. */
+int cpab_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, void* stream);
+
+/* Border-clamped linear/bilinear/trilinear resampling of data
+ * [n_batch, C, *in_size] at grid [n_batch, ndim, prod(out_size)] (coordinate 0
+ * fastest) into out [n_batch, C, *out_size].
+ * Replaces cpab/pytorch/interpolation.py:3-159 (forward). */
+int cpab_interp_forward(int ndim, int64_t n_batch, int64_t n_channels, const int64_t* in_size,
+                        const int64_t* out_size, const float* data, const float* grid,
+                        float* out, void* stream);
+
+/* Backward of cpab_interp_forward: grad_grid [n_batch, ndim, nP] (may be NULL)
+ * and grad_data [n_batch, C, *in_size] (may be NULL; overwritten).
+ * Replaces the torch autograd backward of interpolation.py:3-159. */
+int cpab_interp_backward(int ndim, int64_t n_batch, int64_t n_channels, const int64_t* in_size,
+                         const int64_t* out_size, const float* data, const float* grid,
+                         const float* grad_out, float* grad_grid, float* grad_data,
+                         void* stream);
+
+/* Kernel timing for benchmarks (no reference counterpart; the reference timed
+ * with torch.cuda.synchronize + perf_counter, benchmarks/benchmark_transformer.py:76-84).
+ * While enabled, HIP events are recorded on the launch stream around the
+ * integrator kernels ("forward": the fixed-step forward kernel; "backward": the
+ * fused replay/adjoint kernel).  cpab_profile_read waits for and sums the
+ * recorded launches of one kernel and forgets them. */
+void cpab_profile_enable(int on);
+int cpab_profile_read(const char* kernel, double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CPAB_HIP_H */

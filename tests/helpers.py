@@ -1,0 +1,50 @@
+"""Shared helpers for the tests: seeded inputs and tolerance checks."""
+import numpy as np
+
+from cpab import Cpab
+
+_CACHE = {}
+
+
+def cpab_for(tess):
+    key = tuple(tess)
+    if key not in _CACHE:
+        _CACHE[key] = Cpab(list(tess))
+    return _CACHE[key]
+
+
+def seeded_theta(T, n, scale, seed):
+    return (np.random.default_rng(seed).standard_normal((n, T.params.d)) * scale).astype(np.float32)
+
+
+def uniform_points(ndim, n, seed):
+    return np.random.default_rng(seed).random((ndim, n)).astype(np.float32)
+
+
+def meshgrid(sizes):
+    """uniform_meshgrid of the reference (coordinate 0 fastest), in float32."""
+    lin = [np.linspace(0, 1, s, dtype=np.float32) for s in sizes]
+    mesh = np.meshgrid(*lin[::-1], indexing="ij")
+    return np.stack([m.reshape(-1) for m in mesh[::-1]]).astype(np.float32)
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def assert_grad_close(got, ref, rtol=1e-4, atol_frac=1e-5):
+    """Gradient parity: per element |got - ref| <= rtol*|ref| + atol_frac*max|ref|.
+
+    The moments are sums of many per-trajectory contributions accumulated with
+    float atomics in no fixed order, so elements whose contributions cancel
+    carry an absolute (not relative) error of a few fp32 ulps of the summed
+    magnitudes; atol_frac*max|ref| bounds that.
+    """
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = np.abs(ref).max()
+    bad = np.abs(got - ref) > rtol * np.abs(ref) + atol_frac * scale
+    assert not bad.any(), (f"{bad.sum()} of {bad.size} elements off; max abs err "
+                           f"{np.abs(got - ref).max():.3e}, scale {scale:.3e}")

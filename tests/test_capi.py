@@ -1,0 +1,77 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol
+include/cpab_hip.h declares, and rejects bad arguments before any HIP call
+(the reference's TORCH_CHECK set, transformer_cuda.cu:38-48,183-197)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from cpab.pytorch import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.realpath(__file__)))
+
+
+def _declared():
+    txt = open(os.path.join(ROOT, "include", "cpab_hip.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(cpab_\w+)\s*\(", txt)))
+
+
+def test_header_symbols_exported():
+    lib = ctypes.CDLL(_native.LIB_PATH)
+    declared = _declared()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_native.exported_symbols())
+
+
+def test_abi_version():
+    assert _native.load_library().cpab_abi_version() >= 100
+
+
+def _err(lib):
+    return lib.cpab_last_error_string().decode()
+
+
+def test_forward_rejects_bad_steps_and_ndim():
+    lib = _native.load_library()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc = lib.cpab_forward(2, 10, 1, 0, 101, 4, 4, 1, 0, p, p, p, p, None)
+    assert rc == 1 and "CPAB_MAX_STEPS=100" in _err(lib)
+    rc = lib.cpab_forward(2, 10, 1, 0, 0, 4, 4, 1, 0, p, p, p, p, None)
+    assert rc == 1 and "nstepsolver > 0" in _err(lib)
+    rc = lib.cpab_forward(4, 10, 1, 0, 50, 4, 4, 1, 0, p, p, p, p, None)
+    assert rc == 1 and "ndim" in _err(lib)
+    rc = lib.cpab_forward(2, 10, 1, 0, 50, 4, 4, 1, 2, p, p, p, p, None)
+    assert rc == 1 and "adaptive_substeps" in _err(lib)
+    rc = lib.cpab_forward(2, 10, 1, 0, 50, 0, 4, 1, 0, p, p, p, p, None)
+    assert rc == 1 and "tessellation" in _err(lib)
+
+
+def test_backward_rejects_null_and_small_workspace():
+    lib = _native.load_library()
+    p = ctypes.c_void_p(16)
+    rc = lib.cpab_backward(2, 10, 1, 0, 50, 4, 4, 1, 0, p, p, p, None, None, None, 0, None)
+    assert rc == 1 and "moments" in _err(lib)
+    rc = lib.cpab_backward(3, 10, 1, 0, 101, 2, 2, 2, 0, p, p, p, p, None, None, 0, None)
+    assert rc == 1 and "CPAB_MAX_STEPS" in _err(lib)
+
+
+def test_trace_and_interp_validation():
+    lib = _native.load_library()
+    p = ctypes.c_void_p(16)
+    rc = lib.cpab_trace_cells(1, 10, 1, 0, 50, 4, 1, 1, 0, p, p, p, p, None)
+    assert rc == 1
+    sizes = (ctypes.c_int64 * 3)(4, 4, 4)
+    rc = lib.cpab_interp_forward(4, 1, 1, sizes, sizes, p, p, p, None)
+    assert rc == 1 and "ndim" in _err(lib)
+    bad = (ctypes.c_int64 * 2)(0, 4)
+    rc = lib.cpab_interp_forward(2, 1, 1, bad, sizes, p, p, p, None)
+    assert rc == 1
+
+
+def test_missing_library_raises(tmp_path):
+    with pytest.raises(RuntimeError, match="not found"):
+        _native.load_library(str(tmp_path / "nope.so"))

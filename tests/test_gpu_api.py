@@ -1,0 +1,129 @@
+"""End-to-end parity of the drop-in ``Cpab`` API on the GPU against the oracle:
+transform_grid forward + autograd backward (theta and points), transform_data,
+transform_grid_chain, on the benchmark configurations at reduced sizes."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+from helpers import assert_grad_close, cpab_for, meshgrid, seeded_theta, uniform_points
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_grid(T, theta, pts, g_out, nstep=50):
+    """Oracle forward + theta / points gradient of <out, g_out>."""
+    p = T.params
+    nd = p.ndim
+    As = orc.affine(theta, p.basis).reshape(theta.shape[0], p.nC, nd, nd + 1)
+    if nd == 1:
+        out = orc.forward_closed_1d(pts, As, p.nc)
+    else:
+        out = orc.forward_trels(pts, orc.expm(nd, As, 1.0 / nstep), As, p.nc, nstep)
+    mom, gp = orc.backward(pts, As, g_out, p.nc, nstep)
+    gth = orc.project(mom.reshape(theta.shape[0], -1), p.basis, dtype=np.float64)
+    if pts.ndim == 2:
+        gp = gp.astype(np.float64).sum(0)
+    return out, gth, gp
+
+
+@pytest.mark.parametrize("tess,n,B", [([50], 10000, 16), ([20, 20], 20000, 4),
+                                      ([16, 16], 30000, 2), ([10, 10, 10], 5000, 2)])
+def test_transform_grid_fwd_bwd(cuda, tess, n, B):
+    T = cpab_for(tess)
+    nd = len(tess)
+    theta = seeded_theta(T, B, 0.5, 200 + nd)
+    pts = (np.linspace(0, 1, n, dtype=np.float32)[None] if nd == 1 else uniform_points(nd, n, 201))
+    g = np.random.default_rng(202).standard_normal((B, nd, n)).astype(np.float32)
+    th = torch.tensor(theta, device=cuda, requires_grad=True)
+    x = torch.tensor(pts, device=cuda, requires_grad=True)
+    out = T.transform_grid(x, th)
+    out.backward(torch.tensor(g, device=cuda))
+    ref_out, ref_gth, ref_gp = _oracle_grid(T, theta, pts, g)
+    np.testing.assert_allclose(out.detach().cpu().numpy(), ref_out, atol=1e-5, rtol=0)
+    assert_grad_close(th.grad.cpu().numpy(), ref_gth)
+    np.testing.assert_allclose(x.grad.cpu().numpy(), ref_gp, rtol=1e-5,
+                               atol=1e-6 * np.abs(ref_gp).max())
+
+
+def test_transform_grid_mse_loss_c2_shape(cuda):
+    # C2's loss: MSE to a second seeded theta's warped points (reduced nP).
+    T = cpab_for([20, 20])
+    pts = uniform_points(2, 25000, 21)
+    theta = seeded_theta(T, 16, 0.5, 22)
+    theta_t = seeded_theta(T, 16, 0.5, 23)
+    x = torch.tensor(pts, device=cuda)
+    with torch.no_grad():
+        target = T.transform_grid(x, torch.tensor(theta_t, device=cuda))
+    th = torch.tensor(theta, device=cuda, requires_grad=True)
+    out = T.transform_grid(x, th)
+    loss = ((out - target) ** 2).mean()
+    loss.backward()
+    g = (2.0 / out.numel()) * (out - target).detach().cpu().numpy().astype(np.float32)
+    ref_out, ref_gth, _ = _oracle_grid(T, theta, pts, g)
+    np.testing.assert_allclose(out.detach().cpu().numpy(), ref_out, atol=1e-5, rtol=0)
+    assert_grad_close(th.grad.cpu().numpy(), ref_gth)
+
+
+@pytest.mark.parametrize("tess,ins", [([30, 30], (64, 48)), ([10, 10, 10], (20, 18, 16))])
+def test_transform_data(cuda, tess, ins):
+    T = cpab_for(tess)
+    nd = len(tess)
+    B = 2
+    rng = np.random.default_rng(31)
+    data = rng.random((B, 1, *ins)).astype(np.float32)
+    theta = seeded_theta(T, B, 0.5, 33)
+    th = torch.tensor(theta, device=cuda, requires_grad=True)
+    out = T.transform_data(torch.tensor(data, device=cuda), th, list(ins))
+    gout = rng.standard_normal(out.shape).astype(np.float32)
+    out.backward(torch.tensor(gout, device=cuda))
+    grid = T.uniform_meshgrid(list(ins)).cpu().numpy()
+    # torch's device linspace may differ from numpy's by an ulp
+    np.testing.assert_allclose(grid, meshgrid(list(ins)), rtol=0, atol=1.2e-7)
+    p = T.params
+    As = orc.affine(theta, p.basis).reshape(B, p.nC, nd, nd + 1)
+    grid_t = orc.forward_trels(grid, orc.expm(nd, As, 1 / 50), As, p.nc, 50)
+    ref = orc.interp_forward(nd, data, grid_t, ins)
+    np.testing.assert_allclose(out.detach().cpu().numpy(), ref, atol=1e-5, rtol=0)
+    gg, _ = orc.interp_backward(nd, data, grid_t, ins, gout, want_data=False)
+    mom, _ = orc.backward(grid, As, gg, p.nc, 50)
+    ref_gth = orc.project(mom.reshape(B, -1), p.basis, dtype=np.float64)
+    assert_grad_close(th.grad.cpu().numpy(), ref_gth, rtol=1e-3)
+
+
+def test_transform_grid_chain(cuda):
+    T = cpab_for([16, 16])
+    K = 8
+    chain = (np.random.default_rng(51).standard_normal((K, T.params.d)) * 0.3).astype(np.float32)
+    pts = meshgrid([64, 64])
+    th = torch.tensor(chain, device=cuda, requires_grad=True)
+    out = T.transform_grid_chain(torch.tensor(pts, device=cuda), th, scale_by_dt=True)
+    g = np.random.default_rng(52).standard_normal(out.shape).astype(np.float32)
+    out.backward(torch.tensor(g, device=cuda))
+    # Oracle: K stages forward, then reverse-mode through the stages.
+    p = T.params
+    xs = [pts]
+    As_all = []
+    for i in range(K):
+        th_i = chain[i:i + 1] * np.float32(1.0 / K)
+        As = orc.affine(th_i, p.basis).reshape(1, p.nC, 2, 3)
+        As_all.append(As)
+        xs.append(orc.forward_trels(xs[-1], orc.expm(2, As, 1 / 50), As, p.nc, 50))
+    np.testing.assert_allclose(out.detach().cpu().numpy(), xs[-1], atol=1e-5, rtol=0)
+    lam = g
+    grads = [None] * K
+    for i in reversed(range(K)):
+        mom, gp = orc.backward(xs[i], As_all[i], lam, p.nc, 50)
+        grads[i] = orc.project(mom.reshape(1, -1), p.basis, dtype=np.float64)[0] / K
+        lam = gp
+    assert_grad_close(th.grad.cpu().numpy(), np.stack(grads), rtol=1e-3)
+
+
+def test_identity_theta_is_identity(cuda):
+    for tess in ([50], [20, 20], [10, 10, 10]):
+        T = cpab_for(tess)
+        nd = len(tess)
+        pts = uniform_points(nd, 4000, 7)
+        out = T.transform_grid(torch.tensor(pts, device=cuda), T.identity(3))
+        np.testing.assert_array_equal(out.cpu().numpy(), np.broadcast_to(pts, (3, nd, 4000)))

@@ -1,0 +1,205 @@
+"""Kernel-level parity: HIP library (through its C ABI) vs the CPU oracle on the
+same seeded inputs.  Bit-exact for the fixed-step integrators, cell sequences,
+the 1D closed form, point adjoints, affine map, expm and projection; within
+tolerance only for the moment sums (float atomics, no fixed order) and the
+interpolation backward."""
+import numpy as np
+import pytest
+import torch
+
+from cpab.pytorch._native import native
+from cpab.pytorch.transformer import basis_tables
+from oracle import oracle as orc
+
+from helpers import assert_grad_close, cpab_for, meshgrid, seeded_theta, uniform_points
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, cuda):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+def _As_gpu(T, theta, cuda):
+    p = T.params
+    tab = basis_tables(p, cuda)
+    As = torch.empty((theta.shape[0], p.nC, p.ndim, p.ndim + 1), device=cuda)
+    native().affine(p.ndim, _dev(theta, cuda), p.nC, tab["row_ptr"], tab["col_idx"], tab["vals"], As)
+    return As
+
+
+@pytest.mark.parametrize("tess", [[50], [20, 20], [4, 3], [3, 4, 2], [10, 10, 10]])
+def test_affine_and_expm_bitexact(cuda, tess):
+    T = cpab_for(tess)
+    nd = len(tess)
+    theta = seeded_theta(T, 4, 0.5, 100 + nd)
+    As = _As_gpu(T, theta, cuda)
+    ref = orc.affine(theta, T.params.basis).reshape(As.shape)
+    np.testing.assert_array_equal(As.cpu().numpy(), ref)
+    Tr = torch.empty_like(As)
+    native().expm(nd, As, 1.0 / 50, Tr)
+    np.testing.assert_array_equal(Tr.cpu().numpy(), orc.expm(nd, ref, 1.0 / 50))
+
+
+def test_expm_squaring_branch_bitexact(cuda):
+    # Large |A| exercises the scaling-and-squaring branch (norm > 0.5).
+    rng = np.random.default_rng(5)
+    for nd in (1, 2, 3):
+        A = (rng.standard_normal((257, nd, nd + 1)) * 40).astype(np.float32)
+        out = torch.empty(A.shape, device=cuda)
+        native().expm(nd, _dev(A, cuda), 0.5, out)
+        np.testing.assert_array_equal(out.cpu().numpy(), orc.expm(nd, A, 0.5))
+
+
+def _forward_case(T, theta, pts, cuda, nstep=50, adaptive=0):
+    p = T.params
+    nd = p.ndim
+    As = _As_gpu(T, theta, cuda)
+    Tr = torch.empty_like(As)
+    native().expm(nd, As, 1.0 / nstep, Tr)
+    pts_d = _dev(pts, cuda)
+    batched = pts.ndim == 3
+    nP = pts.shape[-1]
+    out = torch.empty((theta.shape[0], nd, nP), device=cuda)
+    native().forward(nd, pts_d, batched, theta.shape[0], nP, nstep, p.nc, adaptive, Tr, As, out)
+    cells = torch.empty((theta.shape[0], nP, nstep), dtype=torch.int32, device=cuda)
+    native().trace_cells(nd, pts_d, batched, theta.shape[0], nP, nstep, p.nc, adaptive, Tr, As, cells)
+    return As.cpu().numpy(), Tr.cpu().numpy(), out.cpu().numpy(), cells.cpu().numpy()
+
+
+@pytest.mark.parametrize("adaptive", [0, 1])
+@pytest.mark.parametrize("tess,pts_kind", [([20, 20], "uniform"), ([16, 16], "mesh"),
+                                           ([30, 30], "mesh"), ([3, 5], "outside")])
+def test_forward_2d_bitexact(cuda, tess, pts_kind, adaptive):
+    T = cpab_for(tess)
+    theta = seeded_theta(T, 3, 0.5, 22)
+    if pts_kind == "uniform":
+        pts = uniform_points(2, 20000, 21)
+    elif pts_kind == "mesh":
+        pts = meshgrid([96, 80])
+    else:  # points outside the domain exercise the boundary-triangle rules
+        pts = (uniform_points(2, 20000, 3) * 1.6 - 0.3).astype(np.float32)
+    As, Tr, out, cells = _forward_case(T, theta, pts, cuda, adaptive=adaptive)
+    ref, ref_cells = orc.forward_trels(pts, Tr, As, tess, 50, adaptive=bool(adaptive),
+                                       return_cells=True)
+    np.testing.assert_array_equal(cells, ref_cells)
+    np.testing.assert_array_equal(out, ref)
+
+
+@pytest.mark.parametrize("adaptive", [0, 1])
+@pytest.mark.parametrize("tess,pts_kind", [([4, 4, 4], "mesh"), ([10, 10, 10], "uniform"),
+                                           ([2, 3, 2], "outside")])
+def test_forward_3d_bitexact(cuda, tess, pts_kind, adaptive):
+    T = cpab_for(tess)
+    theta = seeded_theta(T, 2, 0.5, 43)
+    if pts_kind == "mesh":
+        pts = meshgrid([21, 17, 13])
+    elif pts_kind == "uniform":
+        pts = uniform_points(3, 8000, 41)
+    else:
+        pts = (uniform_points(3, 8000, 4) * 1.6 - 0.3).astype(np.float32)
+    As, Tr, out, cells = _forward_case(T, theta, pts, cuda, adaptive=adaptive)
+    ref, ref_cells = orc.forward_trels(pts, Tr, As, tess, 50, adaptive=bool(adaptive),
+                                       return_cells=True)
+    np.testing.assert_array_equal(cells, ref_cells)
+    np.testing.assert_array_equal(out, ref)
+
+
+def test_forward_batched_points(cuda):
+    T = cpab_for([20, 20])
+    theta = seeded_theta(T, 3, 0.5, 9)
+    pts = np.random.default_rng(8).random((3, 2, 5000)).astype(np.float32)
+    As, Tr, out, cells = _forward_case(T, theta, pts, cuda)
+    ref = orc.forward_trels(pts, Tr, As, [20, 20], 50)
+    np.testing.assert_array_equal(out, ref)
+
+
+def test_forward_1d_closed_form(cuda):
+    T = cpab_for([50])
+    theta = seeded_theta(T, 16, 0.5, 11)
+    pts = np.linspace(0, 1, 10000, dtype=np.float32)[None]
+    As = _As_gpu(T, theta, cuda)
+    out = torch.empty((16, 1, 10000), device=cuda)
+    native().forward_1d_closed_form(_dev(pts, cuda), False, 16, 10000, 50, As, out)
+    ref = orc.forward_closed_1d(pts, As.cpu().numpy(), [50])
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+
+
+def _backward_case(T, theta, pts, g, cuda, nstep=50, adaptive=0, want_points=True):
+    p = T.params
+    nd = p.ndim
+    As = _As_gpu(T, theta, cuda)
+    n_theta, nP = theta.shape[0], pts.shape[-1]
+    mom = torch.empty((n_theta, p.nC, nd * (nd + 1)), device=cuda)
+    gp = torch.empty((n_theta, nd, nP), device=cuda) if want_points else None
+    nbytes = native().backward_workspace_size(nd, nP, n_theta, p.nC)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=cuda) if nbytes else None
+    native().backward(nd, _dev(pts, cuda), pts.ndim == 3, n_theta, nP, nstep, p.nc, adaptive, As,
+                      _dev(g, cuda), mom, gp, ws)
+    return As.cpu().numpy(), mom.cpu().numpy(), None if gp is None else gp.cpu().numpy()
+
+
+@pytest.mark.parametrize("adaptive", [0, 1])
+@pytest.mark.parametrize("tess,kind,n", [([50], "line", 10000), ([20, 20], "uniform", 20000),
+                                         ([30, 30], "mesh", 0), ([10, 10, 10], "uniform", 6000),
+                                         ([4, 4, 4], "mesh", 0)])
+def test_backward_parity(cuda, tess, kind, n, adaptive):
+    T = cpab_for(tess)
+    nd = len(tess)
+    theta = seeded_theta(T, 3, 0.5, 60 + nd)
+    if kind == "line":
+        pts = np.linspace(0, 1, n, dtype=np.float32)[None]
+    elif kind == "uniform":
+        pts = uniform_points(nd, n, 61)
+    else:
+        pts = meshgrid([64, 48] if nd == 2 else [17, 13, 11])
+    g = np.random.default_rng(62).standard_normal((3, nd, pts.shape[-1])).astype(np.float32)
+    As, mom, gp = _backward_case(T, theta, pts, g, cuda, adaptive=adaptive)
+    ref_m, ref_gp = orc.backward(pts, As, g, tess, 50, adaptive=bool(adaptive))
+    np.testing.assert_array_equal(gp, ref_gp)
+    assert_grad_close(mom, ref_m, rtol=2e-5)
+
+
+def test_backward_no_points_grad(cuda):
+    T = cpab_for([20, 20])
+    theta = seeded_theta(T, 2, 0.5, 3)
+    pts = uniform_points(2, 3000, 4)
+    g = np.random.default_rng(5).standard_normal((2, 2, 3000)).astype(np.float32)
+    As, mom, _ = _backward_case(T, theta, pts, g, cuda, want_points=False)
+    ref_m, _ = orc.backward(pts, As, g, [20, 20], 50)
+    assert_grad_close(mom, ref_m, rtol=2e-5)
+
+
+@pytest.mark.parametrize("tess", [[50], [20, 20], [10, 10, 10]])
+def test_project_bitexact(cuda, tess):
+    T = cpab_for(tess)
+    p = T.params
+    tab = basis_tables(p, cuda)
+    M = np.random.default_rng(1).standard_normal((5, p.D)).astype(np.float32)
+    out = torch.empty((5, p.d), device=cuda)
+    native().project(_dev(M, cuda), p.D, p.d, tab["col_ptr"], tab["row_idx"], tab["vals_t"], out)
+    np.testing.assert_array_equal(out.cpu().numpy(), orc.project(M, p.basis))
+
+
+@pytest.mark.parametrize("nd,ins,outs", [(2, (40, 56), (48, 36)), (3, (12, 10, 14), (9, 11, 13)),
+                                         (1, (77,), (50,)), (2, (512, 512), (130, 70))])
+def test_interp_parity(cuda, nd, ins, outs):
+    rng = np.random.default_rng(30 + nd)
+    B, C = 2, 3
+    data = rng.random((B, C, *ins)).astype(np.float32)
+    nP = int(np.prod(outs))
+    grid = (rng.random((B, nd, nP)) * 1.3 - 0.15).astype(np.float32)  # incl. clamped border
+    gout = rng.standard_normal((B, C, *outs)).astype(np.float32)
+    out = torch.empty((B, C, *outs), device=cuda)
+    native().interp_forward(nd, _dev(data, cuda), _dev(grid, cuda), outs, out)
+    np.testing.assert_array_equal(out.cpu().numpy(), orc.interp_forward(nd, data, grid, outs))
+    gg = torch.empty((B, nd, nP), device=cuda)
+    gd = torch.empty_like(torch.from_numpy(data)).to(cuda)
+    native().interp_backward(nd, _dev(data, cuda), _dev(grid, cuda), outs, _dev(gout, cuda), gg, gd)
+    rg, rd = orc.interp_backward(nd, data, grid, outs, gout, dtype=np.float64)
+    np.testing.assert_allclose(gg.cpu().numpy(), rg, rtol=1e-5, atol=1e-5 * np.abs(rg).max())
+    # grad_data sums many float-atomic contributions per pixel (clamped border
+    # points pile up): bound the error by the summed magnitudes per pixel.
+    _, mag = orc.interp_backward(nd, data, grid, outs, np.abs(gout), dtype=np.float64)
+    err = np.abs(gd.cpu().numpy() - rd)
+    assert (err <= 1e-5 * np.abs(rd) + 2e-6 * mag + 1e-7).all(), float(err.max())
