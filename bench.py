@@ -42,7 +42,23 @@ def parse():
                     help="approximate CPU time budget of the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--nstep", type=int, default=50)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run 3 device-to-device copies of MIB MiB (scales the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters) and exit")
     return ap.parse_args()
+
+
+def calibrate_copy(mib):
+    """Plain copy kernel of known size: reads and writes mib MiB per launch."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.rand(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": n * 4, "launches": 3}))
 
 
 def make_inputs(T, nP, B, seed_pts=21, seed_theta=22, seed_target=23):
@@ -163,6 +179,9 @@ def cpu_baseline(args):
 
 def main():
     args = parse()
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
               "(the CPAB path has no multi-GPU component here)", file=sys.stderr)

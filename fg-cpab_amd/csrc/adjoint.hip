@@ -1,16 +1,18 @@
 // Fused backward: midpoint-trajectory replay + discrete adjoint + cell moments
 // (cpab_ops_1d.cu:331-422, cpab_ops_2d.cu:384-513, cpab_ops_3d.cu:405-532).
 //
-// Per trajectory (one lane):
-//   phase 1  T explicit-midpoint steps from p0, keeping a checkpoint every kSeg
-//            steps.  The checkpoint array lives in VGPRs: phase 1 is unrolled
-//            over segments so every store has a static index, and phase 2 reads
-//            a checkpoint with a uniform select chain (no scratch memory).
-//   phase 2  segments last to first: replay kSeg steps from the checkpoint into
-//            a register buffer, then walk them backwards propagating lambda and
-//            accumulating the 2x3 (1x2, 3x4) moment of the current cell; the
-//            moment is flushed whenever the cell changes, exactly as the
-//            reference groups its flushes.
+// Per trajectory (one lane), two variants with identical results:
+//   register  (T == kRegSteps, 1D/2D) phase 1 runs the T explicit-midpoint
+//             steps fully unrolled and keeps every position and cell in VGPRs
+//             (cells packed two per register); phase 2 walks them backwards.
+//             One midpoint pass per trajectory.
+//   segmented (any T <= 100, 3D) phase 1 keeps a checkpoint every kSeg steps
+//             in a VGPR shift register; phase 2 replays each segment from its
+//             checkpoint into registers and walks it backwards (the
+//             reference's scheme, cpab_ops_2d.cu:236-263).
+// In both, phase 2 propagates lambda and accumulates the 2x3 (1x2, 3x4) moment
+// of the current cell, flushing it whenever the cell changes, exactly as the
+// reference groups its flushes.
 //
 // Moment accumulation on MI355X: each workgroup serves ONE theta, and when the
 // nC x ppc table fits it keeps a private copy of that theta's moments in LDS
@@ -44,10 +46,19 @@ template <> __device__ __forceinline__ int lookup<3>(const float (&p)[3], const 
   return cell_3d(p[0], p[1], p[2], g.nx, g.ny, g.nz);
 }
 
-template <int D, typename Ptr> __device__ __forceinline__ Aff<D> fetch(Ptr tab, int c);
-template <> __device__ __forceinline__ Aff<1> fetch<1>(const float* tab, int c) { return load_aff1(tab, c); }
-template <> __device__ __forceinline__ Aff<2> fetch<2>(const float* tab, int c) { return load_aff2(tab, c); }
-template <> __device__ __forceinline__ Aff<3> fetch<3>(const float* tab, int c) { return load_aff3(tab, c); }
+template <int D> struct Fetch;
+template <> struct Fetch<1> {
+  template <typename P> static __device__ __forceinline__ Aff<1> at(P tab, int c) { return load_aff1(tab, c); }
+};
+template <> struct Fetch<2> {
+  template <typename P> static __device__ __forceinline__ Aff<2> at(P tab, int c) { return load_aff2(tab, c); }
+};
+template <> struct Fetch<3> {
+  template <typename P> static __device__ __forceinline__ Aff<3> at(P tab, int c) { return load_aff3(tab, c); }
+};
+template <int D, typename P> __device__ __forceinline__ Aff<D> fetch(P tab, int c) {
+  return Fetch<D>::at(tab, c);
+}
 
 __device__ __forceinline__ void velocity(const Aff<1>& A, const float (&p)[1], float (&v)[1]) {
   v[0] = fmaf(A.a, p[0], A.b);
@@ -85,10 +96,9 @@ __device__ __forceinline__ void adjoint(const Aff<3>& A, const float (&p)[3], fl
 // One replay step from p in cell c (already looked up): explicit midpoint, or
 // with adaptive_substeps the Heun correction when the step leaves the cell
 // (cpab_ops_2d.cu:294-332).
-template <int D, bool ADAPTIVE>
-__device__ __forceinline__ void replay_step(const float* tab, int c, float (&p)[D], float h,
-                                            float hh, const Cells& g) {
-  const Aff<D> A = fetch<D>(tab, c);
+template <int D, bool ADAPTIVE, typename P>
+__device__ __forceinline__ void replay_step_with(P tab, const Aff<D>& A, int c, float (&p)[D],
+                                                 float h, float hh, const Cells& g) {
   if (!ADAPTIVE) {
     midpoint(A, p, h, hh);
     return;
@@ -108,6 +118,12 @@ __device__ __forceinline__ void replay_step(const float* tab, int c, float (&p)[
   velocity(fetch<D>(tab, ce), q, v1);
 #pragma unroll
   for (int k = 0; k < D; ++k) p[k] = fmaf(hh, v0[k] + v1[k], p[k]);
+}
+
+template <int D, bool ADAPTIVE, typename P>
+__device__ __forceinline__ void replay_step(P tab, int c, float (&p)[D], float h, float hh,
+                                            const Cells& g) {
+  replay_step_with<D, ADAPTIVE>(tab, fetch<D>(tab, c), c, p, h, hh, g);
 }
 
 // Checkpoint stack in VGPRs.  Phase 2 consumes checkpoints in exactly the
@@ -171,37 +187,22 @@ __device__ __forceinline__ void flush_global(float* __restrict__ mom, bool need,
   }
 }
 
-template <int D, bool ADAPTIVE, bool LDS_A, bool LDS_BINS>
-__global__ __launch_bounds__(512) void backward_kernel(
-    int nP, int batched, int T, Cells g, int nC, const float* __restrict__ points,
-    const float* __restrict__ As, const float* __restrict__ grad_out,
-    float* __restrict__ moments, float* __restrict__ partials, float* __restrict__ grad_points) {
-  constexpr int P = Dim<D>::P;
-  extern __shared__ float lds[];
-  const int b = blockIdx.y;
-  const int R = nC * P;
-  const float* __restrict__ Ag = As + (size_t)b * R;
-  float* ldsA = lds;
-  float* bins = lds + (LDS_A ? R : 0);
-  if (LDS_A) {
-    const float2* s2 = reinterpret_cast<const float2*>(Ag);
-    float2* d2 = reinterpret_cast<float2*>(ldsA);
-    for (int i = threadIdx.x; i < R / 2; i += blockDim.x) d2[i] = s2[i];
-  }
-  if (LDS_BINS) {
-    for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
-  }
-  if (LDS_A || LDS_BINS) __syncthreads();
-  const float* tab = LDS_A ? static_cast<const float*>(ldsA) : Ag;
-  float* __restrict__ mom_b = moments + (size_t)b * R;
 
+// Segmented variant (any T).
+template <int D, bool ADAPTIVE, bool LDS_BINS, typename P>
+__device__ __forceinline__ void segmented_body(P tab, int nP, int batched, int T, const Cells& g,
+                                               const float* __restrict__ points,
+                                               const float* __restrict__ grad_out, float* bins,
+                                               float* __restrict__ mom_b,
+                                               float* __restrict__ grad_points) {
+  constexpr int PP = Dim<D>::P;
+  const int b = blockIdx.y;
   const float h = 1.0f / (float)T;
   const float hh = h * 0.5f;
   const float hhh = hh * h;
   const int nseg = (T + kSeg - 1) / kSeg;
   const float* __restrict__ pts = points + (batched ? (size_t)b * D * nP : 0);
   const float* __restrict__ gout = grad_out + (size_t)b * D * nP;
-
   // The loop bound is uniform so every wave stays converged (the global flush
   // needs all 64 lanes); lanes past nP replay a clamped point and contribute nothing.
   for (int base = blockIdx.x * blockDim.x; base < nP; base += gridDim.x * blockDim.x) {
@@ -229,9 +230,9 @@ __global__ __launch_bounds__(512) void backward_kernel(
     float lam[D];
 #pragma unroll
     for (int k = 0; k < D; ++k) lam[k] = gout[pi + (size_t)k * nP];
-    float m[P];
+    float m[PP];
 #pragma unroll
-    for (int k = 0; k < P; ++k) m[k] = 0.0f;
+    for (int k = 0; k < PP; ++k) m[k] = 0.0f;
     int prev = -1;
     for (int seg = nseg - 1; seg >= 0; --seg) {
       const int len = min(kSeg, T - seg * kSeg);
@@ -256,13 +257,13 @@ __global__ __launch_bounds__(512) void backward_kernel(
           const int c = sc[s];
           const bool need = valid && c != prev && prev >= 0;
           if (LDS_BINS) {
-            if (need) flush_lds<P>(bins, prev, m);
+            if (need) flush_lds<PP>(bins, prev, m);
           } else {
-            flush_global<P>(mom_b, need, prev, m);
+            flush_global<PP>(mom_b, need, prev, m);
           }
           if (c != prev) {
 #pragma unroll
-            for (int k = 0; k < P; ++k) m[k] = 0.0f;
+            for (int k = 0; k < PP; ++k) m[k] = 0.0f;
             prev = c;
           }
           adjoint(fetch<D>(tab, c), sp[s], h, hh, hhh, m, lam);
@@ -270,16 +271,122 @@ __global__ __launch_bounds__(512) void backward_kernel(
       }
     }
     if (LDS_BINS) {
-      if (valid) flush_lds<P>(bins, prev, m);
+      if (valid) flush_lds<PP>(bins, prev, m);
     } else {
-      flush_global<P>(mom_b, valid, prev, m);
+      flush_global<PP>(mom_b, valid, prev, m);
     }
     if (grad_points && valid) {
 #pragma unroll
       for (int k = 0; k < D; ++k) grad_points[(size_t)b * D * nP + pi + (size_t)k * nP] = lam[k];
     }
   }
+}
 
+// Register variant: T == TS known at compile time, moments in LDS bins.
+template <int D, bool ADAPTIVE, int TS, typename P>
+__device__ __forceinline__ void register_body(P tab, int nP, int batched, const Cells& g,
+                                              const float* __restrict__ points,
+                                              const float* __restrict__ grad_out, float* bins,
+                                              float* __restrict__ grad_points) {
+  constexpr int PP = Dim<D>::P;
+  const int b = blockIdx.y;
+  const float h = 1.0f / (float)TS;
+  const float hh = h * 0.5f;
+  const float hhh = hh * h;
+  const float* __restrict__ pts = points + (batched ? (size_t)b * D * nP : 0);
+  const float* __restrict__ gout = grad_out + (size_t)b * D * nP;
+  for (int base = blockIdx.x * blockDim.x; base < nP; base += gridDim.x * blockDim.x) {
+    const int pi0 = base + (int)threadIdx.x;
+    const bool valid = pi0 < nP;
+    const int pi = valid ? pi0 : nP - 1;
+    float p[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) p[k] = pts[pi + (size_t)k * nP];
+    float lam[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) lam[k] = gout[pi + (size_t)k * nP];
+
+    // Phase 1: the whole midpoint trajectory, positions and cells in VGPRs.
+    // The current cell's affine block stays in registers and is re-read only
+    // at steps where some lane of the wave changed cell.
+    float traj[TS][D];
+    uint32_t cells[(TS + 1) / 2];
+    int cur = lookup<D>(p, g);
+    Aff<D> A = fetch<D>(tab, cur);
+#pragma unroll
+    for (int t = 0; t < TS; ++t) {
+      const int c = (t == 0) ? cur : lookup<D>(p, g);
+      if (__builtin_amdgcn_ballot_w64(c != cur)) {
+        if (c != cur) A = fetch<D>(tab, c);
+        cur = c;
+      }
+      if (t & 1) cells[t >> 1] |= (uint32_t)c << 16;
+      else cells[t >> 1] = (uint32_t)c;
+#pragma unroll
+      for (int k = 0; k < D; ++k) traj[t][k] = p[k];
+      replay_step_with<D, ADAPTIVE>(tab, A, c, p, h, hh, g);
+    }
+
+    // Phase 2: reverse sweep.  The flush test is skipped wave-wide when no
+    // lane changes cell at this step.
+    float m[PP];
+#pragma unroll
+    for (int k = 0; k < PP; ++k) m[k] = 0.0f;
+    int prev = -1;
+#pragma unroll
+    for (int t = TS - 1; t >= 0; --t) {
+      const int c = (int)((t & 1) ? (cells[t >> 1] >> 16) : (cells[t >> 1] & 0xffffu));
+      const bool change = c != prev;
+      if (__builtin_amdgcn_ballot_w64(change)) {
+        if (change) {
+          if (prev >= 0 && valid) flush_lds<PP>(bins, prev, m);
+#pragma unroll
+          for (int k = 0; k < PP; ++k) m[k] = 0.0f;
+          A = fetch<D>(tab, c);
+        }
+        prev = c;
+      }
+      adjoint(A, traj[t], h, hh, hhh, m, lam);
+    }
+    if (valid) flush_lds<PP>(bins, prev, m);
+    if (grad_points && valid) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) grad_points[(size_t)b * D * nP + pi + (size_t)k * nP] = lam[k];
+    }
+  }
+}
+
+// TS == 0: segmented variant; TS > 0: register variant (requires LDS_BINS).
+template <int D, bool ADAPTIVE, bool LDS_A, bool LDS_BINS, int TS>
+__global__ __launch_bounds__(TS ? 768 : 512) void backward_kernel(
+    int nP, int batched, int T, Cells g, int nC, const float* __restrict__ points,
+    const float* __restrict__ As, const float* __restrict__ grad_out,
+    float* __restrict__ moments, float* __restrict__ partials, float* __restrict__ grad_points) {
+  constexpr int PP = Dim<D>::P;
+  extern __shared__ float lds[];
+  const int b = blockIdx.y;
+  const int R = nC * PP;
+  const float* __restrict__ Ag = As + (size_t)b * R;
+  float* ldsA = lds;
+  float* bins = lds + (LDS_A ? R : 0);
+  if (LDS_A) {
+    const float2* s2 = reinterpret_cast<const float2*>(Ag);
+    float2* d2 = reinterpret_cast<float2*>(ldsA);
+    for (int i = threadIdx.x; i < R / 2; i += blockDim.x) d2[i] = s2[i];
+  }
+  if (LDS_BINS) {
+    for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
+  }
+  if (LDS_A || LDS_BINS) __syncthreads();
+  if constexpr (TS > 0) {
+    static_assert(LDS_BINS, "the register variant accumulates in LDS bins");
+    if (LDS_A) register_body<D, ADAPTIVE, TS>(as_lds(ldsA), nP, batched, g, points, grad_out, bins, grad_points);
+    else register_body<D, ADAPTIVE, TS>(Ag, nP, batched, g, points, grad_out, bins, grad_points);
+  } else {
+    float* __restrict__ mom_b = moments + (size_t)b * R;
+    if (LDS_A) segmented_body<D, ADAPTIVE, LDS_BINS>(as_lds(ldsA), nP, batched, T, g, points, grad_out, bins, mom_b, grad_points);
+    else segmented_body<D, ADAPTIVE, LDS_BINS>(Ag, nP, batched, T, g, points, grad_out, bins, mom_b, grad_points);
+  }
   if (LDS_BINS) {
     __syncthreads();
     float* dst = partials + ((size_t)b * gridDim.x + blockIdx.x) * R;
@@ -287,11 +394,11 @@ __global__ __launch_bounds__(512) void backward_kernel(
   }
 }
 
-template <int D, bool ADAPTIVE, bool LDS_A, bool LDS_BINS>
+template <int D, bool ADAPTIVE, bool LDS_A, bool LDS_BINS, int TS>
 hipError_t go(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int T,
               const float* points, const float* As, const float* grad_out, float* moments,
               float* partials, float* grad_points, const LaunchCfg& cfg, hipStream_t s) {
-  auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, LDS_BINS>;
+  auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, LDS_BINS, TS>;
   const size_t R = (size_t)geo.nC * Dim<D>::P;
   const size_t lds = R * sizeof(float) * ((LDS_A ? 1 : 0) + (LDS_BINS ? 1 : 0));
   if (lds > 65536) {
@@ -311,19 +418,28 @@ hipError_t dispatch(const Geometry& geo, int64_t nP, int64_t n_theta, int batche
                     int adaptive, const float* points, const float* As, const float* grad_out,
                     float* moments, float* partials, float* grad_points, const LaunchCfg& cfg,
                     hipStream_t s) {
-#define CPAB_GO(AD, LA, LB)                                                                  \
-  return go<D, AD, LA, LB>(geo, nP, n_theta, batched, T, points, As, grad_out, moments,     \
-                           partials, grad_points, cfg, s)
+#define CPAB_GO(AD, LA, LB, TS)                                                               \
+  return go<D, AD, LA, LB, TS>(geo, nP, n_theta, batched, T, points, As, grad_out, moments,   \
+                               partials, grad_points, cfg, s)
+  if (D <= 2 && cfg.reg_steps == kRegSteps && T == kRegSteps && cfg.lds_bins) {
+    const int key = (adaptive ? 2 : 0) | (cfg.lds_table ? 1 : 0);
+    switch (key) {
+      case 0: CPAB_GO(false, false, true, kRegSteps);
+      case 1: CPAB_GO(false, true, true, kRegSteps);
+      case 2: CPAB_GO(true, false, true, kRegSteps);
+      default: CPAB_GO(true, true, true, kRegSteps);
+    }
+  }
   const int key = (adaptive ? 4 : 0) | (cfg.lds_table ? 2 : 0) | (cfg.lds_bins ? 1 : 0);
   switch (key) {
-    case 0: CPAB_GO(false, false, false);
-    case 1: CPAB_GO(false, false, true);
-    case 2: CPAB_GO(false, true, false);
-    case 3: CPAB_GO(false, true, true);
-    case 4: CPAB_GO(true, false, false);
-    case 5: CPAB_GO(true, false, true);
-    case 6: CPAB_GO(true, true, false);
-    default: CPAB_GO(true, true, true);
+    case 0: CPAB_GO(false, false, false, 0);
+    case 1: CPAB_GO(false, false, true, 0);
+    case 2: CPAB_GO(false, true, false, 0);
+    case 3: CPAB_GO(false, true, true, 0);
+    case 4: CPAB_GO(true, false, false, 0);
+    case 5: CPAB_GO(true, false, true, 0);
+    case 6: CPAB_GO(true, true, false, 0);
+    default: CPAB_GO(true, true, true, 0);
   }
 #undef CPAB_GO
 }

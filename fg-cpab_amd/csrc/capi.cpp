@@ -128,18 +128,28 @@ cpab::LaunchCfg forward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta
   return c;
 }
 
-cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta) {
+cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta, int T) {
   const DeviceInfo dev = device_info();
   const int64_t table = (int64_t)g.nC * g.ppc() * 4;
   cpab::LaunchCfg c{};
-  c.block = env_int("CPAB_BWD_BLOCK", 512);
   c.lds_bins = (table <= dev.lds) ? env_int("CPAB_BWD_LDS_BINS", 1) : 0;
   const int64_t used = c.lds_bins ? table : 0;
   c.lds_table = (used + table <= dev.lds) ? env_int("CPAB_BWD_LDS_TABLE", 1) : 0;
   const int64_t lds = table * (c.lds_bins + c.lds_table);
-  const int max_wg_threads = 2048;  // 32 waves per CU
-  int wg_per_cu = std::max(1, max_wg_threads / c.block);
-  if (lds > 0) wg_per_cu = (int)std::max<int64_t>(1, std::min<int64_t>(wg_per_cu, dev.lds / lds));
+  // Register variant: whole trajectory in VGPRs (~160 per lane -> 3 waves per
+  // SIMD), so one 768-thread workgroup (12 waves) per CU.
+  const bool reg = g.ndim <= 2 && T == cpab::kRegSteps && c.lds_bins && g.nC <= 65535 &&
+                   env_int("CPAB_BWD_REG", 1);
+  c.reg_steps = reg ? cpab::kRegSteps : 0;
+  int wg_per_cu;
+  if (reg) {
+    c.block = 768;
+    wg_per_cu = 1;
+  } else {
+    c.block = env_int("CPAB_BWD_BLOCK", 512);
+    wg_per_cu = std::max(1, 2048 / c.block);  // 32 waves per CU
+    if (lds > 0) wg_per_cu = (int)std::max<int64_t>(1, std::min<int64_t>(wg_per_cu, dev.lds / lds));
+  }
   const int64_t want = (int64_t)dev.cus * wg_per_cu;
   int64_t chunks = std::max<int64_t>(1, div_up(want, std::max<int64_t>(n_theta, 1)));
   chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
@@ -266,9 +276,11 @@ int64_t cpab_backward_workspace_size(int ndim, int64_t nP, int64_t n_theta, int 
   cpab::Geometry g{};
   g.ndim = ndim;
   g.nC = nC;
-  const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_theta);
-  if (!cfg.lds_bins) return 0;
-  return (int64_t)n_theta * cfg.chunks * nC * g.ppc() * (int64_t)sizeof(float);
+  // Partials: one moment table per workgroup, for whichever variant runs.
+  const cpab::LaunchCfg a = backward_cfg(g, nP, n_theta, cpab::kRegSteps);
+  const cpab::LaunchCfg b = backward_cfg(g, nP, n_theta, 0);
+  const int64_t chunks = std::max(a.lds_bins ? a.chunks : 0, b.lds_bins ? b.chunks : 0);
+  return (int64_t)n_theta * chunks * nC * g.ppc() * (int64_t)sizeof(float);
 }
 
 int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver, int ncx,
@@ -287,7 +299,7 @@ int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nsteps
   const int R = g.nC * g.ppc();
   if (nP == 0) return check_hip(cpab::launch_fill(moments, n_theta * R, 0.0f, s), "cpab_backward");
   CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(grad_out);
-  const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_theta);
+  const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_theta, nstepsolver);
   const int64_t need = cfg.lds_bins ? (int64_t)n_theta * cfg.chunks * R * (int64_t)sizeof(float) : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld", (long long)need,

@@ -26,6 +26,9 @@ constexpr int kMaxSteps = 100;
 // position buffer in 26 VGPRs.
 constexpr int kSeg = 8;
 constexpr int kMaxSeg = (kMaxSteps + kSeg - 1) / kSeg;
+// Step count whose backward keeps the whole trajectory in registers (the
+// library default nstepsolver=50); other step counts use the segmented replay.
+constexpr int kRegSteps = 50;
 
 // Correctly rounded float exp / log / expm1: evaluated in double and rounded
 // once.  The reference calls CUDA's expf/logf (a few ulp, implementation
@@ -45,40 +48,64 @@ __device__ __forceinline__ int floor_to_int(float x) {
 //   1D: cpab_ops_1d.cu:52-59   2D: cpab_ops_2d.cu:71-128   3D: cpab_ops_3d.cu:67-131
 // ---------------------------------------------------------------------------
 
+// Clamp bound of the 1D/2D lookups: 1 - 1e-7 rounds to 1 - 2^-23.  For any
+// n < 2^24, clamp(x) * n rounds to a value strictly below n, so
+// floor(clamp(x) * n) <= n - 1 and the reference's min(cell, n-1) never binds;
+// the float floor is then the exact cell coordinate.
+constexpr float kClampHi = 1.0f - 1e-7f;
+
+__device__ __forceinline__ float clamp_lookup(float x) {
+  return __builtin_amdgcn_fmed3f(x, 0.0f, kClampHi);
+}
+
 __device__ __forceinline__ int cell_1d(float px, int nx) {
-  const float xc = fminf(fmaxf(px, 0.0f), 1.0f - 1e-7f);
-  return min(floor_to_int(xc * (float)nx), nx - 1);
+  return (int)__builtin_floorf(clamp_lookup(px) * (float)nx);
+}
+
+// Triangle within a square from the local coordinates (lx, ly) in [0,1):
+//   bit1 = lx < ly (above the main diagonal), bit0 = (1 - lx) < ly (above the
+//   anti-diagonal); raw 0,1,2,3 -> triangle 0,1,3,2 (cpab_ops_2d.cu:119-127).
+__device__ __forceinline__ int tri_2d(float lx, float ly) {
+  const int t1 = ((1.0f - lx) < ly) ? 1 : 0;
+  const int t3 = (lx < ly) ? 3 : 0;
+  return t3 ^ t1;
+}
+
+// Out-of-domain rules (cpab_ops_2d.cu:97-117): the boundary triangle of the
+// nearest square; beyond a corner the diagonal through the corner decides.
+// Falls through to the inside rule exactly as the reference does (NaN input).
+__device__ __forceinline__ int cell_2d_outside(float px, float py, float fx, float fy,
+                                                         int base, float lx, float ly) {
+  if (px <= 0.0f) {
+    if (py <= 0.0f && py * fy < px * fx) return base;
+    if (py >= 1.0f && fmaf(py, fy, -fy) > (-px) * fx) return base + 2;
+    return base + 3;
+  }
+  if (px >= 1.0f) {
+    if (py <= 0.0f && (-py) * fy > fmaf(px, fx, -fx)) return base;
+    if (py >= 1.0f && fmaf(py, fy, -fy) > fmaf(px, fx, -fx)) return base + 2;
+    return base + 1;
+  }
+  if (py <= 0.0f) return base;
+  if (py >= 1.0f) return base + 2;
+  return base + tri_2d(lx, ly);
 }
 
 // Square (cx, cy) holds triangles 4*(cx + cy*nx) + {0 top, 1 right, 2 bottom, 3 left}.
+// Lanes strictly inside (0,1)^2 use the inside rule; if any lane of the wave is
+// outside, a wave-uniform branch applies the boundary rules to those lanes.
 __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   const float fx = (float)nx, fy = (float)ny;
-  const float xc = fminf(fmaxf(px, 0.0f), 1.0f - 1e-7f);
-  const float yc = fminf(fmaxf(py, 0.0f), 1.0f - 1e-7f);
-  const int cx = min(floor_to_int(xc * fx), nx - 1);
-  const int cy = min(floor_to_int(yc * fy), ny - 1);
-  const float lx = fmaf(xc, fx, -(float)cx);
-  const float ly = fmaf(yc, fy, -(float)cy);
-  const int base = (cx + cy * nx) * 4;
-  // Outside [0,1]^2 the point takes the boundary triangle of the nearest
-  // square; beyond a corner the diagonal through the corner decides.
-  if (px <= 0.0f || px >= 1.0f || py <= 0.0f || py >= 1.0f) {
-    if (px <= 0.0f) {
-      if (py <= 0.0f && py * fy < px * fx) return base;
-      if (py >= 1.0f && fmaf(py, fy, -fy) > (-px) * fx) return base + 2;
-      return base + 3;
-    }
-    if (px >= 1.0f) {
-      if (py <= 0.0f && (-py) * fy > fmaf(px, fx, -fx)) return base;
-      if (py >= 1.0f && fmaf(py, fy, -fy) > fmaf(px, fx, -fx)) return base + 2;
-      return base + 1;
-    }
-    return (py <= 0.0f) ? base : base + 2;
+  const float xc = clamp_lookup(px), yc = clamp_lookup(py);
+  const float sx = __builtin_floorf(xc * fx), sy = __builtin_floorf(yc * fy);
+  const float lx = fmaf(xc, fx, -sx), ly = fmaf(yc, fy, -sy);
+  const int base = (int)fmaf(sy, fx, sx) << 2;  // exact: cx + cy*nx < 2^24
+  int c = base + tri_2d(lx, ly);
+  const bool inside = (px > 0.0f) & (px < 1.0f) & (py > 0.0f) & (py < 1.0f);
+  if (__builtin_amdgcn_ballot_w64(!inside)) {
+    if (!inside) c = cell_2d_outside(px, py, fx, fy, base, lx, ly);
   }
-  // Inside: the two diagonals of the square pick the triangle.
-  const int above_main = lx < ly;          // below-left of y = x
-  const int above_anti = (1.0f - lx) < ly; // beyond x + y = 1
-  return base + (above_main ? 3 - above_anti : above_anti);
+  return c;
 }
 
 // Cube (i, j, k) holds tetrahedra 5*(i + j*nx + k*nx*ny) + {0 central, 1..4 corners};
@@ -130,23 +157,42 @@ template <> struct Aff<1> { float a, b; };
 template <> struct Aff<2> { float m[6]; };
 template <> struct Aff<3> { float m[12]; };
 
-// Loads from LDS or global memory depending on where `tab` points; the caller
-// passes an address-space-specific pointer so the right instructions are used.
-template <typename P>
-__device__ __forceinline__ Aff<1> load_aff1(P tab, int c) {
-  const float2 v = *reinterpret_cast<const float2*>(tab + 2 * c);
+// Per-cell table loads.  Global tables use 64-bit addressing; LDS tables are
+// passed as address-space-3 pointers so the offsets stay 32-bit (one
+// v_mul_u32_u24 per fetch) and the loads become ds_read2_b64 / ds_read_b128.
+#define CPAB_LDS __attribute__((address_space(3)))
+template <typename T> using lds_ptr = const T CPAB_LDS*;
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ lds_ptr<float> as_lds(const float* p) { return (lds_ptr<float>)p; }
+
+__device__ __forceinline__ Aff<1> load_aff1(const float* tab, int c) {
+  const v2f v = reinterpret_cast<const v2f*>(tab)[c];
   return {v.x, v.y};
 }
-template <typename P>
-__device__ __forceinline__ Aff<2> load_aff2(P tab, int c) {
-  const float2* q = reinterpret_cast<const float2*>(tab + 6 * c);
-  const float2 a = q[0], b = q[1], d = q[2];
+__device__ __forceinline__ Aff<1> load_aff1(lds_ptr<float> tab, int c) {
+  const v2f v = ((lds_ptr<v2f>)tab)[(uint32_t)c];
+  return {v.x, v.y};
+}
+__device__ __forceinline__ Aff<2> load_aff2(const float* tab, int c) {
+  const v2f* q = reinterpret_cast<const v2f*>(tab) + 3 * (int64_t)c;
+  const v2f a = q[0], b = q[1], d = q[2];
   return {{a.x, a.y, b.x, b.y, d.x, d.y}};
 }
-template <typename P>
-__device__ __forceinline__ Aff<3> load_aff3(P tab, int c) {
-  const float4* q = reinterpret_cast<const float4*>(tab + 12 * c);
-  const float4 a = q[0], b = q[1], d = q[2];
+__device__ __forceinline__ Aff<2> load_aff2(lds_ptr<float> tab, int c) {
+  lds_ptr<v2f> q = (lds_ptr<v2f>)tab + __umul24((uint32_t)c, 3u);
+  const v2f a = q[0], b = q[1], d = q[2];
+  return {{a.x, a.y, b.x, b.y, d.x, d.y}};
+}
+__device__ __forceinline__ Aff<3> load_aff3(const float* tab, int c) {
+  const v4f* q = reinterpret_cast<const v4f*>(tab) + 3 * (int64_t)c;
+  const v4f a = q[0], b = q[1], d = q[2];
+  return {{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w}};
+}
+__device__ __forceinline__ Aff<3> load_aff3(lds_ptr<float> tab, int c) {
+  lds_ptr<v4f> q = (lds_ptr<v4f>)tab + __umul24((uint32_t)c, 3u);
+  const v4f a = q[0], b = q[1], d = q[2];
   return {{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w}};
 }
 

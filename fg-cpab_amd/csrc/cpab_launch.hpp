@@ -20,6 +20,7 @@ struct LaunchCfg {
   int chunks;       // workgroups per theta (gridDim.x)
   int lds_table;    // stage the per-theta cell table in LDS
   int lds_bins;     // accumulate moments in LDS bins (else global atomics)
+  int reg_steps;    // backward: compile-time step count of the register variant (0 = segmented)
 };
 
 int device_cu_count();

@@ -122,13 +122,26 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
       px[k] = pts[p];
       py[k] = pts[p + nP];
     }
+    // The one-step map of the current cell stays in registers; it is
+    // re-read (LDS / L1) only at steps where some lane of the wave changed
+    // cell, which keeps table traffic and LDS bank conflicts off most steps.
+    int cur[PPT];
+    Aff<2> M[PPT];
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      cur[k] = cell_2d(px[k], py[k], nx, ny);
+      M[k] = LDS ? load_aff2(as_lds(lds), cur[k]) : load_aff2(Tg, cur[k]);
+    }
     for (int t = 0; t < T; ++t) {
 #pragma unroll
       for (int k = 0; k < PPT; ++k) {
-        const int c = cell_2d(px[k], py[k], nx, ny);
-        const Aff<2> M = LDS ? load_aff2(static_cast<const float*>(lds), c) : load_aff2(Tg, c);
+        const int c = (t == 0) ? cur[k] : cell_2d(px[k], py[k], nx, ny);
+        if (__builtin_amdgcn_ballot_w64(c != cur[k])) {
+          if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
+          cur[k] = c;
+        }
         float sx, sy;
-        apply2(M, px[k], py[k], sx, sy);
+        apply2(M[k], px[k], py[k], sx, sy);
         if (ADAPTIVE) {
           const int ce = cell_2d(sx, sy, nx, ny);
           if (ce != c) {
@@ -177,7 +190,7 @@ __global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T,
     float px = pts[p], py = pts[p + nP], pz = pts[p + 2 * (size_t)nP];
     for (int t = 0; t < T; ++t) {
       const int c = cell_3d(px, py, pz, nx, ny, nz);
-      const Aff<3> M = LDS ? load_aff3(static_cast<const float*>(lds), c) : load_aff3(Tg, c);
+      const Aff<3> M = LDS ? load_aff3(as_lds(lds), c) : load_aff3(Tg, c);
       float sx, sy, sz;
       apply3(M, px, py, pz, sx, sy, sz);
       if (ADAPTIVE) {

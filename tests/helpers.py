@@ -34,13 +34,14 @@ def rel_err(a, b):
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
 
 
-def assert_grad_close(got, ref, rtol=1e-4, atol_frac=1e-5):
+def assert_grad_close(got, ref, rtol=1e-4, atol_frac=5e-5):
     """Gradient parity: per element |got - ref| <= rtol*|ref| + atol_frac*max|ref|.
 
     The moments are sums of many per-trajectory contributions accumulated with
     float atomics in no fixed order, so elements whose contributions cancel
     carry an absolute (not relative) error of a few fp32 ulps of the summed
-    magnitudes; atol_frac*max|ref| bounds that.
+    magnitudes; atol_frac*max|ref| bounds that (normwise, half the 1e-4
+    relative tolerance the gradients are held to).
     """
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)

@@ -89,7 +89,9 @@ def test_transform_data(cuda, tess, ins):
     gg, _ = orc.interp_backward(nd, data, grid_t, ins, gout, want_data=False)
     mom, _ = orc.backward(grid, As, gg, p.nc, 50)
     ref_gth = orc.project(mom.reshape(B, -1), p.basis, dtype=np.float64)
-    assert_grad_close(th.grad.cpu().numpy(), ref_gth, rtol=1e-3)
+    # normwise 1e-4; near-zero components carry the
+    # absolute error of their cancelling float sums
+    assert_grad_close(th.grad.cpu().numpy(), ref_gth, rtol=1e-3, atol_frac=1e-4)
 
 
 def test_transform_grid_chain(cuda):

@@ -196,10 +196,14 @@ def test_interp_parity(cuda, nd, ins, outs):
     gg = torch.empty((B, nd, nP), device=cuda)
     gd = torch.empty_like(torch.from_numpy(data)).to(cuda)
     native().interp_backward(nd, _dev(data, cuda), _dev(grid, cuda), outs, _dev(gout, cuda), gg, gd)
-    rg, rd = orc.interp_backward(nd, data, grid, outs, gout, dtype=np.float64)
-    np.testing.assert_allclose(gg.cpu().numpy(), rg, rtol=1e-5, atol=1e-5 * np.abs(rg).max())
-    # grad_data sums many float-atomic contributions per pixel (clamped border
-    # points pile up): bound the error by the summed magnitudes per pixel.
+    # Same fp32 weights and per-point sums as the oracle: grad_grid is bit-exact.
+    rg, rd = orc.interp_backward(nd, data, grid, outs, gout)
+    np.testing.assert_array_equal(gg.cpu().numpy(), rg)
+    # grad_data sums many contributions per pixel with float atomics (clamped
+    # border points pile up, several hundred per pixel here) in an order that
+    # differs from the oracle's sequential fp32 sum; both round each partial
+    # sum, so the difference is bounded by ~(count * 2^-24) of the summed
+    # contribution magnitudes of the pixel.
     _, mag = orc.interp_backward(nd, data, grid, outs, np.abs(gout), dtype=np.float64)
-    err = np.abs(gd.cpu().numpy() - rd)
-    assert (err <= 1e-5 * np.abs(rd) + 2e-6 * mag + 1e-7).all(), float(err.max())
+    err = np.abs(gd.cpu().numpy().astype(np.float64) - rd)
+    assert (err <= 1e-4 * mag + 1e-12).all(), float((err / (mag + 1e-30)).max())
