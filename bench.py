@@ -1,18 +1,22 @@
-"""Benchmark of the CPAB hot path on one MI355X (BASELINE.json metric).
+"""Benchmark of the CPAB hot path on one MI355X (BASELINE.json metric and configs).
 
-Workload ("C2"): 2D tessellation [20, 20] on [0,1]^2,
-zero_boundary=True, fp32, batch 16, 125,000 points uniform in [0,1]^2 (seed 21);
-theta ~ N(0,1) * 0.5 in basis coordinates (seed 22); loss = MSE against a second
-seeded theta's (seed 23) warped points.  One step = transform_grid forward +
-MSE + backward w.r.t. theta (the Cpab API path: A = B theta, expm, fixed-step
-forward kernel, fused replay/adjoint kernel, projection), inputs resident in HBM.
+Default (the driver's line) = BASELINE.json configs[1], "C2": 2D tessellation
+[20, 20] on [0,1]^2, zero_boundary=True, fp32, batch 16, 125,000 points uniform
+in [0,1]^2 (seed 21); theta ~ N(0,1) * 0.5 in basis coordinates (seed 22);
+loss = MSE against a second seeded theta's (seed 23) warped points.  One step =
+Cpab.transform_grid forward + MSE + backward w.r.t. theta, inputs resident in
+HBM (A = B theta, expm, fixed-step forward kernel, fused replay/adjoint kernel,
+projection).  --config c1|c3|c4|c5|all measures the other BASELINE.json
+configs the same way (not the driver's line).
 
-Prints ONE JSON line.  Besides the step throughput it reports
-  roofline      the dominant kernel's algorithmic fp32 FLOPs per launch over its
-                average duration, timed with HIP events recorded by the library on
-                the launch stream during the timed steps;
-  cpu_baseline  the reference-semantics CPU restatement (oracle/, OpenMP) timed on
-                this host on a bounded sample of the same workload.
+Prints one JSON line per config with, besides the throughput,
+  roofline      the dominant kernel: algorithmic work per launch (fp32 FLOPs, or
+                bytes for the resampling kernels) over its average duration,
+                timed with HIP events that the library records on the launch
+                stream around every launch during the timed steps;
+  cpu_baseline  the reference-semantics CPU restatement (oracle/, C + OpenMP)
+                timed on this host on a bounded sample of the same workload
+                (default config only).
 """
 import argparse
 import json
@@ -24,13 +28,17 @@ ROOT = os.path.dirname(os.path.realpath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "fg-cpab_amd"))
 sys.path.insert(0, ROOT)
 
-# Algorithmic fp32 FLOPs per trajectory and step (FMA = 2), from the reference
-# kernels: forward Trels step 15 (lookup 7 + affine apply 8); backward = midpoint
-# replay 31 (lookup 7 + 2 affine evals 16 + 4 fma 8) + adjoint/moments 52.
-FLOPS_FWD_STEP_2D = 15
-FLOPS_BWD_STEP_2D = 31 + 52
+# Algorithmic fp32 FLOPs per trajectory and integration step (FMA = 2), counted
+# from the reference kernels (cpab_ops_{1d,2d,3d}.cu):
+#   forward  = lookup + Trels apply                  2D 7+8,  3D 25+18
+#   backward = midpoint replay + adjoint/moments     2D 31+52, 3D 73+114, 1D 9+18
+# The 1D forward is the closed form (~15 flops + 9 per crossing; 15 counted).
+FLOPS = {1: {"forward": None, "backward": 27}, 2: {"forward": 15, "backward": 83},
+         3: {"forward": 43, "backward": 187}}
+FLOPS_1D_FWD = 15
 PEAK_FP32_TFLOPS = 157.3   # MI355X fp32 vector peak (packed); non-packed issue tops out at half
 PEAK_HBM_GBS = 8000.0
+METRIC = "points/sec (fwd+grad), 2D 20x20 tess, 125k pts, B=16; % fp32 VALU peak"
 
 
 def parse():
@@ -38,6 +46,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "all"])
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -61,42 +70,131 @@ def calibrate_copy(mib):
     print(json.dumps({"copy_bytes_per_launch": n * 4, "launches": 3}))
 
 
-def make_inputs(T, nP, B, seed_pts=21, seed_theta=22, seed_target=23):
+def _theta(T, n, scale, seed):
     import numpy as np
-    pts = np.random.default_rng(seed_pts).random((2, nP)).astype(np.float32)
-    theta = (np.random.default_rng(seed_theta).standard_normal((B, T.params.d)) * 0.5).astype(np.float32)
-    theta_t = (np.random.default_rng(seed_target).standard_normal((B, T.params.d)) * 0.5).astype(np.float32)
-    return pts, theta, theta_t
+    return (np.random.default_rng(seed).standard_normal((n, T.params.d)) * scale).astype(np.float32)
 
 
-def gpu_bench(args):
+def _blur_noise(shape, sigma, seed):
+    import numpy as np
+    from scipy.ndimage import gaussian_filter
+    x = np.random.default_rng(seed).random(shape).astype(np.float32)
+    nsp = len(shape) - 2
+    return gaussian_filter(x, sigma=[0, 0] + [sigma] * nsp, mode="reflect",
+                           truncate=4.0).astype(np.float32)
+
+
+def make_c2_inputs(T, nP=125_000, B=16):
+    import numpy as np
+    pts = np.random.default_rng(21).random((2, nP)).astype(np.float32)
+    return pts, _theta(T, B, 0.5, 22), _theta(T, B, 0.5, 23)
+
+
+def setup(cfg, nstep, dev):
+    """Returns (step_fn, info) for one config; step_fn runs one fwd+grad step."""
     import numpy as np
     import torch
     from cpab import Cpab
+
+    if cfg in ("c1", "c2"):
+        if cfg == "c1":
+            T = Cpab([50])
+            pts = np.linspace(0, 1, 10_000, dtype=np.float32)[None]
+            theta, theta_t = _theta(T, 16, 0.5, 11), _theta(T, 16, 0.5, 12)
+            desc = ("C1: 1D CPAB transform_grid fwd+MSE+backward, tess [50], zero_boundary, "
+                    "10000 grid points, batch 16, nstepsolver %d" % nstep)
+        else:
+            T = Cpab([20, 20])
+            pts, theta, theta_t = make_c2_inputs(T)
+            desc = ("C2: 2D CPAB transform_grid fwd+MSE+backward, tess [20,20], zero_boundary, "
+                    "125000 uniform points, batch 16, nstepsolver %d" % nstep)
+        T.set_solver_params(nstepsolver=nstep)
+        x = torch.tensor(pts, device=dev)
+        th0 = torch.tensor(theta, device=dev)
+        with torch.no_grad():
+            target = T.transform_grid(x, torch.tensor(theta_t, device=dev))
+
+        def step():
+            th = th0.detach().requires_grad_(True)
+            out = T.transform_grid(x, th)
+            torch.mean((out - target) ** 2).backward()
+            return th.grad
+
+        traj = pts.shape[1] * theta.shape[0]
+        return step, {"ndim": T.params.ndim, "traj": traj, "desc": desc,
+                      "global_batch": theta.shape[0], "points": pts.shape[1]}
+
+    if cfg in ("c3", "c4"):
+        if cfg == "c3":
+            T = Cpab([30, 30])
+            B, size, sigma, seeds = 16, [512, 512], 4.0, (31, 32, 33)
+            desc = ("C3: 2D CPAB transform_data fwd+MSE+backward, tess [30,30], zero_boundary, "
+                    "16x1x512x512 blurred noise, bilinear, nstepsolver %d" % nstep)
+        else:
+            T = Cpab([10, 10, 10])
+            B, size, sigma, seeds = 1, [128, 128, 128], 3.0, (41, 42, 43)
+            desc = ("C4: 3D CPAB transform_data fwd+MSE+backward, tess [10,10,10], zero_boundary, "
+                    "1x1x128^3 blurred noise, trilinear, nstepsolver %d" % nstep)
+        T.set_solver_params(nstepsolver=nstep)
+        data = torch.tensor(_blur_noise((B, 1, *size), sigma, seeds[0]), device=dev)
+        target = torch.tensor(_blur_noise((B, 1, *size), sigma, seeds[1]), device=dev)
+        th0 = torch.tensor(_theta(T, B, 0.5, seeds[2]), device=dev)
+
+        def step():
+            th = th0.detach().requires_grad_(True)
+            out = T.transform_data(data, th, size)
+            torch.mean((out - target) ** 2).backward()
+            return th.grad
+
+        nP = int(np.prod(size))
+        nd = len(size)
+        # Algorithmic HBM bytes of the resampling (data not requiring grad):
+        # fwd reads grid_t + image and writes out; bwd reads grad_out, grid_t and
+        # image and writes grad_grid.
+        img = B * nP * 4
+        grid_b = B * nd * nP * 4
+        interp_bytes = {"interp_forward": grid_b + img + img,
+                        "interp_backward": img + grid_b + img + grid_b}
+        return step, {"ndim": nd, "traj": B * nP, "desc": desc, "global_batch": B,
+                      "points": nP, "interp_bytes": interp_bytes}
+
+    # c5: chain of 8 stages on a 512x512 meshgrid
+    T = Cpab([16, 16])
+    T.set_solver_params(nstepsolver=nstep)
+    K = 8
+    grid = T.uniform_meshgrid([512, 512])
+    chain0 = torch.tensor((np.random.default_rng(51).standard_normal((K, T.params.d)) * 0.3)
+                          .astype(np.float32), device=dev)
+    chain_t = torch.tensor((np.random.default_rng(52).standard_normal((K, T.params.d)) * 0.3)
+                           .astype(np.float32), device=dev)
+    with torch.no_grad():
+        target = T.transform_grid_chain(grid, chain_t, scale_by_dt=True)
+
+    def step():
+        ch = chain0.detach().requires_grad_(True)
+        out = T.transform_grid_chain(grid, ch, scale_by_dt=True)
+        torch.mean((out - target) ** 2).backward()
+        return ch.grad
+
+    nP = 512 * 512
+    return step, {"ndim": 2, "traj": nP * K, "points_per_step": nP, "desc":
+                  "C5: 2D CPAB transform_grid_chain fwd+MSE+backward, tess [16,16], 8 stages, "
+                  "scale_by_dt, 262144 grid points, nstepsolver %d" % nstep,
+                  "global_batch": 1, "points": nP}
+
+
+def gpu_bench(cfg, args):
+    import torch
     from cpab.pytorch import _native
 
     dev = torch.device("cuda:0")
-    T = Cpab([20, 20])
-    T.set_solver_params(nstepsolver=args.nstep)
-    nP, B = 125_000, 16
-    pts, theta, theta_t = make_inputs(T, nP, B)
-    x = torch.tensor(pts, device=dev)
-    th0 = torch.tensor(theta, device=dev)
-    with torch.no_grad():
-        target = T.transform_grid(x, torch.tensor(theta_t, device=dev))
-
-    def step():
-        th = th0.detach().requires_grad_(True)
-        out = T.transform_grid(x, th)
-        loss = torch.mean((out - target) ** 2)
-        loss.backward()
-        return th.grad
-
+    step, info = setup(cfg, args.nstep, dev)
+    names = ["forward", "backward", "interp_forward", "interp_backward"]
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    _native.profile_read("forward")
-    _native.profile_read("backward")
+    for n in names:
+        _native.profile_read(n)
     _native.profile_enable(True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -105,35 +203,52 @@ def gpu_bench(args):
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     _native.profile_enable(False)
-    fwd_ms, fwd_n = _native.profile_read("forward")
-    bwd_ms, bwd_n = _native.profile_read("backward")
+    timing = {n: _native.profile_read(n) for n in names}
     assert torch.isfinite(g).all()
 
     ms_step = (t1 - t0) * 1e3 / args.steps
-    traj = nP * B
-    kern = {
-        "forward": (fwd_ms / max(fwd_n, 1), FLOPS_FWD_STEP_2D * args.nstep * traj),
-        "backward": (bwd_ms / max(bwd_n, 1), FLOPS_BWD_STEP_2D * args.nstep * traj),
-    }
-    dom = max(kern, key=lambda k: kern[k][0])
-    dom_ms, dom_flops = kern[dom]
-    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
-    total_flops = (FLOPS_FWD_STEP_2D + FLOPS_BWD_STEP_2D) * args.nstep * traj
-    return {
-        "ms_per_step": ms_step,
-        "value": traj / (ms_step * 1e-3),
-        "kernels": {k: {"avg_ms": round(v[0], 5), "gflop": round(v[1] / 1e9, 4),
-                        "tflops": round(v[1] / (v[0] * 1e-3) / 1e12, 3)} for k, v in kern.items()},
-        "dominant": dom,
-        "roofline": {"bound": "valu", "kernel": dom, "achieved": round(achieved, 3),
-                     "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None},
-        "step_tflops": round(total_flops / (ms_step * 1e-3) / 1e12, 3),
-    }
+    nd, traj, T = info["ndim"], info["traj"], args.nstep
+    kern = {}
+    for n in ("forward", "backward"):
+        ms, cnt = timing[n]
+        if cnt == 0:
+            continue
+        per_step = cnt / args.steps
+        per_launch_traj = traj / per_step
+        f_step = FLOPS[nd][n]
+        flops = (FLOPS_1D_FWD if f_step is None else f_step * T) * per_launch_traj
+        kern[n] = {"avg_ms": ms / cnt, "work": flops, "unit": "TFLOP/s",
+                   "rate": flops / (ms / cnt * 1e-3) / 1e12, "per_step": per_step}
+    for n, nbytes in info.get("interp_bytes", {}).items():
+        ms, cnt = timing[n]
+        if cnt:
+            kern[n] = {"avg_ms": ms / cnt, "work": nbytes, "unit": "GB/s",
+                       "rate": nbytes / (ms / cnt * 1e-3) / 1e9, "per_step": cnt / args.steps}
+    # dominant kernel = largest share of the step's kernel time
+    dom = max(kern, key=lambda k: kern[k]["avg_ms"] * kern[k]["per_step"])
+    d = kern[dom]
+    peak = PEAK_HBM_GBS if d["unit"] == "GB/s" else PEAK_FP32_TFLOPS
+    roof = {"bound": "hbm" if d["unit"] == "GB/s" else "valu", "kernel": dom,
+            "achieved": round(d["rate"], 3), "peak": peak, "unit": d["unit"],
+            "frac": round(d["rate"] / peak, 4), "traffic": None}
+    pts_per_step = info.get("points_per_step", traj)
+    out = {"ms_per_step": ms_step, "value": pts_per_step / (ms_step * 1e-3), "roofline": roof,
+           "info": info,
+           "kernels": {k: {"avg_ms": round(v["avg_ms"], 5), "launches_per_step": v["per_step"],
+                           v["unit"]: round(v["rate"], 3)} for k, v in kern.items()}}
+    for n in ("interp_forward", "interp_backward"):
+        if n in kern:
+            out.setdefault("interp_roofline", {})[n] = {
+                "achieved_GBs": round(kern[n]["rate"], 1), "peak_GBs": PEAK_HBM_GBS,
+                "frac": round(kern[n]["rate"] / PEAK_HBM_GBS, 4),
+                "algorithmic_bytes": kern[n]["work"]}
+    total = sum(v["work"] * v["per_step"] for v in kern.values() if v["unit"] != "GB/s")
+    out["integrator_tflops_per_step"] = round(total / (ms_step * 1e-3) / 1e12, 3)
+    return out
 
 
 def cpu_baseline(args):
-    """Oracle (C, OpenMP) on a sample of the same workload: forward + MSE grad + backward."""
+    """Oracle (C, OpenMP) on a sample of the C2 workload: forward + MSE grad + backward."""
     import numpy as np
     cores = len(os.sched_getaffinity(0))
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))
@@ -143,25 +258,22 @@ def cpu_baseline(args):
 
     T = Cpab([20, 20])
     B = 16
-    pts_all, theta, theta_t = make_inputs(T, 125_000, B)
+    pts_all, theta, theta_t = make_c2_inputs(T)
     nstep = args.nstep
 
     def run(n):
         pts = pts_all[:, :n]
-        As = orc.affine(theta, T.params.basis).reshape(B, -1, 2, 3)
         At = orc.affine(theta_t, T.params.basis).reshape(B, -1, 2, 3)
         tgt = orc.forward_trels(pts, orc.expm(2, At, 1.0 / nstep), At, [20, 20], nstep)
         t0 = time.perf_counter()
         As = orc.affine(theta, T.params.basis).reshape(B, -1, 2, 3)
         out = orc.forward_trels(pts, orc.expm(2, As, 1.0 / nstep), As, [20, 20], nstep)
         g = (2.0 / out.size) * (out - tgt)
-        mom, gp = orc.backward(pts, As, g.astype(np.float32), [20, 20], nstep)
-        orc.project(mom.reshape(B, -1).astype(np.float32), T.params.basis)
+        orc.backward(pts, As, g.astype(np.float32), [20, 20], nstep)
         return time.perf_counter() - t0
 
     n = 2000
     dt = run(n)
-    # grow the sample to ~cpu_seconds of work (capped at the full 125k points)
     while dt < args.cpu_seconds / 4 and n < 125_000:
         n = min(125_000, int(n * min(8.0, max(2.0, args.cpu_seconds / 4 / max(dt, 1e-3)))))
         dt = run(n)
@@ -174,7 +286,38 @@ def cpu_baseline(args):
     per = tot / reps
     return {"value": round(n * B / per, 1), "unit": "points/s", "cores": cores, "kind": "port",
             "sample": f"{n} of the 125000 points x 16 thetas, fwd+MSE+grad, mean of "
-                      f"{reps} runs ({per:.3f} s each), OpenMP C restatement (oracle/)"}
+                      f"{reps} runs ({per:.3f} s each), C/OpenMP restatement of the reference "
+                      f"kernels (oracle/)"}
+
+
+def line_for(cfg, r, args, cpu):
+    info = r["info"]
+    line = {
+        "metric": METRIC if cfg == "c2" else f"points/sec (fwd+grad), {info['desc'].split(':')[0]}",
+        "value": round(r["value"], 1),
+        "unit": "points/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded inputs as in BASELINE.json configs)",
+        "config": {"workload": info["desc"], "global_batch": info["global_batch"],
+                   "points": info["points"], "parallelism": "single-gpu"},
+        "roofline": r["roofline"],
+        "cpu_baseline": cpu,
+        "kernels": r["kernels"],
+        "integrator_tflops_per_step": r["integrator_tflops_per_step"],
+    }
+    if "interp_roofline" in r:
+        line["interp_roofline"] = r["interp_roofline"]
+    if cfg == "c2":
+        line["pct_fp32_valu_peak_step"] = round(100 * r["integrator_tflops_per_step"]
+                                                / PEAK_FP32_TFLOPS, 2)
+    return line
 
 
 def main():
@@ -186,31 +329,11 @@ def main():
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
               "(the CPAB path has no multi-GPU component here)", file=sys.stderr)
         sys.exit(2)
-    r = gpu_bench(args)
-    cpu = None if args.no_cpu else cpu_baseline(args)
-    line = {
-        "metric": "points/sec (fwd+grad), 2D 20x20 tess, 125k pts, B=16; % fp32 VALU peak",
-        "value": round(r["value"], 1),
-        "unit": "points/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(r["ms_per_step"], 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded uniform points, N(0,1)*0.5 thetas)",
-        "config": {"workload": "C2: 2D CPAB transform_grid fwd+MSE+backward, tess [20,20], "
-                               "zero_boundary, 125000 uniform points, batch 16, nstepsolver 50",
-                   "global_batch": 16, "points": 125000, "parallelism": "single-gpu"},
-        "roofline": r["roofline"],
-        "cpu_baseline": cpu,
-        "kernels": r["kernels"],
-        "step_tflops": r["step_tflops"],
-        "pct_fp32_valu_peak_step": round(100 * r["step_tflops"] / PEAK_FP32_TFLOPS, 2),
-    }
-    print(json.dumps(line))
+    cfgs = ["c1", "c2", "c3", "c4", "c5"] if args.config == "all" else [args.config]
+    for cfg in cfgs:
+        r = gpu_bench(cfg, args)
+        cpu = None if (args.no_cpu or cfg != "c2") else cpu_baseline(args)
+        print(json.dumps(line_for(cfg, r, args, cpu)), flush=True)
 
 
 if __name__ == "__main__":

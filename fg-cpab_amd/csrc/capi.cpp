@@ -114,17 +114,20 @@ cpab::LaunchCfg forward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta
   const DeviceInfo dev = device_info();
   const int64_t table = (int64_t)g.nC * g.ppc() * 4;
   cpab::LaunchCfg c{};
-  c.lds_table = table <= dev.lds ? env_int("CPAB_FWD_LDS", 1) : 0;
-  int wg_per_cu = c.lds_table ? (int)std::min<int64_t>(8, std::max<int64_t>(1, dev.lds / std::max<int64_t>(table, 1))) : 4;
-  int block = 1024 / wg_per_cu;
-  block = std::max(256, std::min(1024, block / 64 * 64));
-  block = env_int("CPAB_FWD_BLOCK", block);
-  c.block = block;
-  const int64_t want = (int64_t)dev.cus * wg_per_cu * env_int("CPAB_FWD_WAVES", 1);
+  // The kernel keeps the current cell's map in registers and re-reads the
+  // table only when a lane changes cell, so the table is read through L1/L2 by
+  // default; staging it in LDS would cap occupancy for little gain.
+  c.lds_table = table <= dev.lds ? env_int("CPAB_FWD_LDS", 0) : 0;
+  c.block = env_int("CPAB_FWD_BLOCK", 512);
+  const int64_t resident = c.lds_table ? std::max<int64_t>(1, std::min<int64_t>(2048 / c.block, dev.lds / std::max<int64_t>(table, 1)))
+                                       : std::max(1, 2048 / c.block);
+  // Two rounds of resident workgroups per CU.
+  const int64_t want = (int64_t)dev.cus * resident * env_int("CPAB_FWD_WAVES", 2);
   int64_t chunks = std::max<int64_t>(1, div_up(want, std::max<int64_t>(n_theta, 1)));
-  chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, block)));
+  chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
   c.chunks = (int)env_int("CPAB_FWD_CHUNKS", (int)chunks);
   c.lds_bins = 0;
+  c.reg_steps = 0;
   return c;
 }
 
@@ -133,18 +136,19 @@ cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_thet
   const int64_t table = (int64_t)g.nC * g.ppc() * 4;
   cpab::LaunchCfg c{};
   c.lds_bins = (table <= dev.lds) ? env_int("CPAB_BWD_LDS_BINS", 1) : 0;
-  const int64_t used = c.lds_bins ? table : 0;
-  c.lds_table = (used + table <= dev.lds) ? env_int("CPAB_BWD_LDS_TABLE", 1) : 0;
-  const int64_t lds = table * (c.lds_bins + c.lds_table);
-  // Register variant: whole trajectory in VGPRs (~160 per lane -> 3 waves per
-  // SIMD), so one 768-thread workgroup (12 waves) per CU.
+  // Register variant: whole trajectory in VGPRs (~168 per lane -> 3 waves per
+  // SIMD = 12 waves per CU), one 768-thread workgroup per CU; the per-cell
+  // table is read through L1/L2 (re-read only when a lane changes cell).
   const bool reg = g.ndim <= 2 && T == cpab::kRegSteps && c.lds_bins && g.nC <= 65535 &&
                    env_int("CPAB_BWD_REG", 1);
   c.reg_steps = reg ? cpab::kRegSteps : 0;
+  const int64_t used = c.lds_bins ? table : 0;
+  c.lds_table = (used + table <= dev.lds) ? env_int("CPAB_BWD_LDS_TABLE", reg ? 0 : 1) : 0;
+  const int64_t lds = table * (c.lds_bins + c.lds_table);
   int wg_per_cu;
   if (reg) {
-    c.block = 768;
-    wg_per_cu = 1;
+    c.block = env_int("CPAB_BWD_BLOCK", 768);
+    wg_per_cu = std::max(1, 768 / c.block);
   } else {
     c.block = env_int("CPAB_BWD_BLOCK", 512);
     wg_per_cu = std::max(1, 2048 / c.block);  // 32 waves per CU
@@ -226,9 +230,13 @@ int cpab_forward_1d_closed_form(int64_t nP, int64_t n_theta, int batched, int nc
   if ((rc = check_points(nP, n_theta, 1))) return rc;
   if (nP == 0 || n_theta == 0) return CPAB_OK;
   CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(out);
-  return check_hip(cpab::launch_forward_1d(g, nP, n_theta, batched ? 1 : 0, points, As, out,
-                                           as_stream(stream)),
-                   "cpab_forward_1d_closed_form");
+  hipEvent_t ev;
+  const bool timed = prof_begin(as_stream(stream), &ev);
+  rc = check_hip(cpab::launch_forward_1d(g, nP, n_theta, batched ? 1 : 0, points, As, out,
+                                         as_stream(stream)),
+                 "cpab_forward_1d_closed_form");
+  prof_end(timed, ev, "forward", as_stream(stream));
+  return rc;
 }
 
 int cpab_forward(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver, int ncx,
@@ -383,6 +391,11 @@ static int check_interp(int ndim, int64_t B, int64_t C, const int64_t* in_size,
     n *= out_size[k];
   }
   if (B * n * (C > 0 ? C : 1) >= (1LL << 40)) return fail(CPAB_ERR_INVALID, "problem too large");
+  int64_t plane = 1;
+  for (int k = 0; k < ndim; ++k) plane *= in_size[k];
+  if (plane >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "one data channel must hold < 2^31 values");
+  if (ndim >= 2 && (out_size[ndim - 1] + 63) / 64 >= 65536)
+    return fail(CPAB_ERR_INVALID, "last output size exceeds the grid limit");
   if (ndim >= 2 && B * (ndim == 3 ? out_size[1] : 1) >= 65536)
     return fail(CPAB_ERR_INVALID, "n_batch * mid size exceeds the grid limit");
   return CPAB_OK;
@@ -394,9 +407,13 @@ int cpab_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
   int rc = check_interp(ndim, B, C, in_size, out_size);
   if (rc) return rc;
   CPAB_REQUIRE(data); CPAB_REQUIRE(grid); CPAB_REQUIRE(out);
-  return check_hip(cpab::launch_interp_forward(ndim, B, C, in_size, out_size, data, grid, out,
-                                               as_stream(stream)),
-                   "cpab_interp_forward");
+  hipEvent_t ev;
+  const bool timed = prof_begin(as_stream(stream), &ev);
+  rc = check_hip(cpab::launch_interp_forward(ndim, B, C, in_size, out_size, data, grid, out,
+                                             as_stream(stream)),
+                 "cpab_interp_forward");
+  prof_end(timed, ev, "interp_forward", as_stream(stream));
+  return rc;
 }
 
 int cpab_interp_backward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
@@ -406,9 +423,13 @@ int cpab_interp_backward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
   int rc = check_interp(ndim, B, C, in_size, out_size);
   if (rc) return rc;
   CPAB_REQUIRE(data); CPAB_REQUIRE(grid); CPAB_REQUIRE(grad_out);
-  return check_hip(cpab::launch_interp_backward(ndim, B, C, in_size, out_size, data, grid,
-                                                grad_out, grad_grid, grad_data, as_stream(stream)),
-                   "cpab_interp_backward");
+  hipEvent_t ev;
+  const bool timed = prof_begin(as_stream(stream), &ev);
+  rc = check_hip(cpab::launch_interp_backward(ndim, B, C, in_size, out_size, data, grid,
+                                              grad_out, grad_grid, grad_data, as_stream(stream)),
+                 "cpab_interp_backward");
+  prof_end(timed, ev, "interp_backward", as_stream(stream));
+  return rc;
 }
 
 }  // extern "C"

@@ -7,7 +7,7 @@
 // with coordinate 0 fastest, p = i0 + o0*(i1 + o1*i2); the output is
 // [B, C, o0, o1(, o2)] with the LAST axis fastest.  So the point order and the
 // output order are transposes of each other.  HBM-bound, so each workgroup
-// takes a 64 x 64 tile over (i0, i_last) at fixed i_mid, reads the grid rows
+// takes a 32 x 64 tile over (i0, i_last) at fixed i_mid, reads the grid rows
 // coalesced along i0 into LDS, and computes/writes with i_last across the
 // lanes (coalesced output and, for smooth warps, near-contiguous data rows).
 // The backward does the same transpose in the other direction for grad_grid.
@@ -22,8 +22,10 @@
 namespace cpab {
 namespace {
 
-constexpr int kTile = 64;
+constexpr int kT0 = 32;      // tile extent along i0 (grid rows are contiguous in i0)
+constexpr int kTL = 64;      // tile extent along i_last (output rows are contiguous in i_last)
 constexpr int kThreads = 256;
+constexpr int kUnroll = 4;   // outputs in flight per lane in the compute loop
 
 struct Axis {
   int i0, i1;   // clamped corner indices
@@ -52,24 +54,25 @@ struct Shape {
   int in[3];     // data spatial sizes
   int o0, omid, olast;
   int64_t nP;
+  int vec4;      // grid rows are 16-byte aligned along i0 (o0 % 4 == 0)
 };
 
-__device__ __forceinline__ int64_t data_index(const Shape& s, int64_t bc, int x, int y, int z) {
-  if (s.ndim == 2) return (bc * s.in[0] + x) * (int64_t)s.in[1] + y;
-  return ((bc * s.in[0] + x) * (int64_t)s.in[1] + y) * (int64_t)s.in[2] + z;
+// Offset of (x, y, z) inside one [*in] plane (< 2^31, checked by the caller).
+template <int ND>
+__device__ __forceinline__ int plane_index(const Shape& s, int x, int y, int z) {
+  if (ND == 2) return x * s.in[1] + y;
+  return (x * s.in[1] + y) * s.in[2] + z;
 }
 
-// Sample data[b, ch] at the three axis weights (z unused in 2D).
-__device__ __forceinline__ float sample(const Shape& s, const float* __restrict__ data, int64_t bc,
+template <int ND>
+__device__ __forceinline__ float sample(const Shape& s, const float* __restrict__ d,
                                         const Axis& ax, const Axis& ay, const Axis& az) {
-  if (s.ndim == 2) {
-    const float c00 = data[data_index(s, bc, ax.i0, ay.i0, 0)];
-    const float c01 = data[data_index(s, bc, ax.i0, ay.i1, 0)];
-    const float c10 = data[data_index(s, bc, ax.i1, ay.i0, 0)];
-    const float c11 = data[data_index(s, bc, ax.i1, ay.i1, 0)];
-    const float c0 = lerp_ref(c00, c10, ax.t);
-    const float c1 = lerp_ref(c01, c11, ax.t);
-    return lerp_ref(c0, c1, ay.t);
+  if (ND == 2) {
+    const float c00 = d[plane_index<2>(s, ax.i0, ay.i0, 0)];
+    const float c01 = d[plane_index<2>(s, ax.i0, ay.i1, 0)];
+    const float c10 = d[plane_index<2>(s, ax.i1, ay.i0, 0)];
+    const float c11 = d[plane_index<2>(s, ax.i1, ay.i1, 0)];
+    return lerp_ref(lerp_ref(c00, c10, ax.t), lerp_ref(c01, c11, ax.t), ay.t);
   }
   float c[2][2][2];
 #pragma unroll
@@ -77,53 +80,50 @@ __device__ __forceinline__ float sample(const Shape& s, const float* __restrict_
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int d = 0; d < 2; ++d)
-        c[a][b][d] = data[data_index(s, bc, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0,
-                                     d ? az.i1 : az.i0)];
+      for (int e = 0; e < 2; ++e)
+        c[a][b][e] = d[plane_index<3>(s, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, e ? az.i1 : az.i0)];
   const float c00 = lerp_ref(c[0][0][0], c[1][0][0], ax.t);
   const float c01 = lerp_ref(c[0][0][1], c[1][0][1], ax.t);
   const float c10 = lerp_ref(c[0][1][0], c[1][1][0], ax.t);
   const float c11 = lerp_ref(c[0][1][1], c[1][1][1], ax.t);
-  const float c0 = lerp_ref(c00, c10, ay.t);
-  const float c1 = lerp_ref(c01, c11, ay.t);
-  return lerp_ref(c0, c1, az.t);
+  return lerp_ref(lerp_ref(c00, c10, ay.t), lerp_ref(c01, c11, ay.t), az.t);
 }
 
-// d out / d (x, y, z) for one channel with upstream gradient g, before the
-// (size-1) chain factor; and the 4 / 8 corner weights for grad_data.
-__device__ __forceinline__ void sample_grad(const Shape& s, const float* __restrict__ data,
-                                            int64_t bc, const Axis& ax, const Axis& ay,
-                                            const Axis& az, float g, float* dxyz,
-                                            float* __restrict__ grad_data) {
+// d out / d (x, y, z) for one channel with upstream gradient g (before the
+// (size-1) chain factor), and the corner scatter for grad_data.
+template <int ND>
+__device__ __forceinline__ void sample_grad(const Shape& s, const float* __restrict__ d,
+                                            const Axis& ax, const Axis& ay, const Axis& az,
+                                            float g, float* dxyz, float* __restrict__ gd) {
   const float ux = 1.0f - ax.t, uy = 1.0f - ay.t, uz = 1.0f - az.t;
-  if (s.ndim == 2) {
-    const int64_t i00 = data_index(s, bc, ax.i0, ay.i0, 0), i01 = data_index(s, bc, ax.i0, ay.i1, 0);
-    const int64_t i10 = data_index(s, bc, ax.i1, ay.i0, 0), i11 = data_index(s, bc, ax.i1, ay.i1, 0);
+  if (ND == 2) {
+    const int i00 = plane_index<2>(s, ax.i0, ay.i0, 0), i01 = plane_index<2>(s, ax.i0, ay.i1, 0);
+    const int i10 = plane_index<2>(s, ax.i1, ay.i0, 0), i11 = plane_index<2>(s, ax.i1, ay.i1, 0);
     if (dxyz) {
-      const float c00 = data[i00], c01 = data[i01], c10 = data[i10], c11 = data[i11];
+      const float c00 = d[i00], c01 = d[i01], c10 = d[i10], c11 = d[i11];
       const float c0 = lerp_ref(c00, c10, ax.t), c1 = lerp_ref(c01, c11, ax.t);
       dxyz[0] += g * uy * (c10 - c00) + g * ay.t * (c11 - c01);
       dxyz[1] += g * (c1 - c0);
     }
-    if (grad_data) {
+    if (gd) {
       const float g0 = g * uy, g1 = g * ay.t;
-      unsafeAtomicAdd(grad_data + i00, g0 * ux);
-      unsafeAtomicAdd(grad_data + i10, g0 * ax.t);
-      unsafeAtomicAdd(grad_data + i01, g1 * ux);
-      unsafeAtomicAdd(grad_data + i11, g1 * ax.t);
+      unsafeAtomicAdd(gd + i00, g0 * ux);
+      unsafeAtomicAdd(gd + i10, g0 * ax.t);
+      unsafeAtomicAdd(gd + i01, g1 * ux);
+      unsafeAtomicAdd(gd + i11, g1 * ax.t);
     }
     return;
   }
-  int64_t idx[2][2][2];
+  int idx[2][2][2];
   float c[2][2][2];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int d = 0; d < 2; ++d) {
-        idx[a][b][d] = data_index(s, bc, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, d ? az.i1 : az.i0);
-        c[a][b][d] = dxyz ? data[idx[a][b][d]] : 0.0f;
+      for (int e = 0; e < 2; ++e) {
+        idx[a][b][e] = plane_index<3>(s, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, e ? az.i1 : az.i0);
+        c[a][b][e] = dxyz ? d[idx[a][b][e]] : 0.0f;
       }
   if (dxyz) {
     // Along x: the four (y, z) lines; along y: the two z planes; along z: the two halves.
@@ -132,7 +132,7 @@ __device__ __forceinline__ void sample_grad(const Shape& s, const float* __restr
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int d = 0; d < 2; ++d) gx += wyz[b][d] * (c[1][b][d] - c[0][b][d]);
+      for (int e = 0; e < 2; ++e) gx += wyz[b][e] * (c[1][b][e] - c[0][b][e]);
     const float c00 = lerp_ref(c[0][0][0], c[1][0][0], ax.t);
     const float c01 = lerp_ref(c[0][0][1], c[1][0][1], ax.t);
     const float c10 = lerp_ref(c[0][1][0], c[1][1][0], ax.t);
@@ -143,15 +143,15 @@ __device__ __forceinline__ void sample_grad(const Shape& s, const float* __restr
     dxyz[1] += g * gy;
     dxyz[2] += g * gz;
   }
-  if (grad_data) {
+  if (gd) {
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int d = 0; d < 2; ++d) {
-          const float w = (a ? ax.t : ux) * (b ? ay.t : uy) * (d ? az.t : uz);
-          unsafeAtomicAdd(grad_data + idx[a][b][d], g * w);
+        for (int e = 0; e < 2; ++e) {
+          const float w = (a ? ax.t : ux) * (b ? ay.t : uy) * (e ? az.t : uz);
+          unsafeAtomicAdd(gd + idx[a][b][e], g * w);
         }
   }
 }
@@ -161,93 +161,141 @@ __device__ __forceinline__ void sample_grad(const Shape& s, const float* __restr
 __device__ __forceinline__ void tile_origin(const Shape& s, int& b, int& im, int& t0, int& tl) {
   b = blockIdx.z / s.omid;
   im = blockIdx.z - b * s.omid;
-  t0 = blockIdx.x * kTile;
-  tl = blockIdx.y * kTile;
+  t0 = blockIdx.x * kT0;
+  tl = blockIdx.y * kTL;
 }
 
-__device__ __forceinline__ int64_t point_of(const Shape& s, int i0, int im, int il) {
-  return i0 + (int64_t)s.o0 * (im + (int64_t)s.omid * il);
+// Grid rows of this tile -> LDS crd[k][al][a0] (lanes along i0, float4 when aligned).
+template <int ND>
+__device__ __forceinline__ void load_tile(const Shape& s, const float* __restrict__ grid, int b,
+                                          int im, int t0, int tl, int n0, int nl,
+                                          float (*crd)[kTL][kT0 + 1]) {
+  const int64_t row0 = (int64_t)s.o0 * (im + (int64_t)s.omid * tl) + t0;  // point of (t0, tl)
+  const int64_t rstride = (int64_t)s.o0 * s.omid;                        // next i_last
+  if (s.vec4 && n0 == kT0) {
+    constexpr int Q = kT0 / 4;
+    for (int e = threadIdx.x; e < Q * kTL; e += kThreads) {
+      const int q = e % Q, al = e / Q;
+      if (al < nl) {
+#pragma unroll
+        for (int k = 0; k < ND; ++k) {
+          const float4 v = *reinterpret_cast<const float4*>(
+              grid + ((int64_t)b * ND + k) * s.nP + row0 + al * rstride + 4 * q);
+          crd[k][al][4 * q] = v.x;
+          crd[k][al][4 * q + 1] = v.y;
+          crd[k][al][4 * q + 2] = v.z;
+          crd[k][al][4 * q + 3] = v.w;
+        }
+      }
+    }
+  } else {
+    for (int e = threadIdx.x; e < kT0 * kTL; e += kThreads) {
+      const int a0 = e % kT0, al = e / kT0;
+      if (a0 < n0 && al < nl) {
+#pragma unroll
+        for (int k = 0; k < ND; ++k)
+          crd[k][al][a0] = grid[((int64_t)b * ND + k) * s.nP + row0 + al * rstride + a0];
+      }
+    }
+  }
 }
 
+template <int ND>
 __global__ __launch_bounds__(kThreads) void interp_fwd_kernel(Shape s,
                                                               const float* __restrict__ data,
                                                               const float* __restrict__ grid,
                                                               float* __restrict__ out) {
-  __shared__ float crd[3][kTile][kTile + 1];  // [axis][i_last][i0]
+  __shared__ float crd[ND][kTL][kT0 + 1];
   int b, im, t0, tl;
   tile_origin(s, b, im, t0, tl);
-  const int n0 = min(kTile, s.o0 - t0), nl = min(kTile, s.olast - tl);
-  // Load: lanes along i0 (contiguous in the grid rows).
-  for (int e = threadIdx.x; e < kTile * kTile; e += kThreads) {
-    const int a0 = e % kTile, al = e / kTile;
-    if (a0 < n0 && al < nl) {
-      const int64_t p = point_of(s, t0 + a0, im, tl + al);
-      for (int k = 0; k < s.ndim; ++k) crd[k][al][a0] = grid[((int64_t)b * s.ndim + k) * s.nP + p];
-    }
-  }
+  const int n0 = min(kT0, s.o0 - t0), nl = min(kTL, s.olast - tl);
+  load_tile<ND>(s, grid, b, im, t0, tl, n0, nl, crd);
   __syncthreads();
-  // Compute: lanes along i_last (contiguous in the output rows).
-  for (int e = threadIdx.x; e < kTile * kTile; e += kThreads) {
-    const int al = e % kTile, a0 = e / kTile;
-    if (a0 >= n0 || al >= nl) continue;
-    const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
-    const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
-    const Axis az = (s.ndim == 3) ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
-    const int64_t o = ((int64_t)(t0 + a0) * s.omid + im) * s.olast + tl + al;
-    const int64_t plane = (int64_t)s.o0 * s.omid * s.olast;
-    for (int ch = 0; ch < s.C; ++ch) {
-      const int64_t bc = (int64_t)b * s.C + ch;
-      out[bc * plane + o] = sample(s, data, bc, ax, ay, az);
+  const int al = threadIdx.x % kTL;   // lanes along i_last
+  const int w = threadIdx.x / kTL;    // kThreads / kTL rows at a time
+  const int64_t plane_in = (int64_t)s.in[0] * s.in[1] * (ND == 3 ? s.in[2] : 1);
+  const int64_t plane_out = (int64_t)s.o0 * s.omid * s.olast;
+  if (al >= nl) return;
+  for (int ch = 0; ch < s.C; ++ch) {
+    const int64_t bc = (int64_t)b * s.C + ch;
+    const float* __restrict__ d = data + bc * plane_in;
+    float* __restrict__ o = out + bc * plane_out + (int64_t)im * s.olast + tl + al;
+#pragma unroll kUnroll
+    for (int a0 = w; a0 < n0; a0 += kThreads / kTL) {
+      const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
+      const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
+      const Axis az = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
+      o[(int64_t)(t0 + a0) * s.omid * s.olast] = sample<ND>(s, d, ax, ay, az);
     }
   }
 }
 
+template <int ND>
 __global__ __launch_bounds__(kThreads) void interp_bwd_kernel(Shape s,
                                                               const float* __restrict__ data,
                                                               const float* __restrict__ grid,
                                                               const float* __restrict__ grad_out,
                                                               float* __restrict__ grad_grid,
                                                               float* __restrict__ grad_data) {
-  __shared__ float crd[3][kTile][kTile + 1];
+  __shared__ float crd[ND][kTL][kT0 + 1];
   int b, im, t0, tl;
   tile_origin(s, b, im, t0, tl);
-  const int n0 = min(kTile, s.o0 - t0), nl = min(kTile, s.olast - tl);
-  for (int e = threadIdx.x; e < kTile * kTile; e += kThreads) {
-    const int a0 = e % kTile, al = e / kTile;
-    if (a0 < n0 && al < nl) {
-      const int64_t p = point_of(s, t0 + a0, im, tl + al);
-      for (int k = 0; k < s.ndim; ++k) crd[k][al][a0] = grid[((int64_t)b * s.ndim + k) * s.nP + p];
-    }
-  }
+  const int n0 = min(kT0, s.o0 - t0), nl = min(kTL, s.olast - tl);
+  load_tile<ND>(s, grid, b, im, t0, tl, n0, nl, crd);
   __syncthreads();
-  for (int e = threadIdx.x; e < kTile * kTile; e += kThreads) {
-    const int al = e % kTile, a0 = e / kTile;
-    if (a0 >= n0 || al >= nl) continue;
-    const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
-    const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
-    const Axis az = (s.ndim == 3) ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
-    const int64_t o = ((int64_t)(t0 + a0) * s.omid + im) * s.olast + tl + al;
-    const int64_t plane = (int64_t)s.o0 * s.omid * s.olast;
-    float d[3] = {0.0f, 0.0f, 0.0f};
-    for (int ch = 0; ch < s.C; ++ch) {
-      const int64_t bc = (int64_t)b * s.C + ch;
-      sample_grad(s, data, bc, ax, ay, az, grad_out[bc * plane + o], grad_grid ? d : nullptr,
-                  grad_data);
-    }
-    if (grad_grid) {
-      // Chain factor of x = g*(size-1); the result goes back through LDS
-      // (same slot: each thread reads and writes only its own element).
-      for (int k = 0; k < s.ndim; ++k) crd[k][al][a0] = d[k] * (float)(s.in[k] - 1);
+  const int al = threadIdx.x % kTL;
+  const int w = threadIdx.x / kTL;
+  const int64_t plane_in = (int64_t)s.in[0] * s.in[1] * (ND == 3 ? s.in[2] : 1);
+  const int64_t plane_out = (int64_t)s.o0 * s.omid * s.olast;
+  if (al < nl) {
+#pragma unroll kUnroll
+    for (int a0 = w; a0 < n0; a0 += kThreads / kTL) {
+      const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
+      const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
+      const Axis az = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
+      const int64_t o = ((int64_t)(t0 + a0) * s.omid + im) * s.olast + tl + al;
+      float dd[3] = {0.0f, 0.0f, 0.0f};
+      for (int ch = 0; ch < s.C; ++ch) {
+        const int64_t bc = (int64_t)b * s.C + ch;
+        sample_grad<ND>(s, data + bc * plane_in, ax, ay, az, grad_out[bc * plane_out + o],
+                        grad_grid ? dd : nullptr, grad_data ? grad_data + bc * plane_in : nullptr);
+      }
+      if (grad_grid) {
+        // (size-1) chain factor of x = g*(size-1); each thread rewrites only
+        // the LDS slots it read.
+#pragma unroll
+        for (int k = 0; k < ND; ++k) crd[k][al][a0] = dd[k] * (float)(s.in[k] - 1);
+      }
     }
   }
   if (!grad_grid) return;
   __syncthreads();
-  for (int e = threadIdx.x; e < kTile * kTile; e += kThreads) {
-    const int a0 = e % kTile, al = e / kTile;
-    if (a0 < n0 && al < nl) {
-      const int64_t p = point_of(s, t0 + a0, im, tl + al);
-      for (int k = 0; k < s.ndim; ++k)
-        grad_grid[((int64_t)b * s.ndim + k) * s.nP + p] = crd[k][al][a0];
+  const int64_t row0 = (int64_t)s.o0 * (im + (int64_t)s.omid * tl) + t0;
+  const int64_t rstride = (int64_t)s.o0 * s.omid;
+  if (s.vec4 && n0 == kT0) {
+    constexpr int Q = kT0 / 4;
+    for (int e = threadIdx.x; e < Q * kTL; e += kThreads) {
+      const int q = e % Q, l = e / Q;
+      if (l < nl) {
+#pragma unroll
+        for (int k = 0; k < ND; ++k) {
+          float4 v;
+          v.x = crd[k][l][4 * q];
+          v.y = crd[k][l][4 * q + 1];
+          v.z = crd[k][l][4 * q + 2];
+          v.w = crd[k][l][4 * q + 3];
+          *reinterpret_cast<float4*>(grad_grid + ((int64_t)b * ND + k) * s.nP + row0 + l * rstride + 4 * q) = v;
+        }
+      }
+    }
+  } else {
+    for (int e = threadIdx.x; e < kT0 * kTL; e += kThreads) {
+      const int a0 = e % kT0, l = e / kT0;
+      if (a0 < n0 && l < nl) {
+#pragma unroll
+        for (int k = 0; k < ND; ++k)
+          grad_grid[((int64_t)b * ND + k) * s.nP + row0 + l * rstride + a0] = crd[k][l][a0];
+      }
     }
   }
 }
@@ -295,6 +343,7 @@ __global__ __launch_bounds__(kThreads) void interp1d_bwd_kernel(int B, int C, in
 
 Shape make_shape(int ndim, int64_t B, int64_t C, const int64_t* in_size, const int64_t* out_size) {
   Shape s{};
+  s.vec4 = 0;
   s.ndim = ndim;
   s.B = (int)B;
   s.C = (int)C;
@@ -304,11 +353,14 @@ Shape make_shape(int ndim, int64_t B, int64_t C, const int64_t* in_size, const i
   s.olast = (int)out_size[ndim - 1];
   s.nP = 1;
   for (int k = 0; k < ndim; ++k) s.nP *= out_size[k];
+  s.vec4 = (s.o0 % 4) == 0;
   return s;
 }
 
+int aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 dim3 tile_grid(const Shape& s) {
-  return dim3((unsigned)((s.o0 + kTile - 1) / kTile), (unsigned)((s.olast + kTile - 1) / kTile),
+  return dim3((unsigned)((s.o0 + kT0 - 1) / kT0), (unsigned)((s.olast + kTL - 1) / kTL),
               (unsigned)(s.B * s.omid));
 }
 
@@ -317,7 +369,8 @@ dim3 tile_grid(const Shape& s) {
 hipError_t launch_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
                                  const int64_t* out_size, const float* data, const float* grid,
                                  float* out, hipStream_t st) {
-  const Shape s = make_shape(ndim, B, C, in_size, out_size);
+  Shape s = make_shape(ndim, B, C, in_size, out_size);
+  s.vec4 &= aligned16(grid);
   if (s.nP <= 0 || B <= 0) return hipSuccess;
   if (ndim == 1) {
     int64_t g = (B * s.nP + kThreads - 1) / kThreads;
@@ -325,7 +378,10 @@ hipError_t launch_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* 
     hipLaunchKernelGGL(interp1d_fwd_kernel, dim3((unsigned)g), dim3(kThreads), 0, st, s.B, s.C,
                        s.in[0], s.nP, data, grid, out);
   } else {
-    hipLaunchKernelGGL(interp_fwd_kernel, tile_grid(s), dim3(kThreads), 0, st, s, data, grid, out);
+    if (ndim == 2)
+      hipLaunchKernelGGL(interp_fwd_kernel<2>, tile_grid(s), dim3(kThreads), 0, st, s, data, grid, out);
+    else
+      hipLaunchKernelGGL(interp_fwd_kernel<3>, tile_grid(s), dim3(kThreads), 0, st, s, data, grid, out);
   }
   return hipGetLastError();
 }
@@ -334,7 +390,8 @@ hipError_t launch_interp_backward(int ndim, int64_t B, int64_t C, const int64_t*
                                   const int64_t* out_size, const float* data, const float* grid,
                                   const float* grad_out, float* grad_grid, float* grad_data,
                                   hipStream_t st) {
-  const Shape s = make_shape(ndim, B, C, in_size, out_size);
+  Shape s = make_shape(ndim, B, C, in_size, out_size);
+  s.vec4 &= aligned16(grid) & (grad_grid == nullptr || aligned16(grad_grid));
   if (grad_data) {
     int64_t n = B * C;
     for (int k = 0; k < ndim; ++k) n *= in_size[k];
@@ -348,8 +405,12 @@ hipError_t launch_interp_backward(int ndim, int64_t B, int64_t C, const int64_t*
     hipLaunchKernelGGL(interp1d_bwd_kernel, dim3((unsigned)g), dim3(kThreads), 0, st, s.B, s.C,
                        s.in[0], s.nP, data, grid, grad_out, grad_grid, grad_data);
   } else {
-    hipLaunchKernelGGL(interp_bwd_kernel, tile_grid(s), dim3(kThreads), 0, st, s, data, grid,
-                       grad_out, grad_grid, grad_data);
+    if (ndim == 2)
+      hipLaunchKernelGGL(interp_bwd_kernel<2>, tile_grid(s), dim3(kThreads), 0, st, s, data, grid,
+                         grad_out, grad_grid, grad_data);
+    else
+      hipLaunchKernelGGL(interp_bwd_kernel<3>, tile_grid(s), dim3(kThreads), 0, st, s, data, grid,
+                         grad_out, grad_grid, grad_data);
   }
   return hipGetLastError();
 }

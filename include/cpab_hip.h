@@ -120,8 +120,9 @@ int cpab_interp_backward(int ndim, int64_t n_batch, int64_t n_channels, const in
 /* Kernel timing for benchmarks (no reference counterpart; the reference timed
  * with torch.cuda.synchronize + perf_counter, benchmarks/benchmark_transformer.py:76-84).
  * While enabled, HIP events are recorded on the launch stream around the
- * integrator kernels ("forward": the fixed-step forward kernel; "backward": the
- * fused replay/adjoint kernel).  cpab_profile_read waits for and sums the
+ * hot kernels ("forward": the forward integrator, fixed-step or 1D closed form;
+ * "backward": the fused replay/adjoint kernel; "interp_forward" /
+ * "interp_backward": the resampling kernels).  cpab_profile_read waits for and sums the
  * recorded launches of one kernel and forgets them. */
 void cpab_profile_enable(int on);
 int cpab_profile_read(const char* kernel, double* total_ms, int64_t* launches);

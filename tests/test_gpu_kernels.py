@@ -182,7 +182,8 @@ def test_project_bitexact(cuda, tess):
 
 
 @pytest.mark.parametrize("nd,ins,outs", [(2, (40, 56), (48, 36)), (3, (12, 10, 14), (9, 11, 13)),
-                                         (1, (77,), (50,)), (2, (512, 512), (130, 70))])
+                                         (1, (77,), (50,)), (2, (512, 512), (130, 70)),
+                                         (2, (64, 80), (96, 130)), (3, (12, 10, 14), (32, 3, 66))])
 def test_interp_parity(cuda, nd, ins, outs):
     rng = np.random.default_rng(30 + nd)
     B, C = 2, 3
@@ -207,3 +208,25 @@ def test_interp_parity(cuda, nd, ins, outs):
     _, mag = orc.interp_backward(nd, data, grid, outs, np.abs(gout), dtype=np.float64)
     err = np.abs(gd.cpu().numpy().astype(np.float64) - rd)
     assert (err <= 1e-4 * mag + 1e-12).all(), float((err / (mag + 1e-30)).max())
+
+
+def test_interp_unaligned_grid(cuda):
+    # A grid view that starts 4 bytes into its buffer cannot take the 16-byte
+    # vector path; results must not change.
+    rng = np.random.default_rng(7)
+    outs = (64, 64)
+    nP = 64 * 64
+    data = rng.random((1, 2, 33, 47)).astype(np.float32)
+    grid = (rng.random((1, 2, nP)) * 1.2 - 0.1).astype(np.float32)
+    buf = torch.empty(1 + grid.size, device=cuda)
+    view = buf[1:].view(1, 2, nP)
+    view.copy_(torch.from_numpy(grid))
+    out = torch.empty((1, 2, *outs), device=cuda)
+    native().interp_forward(2, _dev(data, cuda), view, outs, out)
+    np.testing.assert_array_equal(out.cpu().numpy(), orc.interp_forward(2, data, grid, outs))
+    gout = rng.standard_normal((1, 2, *outs)).astype(np.float32)
+    gbuf = torch.empty(1 + grid.size, device=cuda)
+    gg = gbuf[1:].view(1, 2, nP)
+    native().interp_backward(2, _dev(data, cuda), view, outs, _dev(gout, cuda), gg, None)
+    rg, _ = orc.interp_backward(2, data, grid, outs, gout)
+    np.testing.assert_array_equal(gg.cpu().numpy(), rg)
