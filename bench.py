@@ -58,7 +58,9 @@ def parse():
 
 
 def calibrate_copy(mib):
-    """Plain copy kernel of known size: reads and writes mib MiB per launch."""
+    """Plain copies of known size for scaling the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    counters: a runtime device-to-device copy and an elementwise kernel (x * 1),
+    each reading and writing ``mib`` MiB per launch, 3 launches each."""
     import torch
     n = mib * (1 << 20) // 4
     src = torch.rand(n, device="cuda:0")
@@ -66,8 +68,11 @@ def calibrate_copy(mib):
     torch.cuda.synchronize()
     for _ in range(3):
         dst.copy_(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
     torch.cuda.synchronize()
-    print(json.dumps({"copy_bytes_per_launch": n * 4, "launches": 3}))
+    print(json.dumps({"copy_bytes_per_launch": n * 4, "launches": 3,
+                      "kernels": ["device copy", "elementwise mul"]}))
 
 
 def _theta(T, n, scale, seed):
@@ -230,7 +235,7 @@ def gpu_bench(cfg, args):
     peak = PEAK_HBM_GBS if d["unit"] == "GB/s" else PEAK_FP32_TFLOPS
     roof = {"bound": "hbm" if d["unit"] == "GB/s" else "valu", "kernel": dom,
             "achieved": round(d["rate"], 3), "peak": peak, "unit": d["unit"],
-            "frac": round(d["rate"] / peak, 4), "traffic": None}
+            "frac": round(d["rate"] / peak, 4), "traffic": profiled_traffic(cfg, dom)}
     pts_per_step = info.get("points_per_step", traj)
     out = {"ms_per_step": ms_step, "value": pts_per_step / (ms_step * 1e-3), "roofline": roof,
            "info": info,
@@ -241,10 +246,31 @@ def gpu_bench(cfg, args):
             out.setdefault("interp_roofline", {})[n] = {
                 "achieved_GBs": round(kern[n]["rate"], 1), "peak_GBs": PEAK_HBM_GBS,
                 "frac": round(kern[n]["rate"] / PEAK_HBM_GBS, 4),
-                "algorithmic_bytes": kern[n]["work"]}
+                "algorithmic_bytes": kern[n]["work"], "traffic": profiled_traffic(cfg, n)}
     total = sum(v["work"] * v["per_step"] for v in kern.values() if v["unit"] != "GB/s")
     out["integrator_tflops_per_step"] = round(total / (ms_step * 1e-3) / 1e12, 3)
     return out
+
+
+KERNEL_PREFIX = {"forward": ("fwd2d_kernel", "fwd3d_kernel", "fwd1d_closed_kernel"),
+                 "backward": ("backward_kernel",),
+                 "interp_forward": ("interp_fwd_kernel", "interp1d_fwd_kernel"),
+                 "interp_backward": ("interp_bwd_kernel", "interp1d_bwd_kernel")}
+
+
+def profiled_traffic(cfg, kernel):
+    """HBM bytes per launch of ``kernel`` for ``cfg`` as measured by the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (profiles/traffic.json, each counter
+    scaled by its plain-copy factor), or None when no such measurement exists."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for name, v in t.get("configs", {}).get(cfg, {}).items():
+        if name.startswith(KERNEL_PREFIX.get(kernel, ())):
+            return v["bytes"]
+    return None
 
 
 def cpu_baseline(args):
