@@ -1,10 +1,12 @@
 import os
+import pathlib
 import sys
 
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.realpath(__file__)))
 PKG = os.path.join(ROOT, "fg-cpab_amd")
+GOLDEN = pathlib.Path(ROOT) / "tests" / "golden"
 for p in (PKG, ROOT):
     if p not in sys.path:
         sys.path.insert(0, p)
