@@ -14,14 +14,22 @@
 // of the current cell, flushing it whenever the cell changes, exactly as the
 // reference groups its flushes.
 //
-// Moment accumulation on MI355X: each workgroup serves ONE theta, and when the
-// nC x ppc table fits it keeps a private copy of that theta's moments in LDS
-// (ds_add_f32, no HBM atomics).  At the end the workgroup writes its table as
-// one partial (plain coalesced stores); a separate pass sums the partials in a
-// fixed order.  When the table does not fit (3D at 10x10x10: 234 KiB) flushes
-// go to HBM with global_atomic_add_f32, pre-aggregated across the wave for
-// lanes that share a cell.
+// Moment accumulation on MI355X: each workgroup serves ONE theta and one
+// contiguous range of points (spatially coherent for meshgrid inputs).
+//   full bins  the nC x ppc table fits in LDS: the workgroup keeps a private
+//              copy of that theta's moments there (ds_add_f32, no HBM
+//              atomics) and writes it as one partial with plain coalesced
+//              stores; a separate pass sums the partials in a fixed order.
+//   cache      the table does not fit (3D at 10x10x10: 234 KiB): a
+//              direct-mapped LDS cache of kCacheSlots cells (linear probing,
+//              kCacheProbes slots) collects the flushes of the cells the
+//              workgroup touches; at the end each occupied slot is added to
+//              the moments with global atomics.  Flushes that find no slot
+//              go straight to HBM.
+//   global     every flush is a global_atomic_add_f32, pre-aggregated across
+//              the wave for lanes that share a cell.
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include "cpab_device.hpp"
 #include "cpab_launch.hpp"
 
@@ -145,12 +153,48 @@ __device__ __forceinline__ float stack_pop(float (&a)[N]) {
   return v;
 }
 
+enum Bins { kBinsGlobal = 0, kBinsFull = 1, kBinsCache = 2 };
+
 template <int P>
 __device__ __forceinline__ void flush_lds(float* bins, int c, const float (&m)[P]) {
   float* q = bins + P * c;
 #pragma unroll
   for (int k = 0; k < P; ++k)
     __hip_atomic_fetch_add(q + k, m[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// LDS cache flush (divergent lanes allowed).  The slot of cell c is claimed
+// with a compare-and-swap on its key; a lane whose probe sequence meets only
+// other cells adds to HBM instead.
+template <int P>
+__device__ __forceinline__ void flush_cache(int* keys, float* vals, float* __restrict__ mom, int c,
+                                            const float (&m)[P]) {
+  int slot = c & (kCacheSlots - 1);
+  for (int probe = 0; probe < kCacheProbes; ++probe) {
+    int k = __hip_atomic_load(keys + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (k == -1) {
+      int expected = -1;
+      __hip_atomic_compare_exchange_strong(keys + slot, &expected, c, __ATOMIC_RELAXED,
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      k = expected == -1 ? c : expected;
+    }
+    if (k == c) {
+      flush_lds<P>(vals, slot, m);
+      return;
+    }
+    slot = (slot + 1) & (kCacheSlots - 1);
+  }
+#pragma unroll
+  for (int k = 0; k < P; ++k) unsafeAtomicAdd(mom + (size_t)P * c + k, m[k]);
+}
+
+// Contiguous point range [lo, hi) of this workgroup, a whole number of blocks long.
+__device__ __forceinline__ void wg_range(int nP, int& lo, int& hi) {
+  const int64_t per = ((int64_t)nP + gridDim.x - 1) / gridDim.x;
+  const int64_t span = (per + blockDim.x - 1) / blockDim.x * blockDim.x;
+  const int64_t l = (int64_t)blockIdx.x * span;
+  lo = (int)std::min<int64_t>(l, nP);
+  hi = (int)std::min<int64_t>(l + span, nP);
 }
 
 // Global flush for a converged wave (all 64 lanes active; `need` marks the
@@ -189,11 +233,11 @@ __device__ __forceinline__ void flush_global(float* __restrict__ mom, bool need,
 
 
 // Segmented variant (any T).
-template <int D, bool ADAPTIVE, bool LDS_BINS, typename P>
+template <int D, bool ADAPTIVE, int BINS, typename P>
 __device__ __forceinline__ void segmented_body(P tab, int nP, int batched, int T, const Cells& g,
                                                const float* __restrict__ points,
                                                const float* __restrict__ grad_out, float* bins,
-                                               float* __restrict__ mom_b,
+                                               int* keys, float* __restrict__ mom_b,
                                                float* __restrict__ grad_points) {
   constexpr int PP = Dim<D>::P;
   const int b = blockIdx.y;
@@ -204,11 +248,14 @@ __device__ __forceinline__ void segmented_body(P tab, int nP, int batched, int T
   const float* __restrict__ pts = points + (batched ? (size_t)b * D * nP : 0);
   const float* __restrict__ gout = grad_out + (size_t)b * D * nP;
   // The loop bound is uniform so every wave stays converged (the global flush
-  // needs all 64 lanes); lanes past nP replay a clamped point and contribute nothing.
-  for (int base = blockIdx.x * blockDim.x; base < nP; base += gridDim.x * blockDim.x) {
+  // needs all 64 lanes); lanes past the range replay a clamped point and
+  // contribute nothing.
+  int lo, hi;
+  wg_range(nP, lo, hi);
+  for (int base = lo; base < hi; base += blockDim.x) {
     const int pi0 = base + (int)threadIdx.x;
-    const bool valid = pi0 < nP;
-    const int pi = valid ? pi0 : nP - 1;
+    const bool valid = pi0 < hi;
+    const int pi = valid ? pi0 : hi - 1;
     float p[D];
 #pragma unroll
     for (int k = 0; k < D; ++k) p[k] = pts[pi + (size_t)k * nP];
@@ -256,8 +303,10 @@ __device__ __forceinline__ void segmented_body(P tab, int nP, int batched, int T
         if (s < len) {
           const int c = sc[s];
           const bool need = valid && c != prev && prev >= 0;
-          if (LDS_BINS) {
+          if (BINS == kBinsFull) {
             if (need) flush_lds<PP>(bins, prev, m);
+          } else if (BINS == kBinsCache) {
+            if (need) flush_cache<PP>(keys, bins, mom_b, prev, m);
           } else {
             flush_global<PP>(mom_b, need, prev, m);
           }
@@ -270,8 +319,10 @@ __device__ __forceinline__ void segmented_body(P tab, int nP, int batched, int T
         }
       }
     }
-    if (LDS_BINS) {
+    if (BINS == kBinsFull) {
       if (valid) flush_lds<PP>(bins, prev, m);
+    } else if (BINS == kBinsCache) {
+      if (valid) flush_cache<PP>(keys, bins, mom_b, prev, m);
     } else {
       flush_global<PP>(mom_b, valid, prev, m);
     }
@@ -295,10 +346,12 @@ __device__ __forceinline__ void register_body(P tab, int nP, int batched, const 
   const float hhh = hh * h;
   const float* __restrict__ pts = points + (batched ? (size_t)b * D * nP : 0);
   const float* __restrict__ gout = grad_out + (size_t)b * D * nP;
-  for (int base = blockIdx.x * blockDim.x; base < nP; base += gridDim.x * blockDim.x) {
+  int lo, hi;
+  wg_range(nP, lo, hi);
+  for (int base = lo; base < hi; base += blockDim.x) {
     const int pi0 = base + (int)threadIdx.x;
-    const bool valid = pi0 < nP;
-    const int pi = valid ? pi0 : nP - 1;
+    const bool valid = pi0 < hi;
+    const int pi = valid ? pi0 : hi - 1;
     float p[D];
 #pragma unroll
     for (int k = 0; k < D; ++k) p[k] = pts[pi + (size_t)k * nP];
@@ -356,9 +409,9 @@ __device__ __forceinline__ void register_body(P tab, int nP, int batched, const 
   }
 }
 
-// TS == 0: segmented variant; TS > 0: register variant (requires LDS_BINS).
-template <int D, bool ADAPTIVE, bool LDS_A, bool LDS_BINS, int TS>
-__global__ __launch_bounds__(TS ? 768 : 512) void backward_kernel(
+// TS == 0: segmented variant; TS > 0: register variant (requires full bins).
+template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
+__global__ __launch_bounds__(768) void backward_kernel(
     int nP, int batched, int T, Cells g, int nC, const float* __restrict__ points,
     const float* __restrict__ As, const float* __restrict__ grad_out,
     float* __restrict__ moments, float* __restrict__ partials, float* __restrict__ grad_points) {
@@ -367,40 +420,55 @@ __global__ __launch_bounds__(TS ? 768 : 512) void backward_kernel(
   const int b = blockIdx.y;
   const int R = nC * PP;
   const float* __restrict__ Ag = As + (size_t)b * R;
+  float* __restrict__ mom_b = moments + (size_t)b * R;
   float* ldsA = lds;
-  float* bins = lds + (LDS_A ? R : 0);
+  float* after_a = lds + (LDS_A ? R : 0);
+  // full bins: R floats; cache: kCacheSlots keys, then kCacheSlots * PP floats
+  int* keys = reinterpret_cast<int*>(after_a);
+  float* bins = BINS == kBinsCache ? after_a + kCacheSlots : after_a;
   if (LDS_A) {
     const float2* s2 = reinterpret_cast<const float2*>(Ag);
     float2* d2 = reinterpret_cast<float2*>(ldsA);
     for (int i = threadIdx.x; i < R / 2; i += blockDim.x) d2[i] = s2[i];
   }
-  if (LDS_BINS) {
+  if (BINS == kBinsFull) {
     for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
+  } else if (BINS == kBinsCache) {
+    for (int i = threadIdx.x; i < kCacheSlots; i += blockDim.x) keys[i] = -1;
+    for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) bins[i] = 0.0f;
   }
-  if (LDS_A || LDS_BINS) __syncthreads();
+  if (LDS_A || BINS != kBinsGlobal) __syncthreads();
   if constexpr (TS > 0) {
-    static_assert(LDS_BINS, "the register variant accumulates in LDS bins");
+    static_assert(BINS == kBinsFull, "the register variant accumulates in full LDS bins");
     if (LDS_A) register_body<D, ADAPTIVE, TS>(as_lds(ldsA), nP, batched, g, points, grad_out, bins, grad_points);
     else register_body<D, ADAPTIVE, TS>(Ag, nP, batched, g, points, grad_out, bins, grad_points);
   } else {
-    float* __restrict__ mom_b = moments + (size_t)b * R;
-    if (LDS_A) segmented_body<D, ADAPTIVE, LDS_BINS>(as_lds(ldsA), nP, batched, T, g, points, grad_out, bins, mom_b, grad_points);
-    else segmented_body<D, ADAPTIVE, LDS_BINS>(Ag, nP, batched, T, g, points, grad_out, bins, mom_b, grad_points);
+    if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(ldsA), nP, batched, T, g, points, grad_out, bins, keys, mom_b, grad_points);
+    else segmented_body<D, ADAPTIVE, BINS>(Ag, nP, batched, T, g, points, grad_out, bins, keys, mom_b, grad_points);
   }
-  if (LDS_BINS) {
+  if (BINS == kBinsFull) {
     __syncthreads();
     float* dst = partials + ((size_t)b * gridDim.x + blockIdx.x) * R;
     for (int i = threadIdx.x; i < R; i += blockDim.x) dst[i] = bins[i];
+  } else if (BINS == kBinsCache) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) {
+      const int slot = i / PP;
+      const int c = keys[slot];
+      if (c >= 0) unsafeAtomicAdd(mom_b + (size_t)PP * c + (i - slot * PP), bins[i]);
+    }
   }
 }
 
-template <int D, bool ADAPTIVE, bool LDS_A, bool LDS_BINS, int TS>
+template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 hipError_t go(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int T,
               const float* points, const float* As, const float* grad_out, float* moments,
               float* partials, float* grad_points, const LaunchCfg& cfg, hipStream_t s) {
-  auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, LDS_BINS, TS>;
+  auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
   const size_t R = (size_t)geo.nC * Dim<D>::P;
-  const size_t lds = R * sizeof(float) * ((LDS_A ? 1 : 0) + (LDS_BINS ? 1 : 0));
+  size_t lds = LDS_A ? R * sizeof(float) : 0;
+  if (BINS == kBinsFull) lds += R * sizeof(float);
+  if (BINS == kBinsCache) lds += (size_t)kCacheSlots * (Dim<D>::P + 1) * sizeof(float);
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -421,25 +489,32 @@ hipError_t dispatch(const Geometry& geo, int64_t nP, int64_t n_theta, int batche
 #define CPAB_GO(AD, LA, LB, TS)                                                               \
   return go<D, AD, LA, LB, TS>(geo, nP, n_theta, batched, T, points, As, grad_out, moments,   \
                                partials, grad_points, cfg, s)
-  if (D <= 2 && cfg.reg_steps == kRegSteps && T == kRegSteps && cfg.lds_bins) {
-    const int key = (adaptive ? 2 : 0) | (cfg.lds_table ? 1 : 0);
-    switch (key) {
-      case 0: CPAB_GO(false, false, true, kRegSteps);
-      case 1: CPAB_GO(false, true, true, kRegSteps);
-      case 2: CPAB_GO(true, false, true, kRegSteps);
-      default: CPAB_GO(true, true, true, kRegSteps);
+  if constexpr (D <= 2) {
+    if (cfg.reg_steps == kRegSteps && T == kRegSteps && cfg.lds_bins) {
+      const int key = (adaptive ? 2 : 0) | (cfg.lds_table ? 1 : 0);
+      switch (key) {
+        case 0: CPAB_GO(false, false, kBinsFull, kRegSteps);
+        case 1: CPAB_GO(false, true, kBinsFull, kRegSteps);
+        case 2: CPAB_GO(true, false, kBinsFull, kRegSteps);
+        default: CPAB_GO(true, true, kBinsFull, kRegSteps);
+      }
     }
   }
-  const int key = (adaptive ? 4 : 0) | (cfg.lds_table ? 2 : 0) | (cfg.lds_bins ? 1 : 0);
+  const int bins = cfg.lds_bins ? kBinsFull : (cfg.lds_cache ? kBinsCache : kBinsGlobal);
+  const int key = (adaptive ? 6 : 0) + (cfg.lds_table ? 3 : 0) + bins;
   switch (key) {
-    case 0: CPAB_GO(false, false, false, 0);
-    case 1: CPAB_GO(false, false, true, 0);
-    case 2: CPAB_GO(false, true, false, 0);
-    case 3: CPAB_GO(false, true, true, 0);
-    case 4: CPAB_GO(true, false, false, 0);
-    case 5: CPAB_GO(true, false, true, 0);
-    case 6: CPAB_GO(true, true, false, 0);
-    default: CPAB_GO(true, true, true, 0);
+    case 0: CPAB_GO(false, false, kBinsGlobal, 0);
+    case 1: CPAB_GO(false, false, kBinsFull, 0);
+    case 2: CPAB_GO(false, false, kBinsCache, 0);
+    case 3: CPAB_GO(false, true, kBinsGlobal, 0);
+    case 4: CPAB_GO(false, true, kBinsFull, 0);
+    case 5: CPAB_GO(false, true, kBinsCache, 0);
+    case 6: CPAB_GO(true, false, kBinsGlobal, 0);
+    case 7: CPAB_GO(true, false, kBinsFull, 0);
+    case 8: CPAB_GO(true, false, kBinsCache, 0);
+    case 9: CPAB_GO(true, true, kBinsGlobal, 0);
+    case 10: CPAB_GO(true, true, kBinsFull, 0);
+    default: CPAB_GO(true, true, kBinsCache, 0);
   }
 #undef CPAB_GO
 }

@@ -118,15 +118,16 @@ cpab::LaunchCfg forward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta
   // table only when a lane changes cell, so the table is read through L1/L2 by
   // default; staging it in LDS would cap occupancy for little gain.
   c.lds_table = table <= dev.lds ? env_int("CPAB_FWD_LDS", 0) : 0;
-  c.block = env_int("CPAB_FWD_BLOCK", 512);
+  c.block = std::min(1024, std::max(64, env_int("CPAB_FWD_BLOCK", 512) / 64 * 64));  // launch bound
   const int64_t resident = c.lds_table ? std::max<int64_t>(1, std::min<int64_t>(2048 / c.block, dev.lds / std::max<int64_t>(table, 1)))
                                        : std::max(1, 2048 / c.block);
   // Two rounds of resident workgroups per CU.
   const int64_t want = (int64_t)dev.cus * resident * env_int("CPAB_FWD_WAVES", 2);
   int64_t chunks = std::max<int64_t>(1, div_up(want, std::max<int64_t>(n_theta, 1)));
   chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
-  c.chunks = (int)env_int("CPAB_FWD_CHUNKS", (int)chunks);
+  c.chunks = std::max(1, env_int("CPAB_FWD_CHUNKS", (int)chunks));
   c.lds_bins = 0;
+  c.lds_cache = 0;
   c.reg_steps = 0;
   return c;
 }
@@ -142,22 +143,28 @@ cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_thet
   const bool reg = g.ndim <= 2 && T == cpab::kRegSteps && c.lds_bins && g.nC <= 65535 &&
                    env_int("CPAB_BWD_REG", 1);
   c.reg_steps = reg ? cpab::kRegSteps : 0;
-  const int64_t used = c.lds_bins ? table : 0;
+  // Table too large for LDS: hashed cell cache in LDS, flushed to HBM at the end.
+  const int64_t cache = (int64_t)cpab::kCacheSlots * (g.ppc() + 1) * 4;
+  c.lds_cache = (!c.lds_bins && cache <= dev.lds) ? env_int("CPAB_BWD_CACHE", 1) : 0;
+  const int64_t used = c.lds_bins ? table : (c.lds_cache ? cache : 0);
   c.lds_table = (used + table <= dev.lds) ? env_int("CPAB_BWD_LDS_TABLE", reg ? 0 : 1) : 0;
-  const int64_t lds = table * (c.lds_bins + c.lds_table);
+  const int64_t lds = used + (c.lds_table ? table : 0);
   int wg_per_cu;
   if (reg) {
     c.block = env_int("CPAB_BWD_BLOCK", 768);
     wg_per_cu = std::max(1, 768 / c.block);
   } else {
-    c.block = env_int("CPAB_BWD_BLOCK", 512);
+    // The cache variant runs one workgroup per CU (104 KiB of LDS in 3D): make
+    // it 12 waves.
+    c.block = env_int("CPAB_BWD_BLOCK", c.lds_cache ? 768 : 512);
     wg_per_cu = std::max(1, 2048 / c.block);  // 32 waves per CU
     if (lds > 0) wg_per_cu = (int)std::max<int64_t>(1, std::min<int64_t>(wg_per_cu, dev.lds / lds));
   }
+  c.block = std::min(768, std::max(64, c.block / 64 * 64));  // kernel launch bound
   const int64_t want = (int64_t)dev.cus * wg_per_cu;
   int64_t chunks = std::max<int64_t>(1, div_up(want, std::max<int64_t>(n_theta, 1)));
   chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
-  c.chunks = env_int("CPAB_BWD_CHUNKS", (int)chunks);
+  c.chunks = std::max(1, env_int("CPAB_BWD_CHUNKS", (int)chunks));
   return c;
 }
 

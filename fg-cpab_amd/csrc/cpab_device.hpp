@@ -29,6 +29,11 @@ constexpr int kMaxSeg = (kMaxSteps + kSeg - 1) / kSeg;
 // Step count whose backward keeps the whole trajectory in registers (the
 // library default nstepsolver=50); other step counts use the segmented replay.
 constexpr int kRegSteps = 50;
+// Hashed LDS cell cache of the backward when the full moment table does not
+// fit in LDS: slots (a power of two) and linear-probe length.  3D: 2048 x 13
+// words = 104 KiB.
+constexpr int kCacheSlots = 2048;
+constexpr int kCacheProbes = 4;
 
 // Correctly rounded float exp / log / expm1: evaluated in double and rounded
 // once.  The reference calls CUDA's expf/logf (a few ulp, implementation

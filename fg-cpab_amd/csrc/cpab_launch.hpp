@@ -19,7 +19,8 @@ struct LaunchCfg {
   int block;        // threads per workgroup
   int chunks;       // workgroups per theta (gridDim.x)
   int lds_table;    // stage the per-theta cell table in LDS
-  int lds_bins;     // accumulate moments in LDS bins (else global atomics)
+  int lds_bins;     // accumulate moments in full LDS bins (per-workgroup partials)
+  int lds_cache;    // else: accumulate in the hashed LDS cell cache (else global atomics)
   int reg_steps;    // backward: compile-time step count of the register variant (0 = segmented)
 };
 

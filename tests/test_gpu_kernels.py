@@ -160,6 +160,26 @@ def test_backward_parity(cuda, tess, kind, n, adaptive):
     assert_grad_close(mom, ref_m, rtol=2e-5)
 
 
+@pytest.mark.parametrize("mode", ["cache", "global"])
+@pytest.mark.parametrize("kind,n", [("mesh", 0), ("uniform", 120000)])
+def test_backward_3d_moment_paths(cuda, monkeypatch, mode, kind, n):
+    # [10,10,10]: the 5000 x 12 moment table does not fit in LDS.  "cache" is the
+    # hashed LDS cell cache: meshgrid points keep the cells of a workgroup few;
+    # 120k uniform points under one theta touch more distinct cells per
+    # workgroup than the cache has slots, so flushes also take the HBM
+    # fallback.  "global" switches the cache off (wave-aggregated HBM atomics).
+    if mode == "global":
+        monkeypatch.setenv("CPAB_BWD_CACHE", "0")
+    T = cpab_for([10, 10, 10])
+    theta = seeded_theta(T, 1, 0.5, 71)
+    pts = meshgrid([40, 36, 30]) if kind == "mesh" else uniform_points(3, n, 72)
+    g = np.random.default_rng(73).standard_normal((1, 3, pts.shape[-1])).astype(np.float32)
+    As, mom, gp = _backward_case(T, theta, pts, g, cuda)
+    ref_m, ref_gp = orc.backward(pts, As, g, [10, 10, 10], 50)
+    np.testing.assert_array_equal(gp, ref_gp)
+    assert_grad_close(mom, ref_m, rtol=2e-5)
+
+
 def test_backward_no_points_grad(cuda):
     T = cpab_for([20, 20])
     theta = seeded_theta(T, 2, 0.5, 3)
