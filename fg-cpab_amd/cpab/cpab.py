@@ -12,6 +12,7 @@ import torch
 from .core.tesselation import Tesselation1D, Tesselation2D, Tesselation3D
 from .core.utility import params, get_dir, create_dir
 from .pytorch.transformer import CPAB_transformer as transformer
+from .pytorch.transformer import CPAB_chain_transformer as chain_transformer
 from .pytorch.interpolation import interpolate
 
 # GPU device constant (HIP devices are exposed as "cuda" by PyTorch-ROCm)
@@ -191,10 +192,9 @@ class Cpab(object):
             assert grid.shape[0] == n_batch, \
                 'When passing a 3D grid, its batch dimension must match theta_chain'
         dt = (1.0 / n_transforms) if scale_by_dt else 1.0
-        out = grid
-        for i in range(n_transforms):
-            out = transformer(out, theta_chain[i] * dt, self.params, compute_points_grad=True)
-        return out
+        # One forward and one backward launch for all stages; stage i uses
+        # theta_chain[i] * dt exactly as the reference's per-stage loop does.
+        return chain_transformer(grid, theta_chain * dt, self.params)
 
     def interpolate(self, data, grid, outsize):
         """Border-clamped linear interpolation of ``data`` at ``grid``."""

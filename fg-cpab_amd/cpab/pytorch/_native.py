@@ -34,6 +34,13 @@ _SIGNATURES = {
     "cpab_backward_workspace_size": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int]),
     "cpab_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int,
                                _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp]),
+    "cpab_chain_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                    _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                    _c_vp]),
+    "cpab_chain_backward_workspace_size": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int, _c_int]),
+    "cpab_chain_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                     _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                     _c_vp, _c_vp, _c_i64, _c_vp]),
     "cpab_project": (_c_int, [_c_i64, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "cpab_sum_batch": (_c_int, [_c_i64, _c_i64, _c_vp, _c_vp, _c_vp]),
     "cpab_interp_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
@@ -135,6 +142,28 @@ class Native:
                                       int(adaptive), _ptr(points), _ptr(As), _ptr(grad_out),
                                       _ptr(moments), _ptr(grad_points), _ptr(workspace), wbytes,
                                       _stream(points.device)), "cpab_backward")
+
+    def chain_forward(self, ndim, points, batched, n_batch, n_stages, nP, T, nc, adaptive, Trels,
+                      As, out, stage_points):
+        ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
+        _check(self.lib.cpab_chain_forward(ndim, nP, n_batch, int(batched), n_stages, int(T), ncx,
+                                           ncy, ncz, int(adaptive), _ptr(points), _ptr(Trels),
+                                           _ptr(As), _ptr(out), _ptr(stage_points),
+                                           _stream(points.device)), "cpab_chain_forward")
+
+    def chain_backward_workspace_size(self, ndim, nP, n_batch, n_stages, nC):
+        return int(self.lib.cpab_chain_backward_workspace_size(ndim, nP, n_batch, n_stages, nC))
+
+    def chain_backward(self, ndim, points, batched, n_batch, n_stages, nP, T, nc, adaptive,
+                       stage_points, As, grad_out, moments, grad_points, workspace):
+        ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
+        wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        _check(self.lib.cpab_chain_backward(ndim, nP, n_batch, int(batched), n_stages, int(T),
+                                            ncx, ncy, ncz, int(adaptive), _ptr(points),
+                                            _ptr(stage_points), _ptr(As), _ptr(grad_out),
+                                            _ptr(moments), _ptr(grad_points), _ptr(workspace),
+                                            wbytes, _stream(points.device)),
+               "cpab_chain_backward")
 
     def project(self, moments, D, d, col_ptr, row_idx, vals, grad_theta):
         _check(self.lib.cpab_project(moments.shape[0], D, d, _ptr(moments), _ptr(col_ptr),

@@ -11,12 +11,16 @@ the integrated points ``[n_theta, ndim, nP]`` and differentiates w.r.t. theta
   backward  fused replay + adjoint + moments (cpab_backward) -> dtheta = B^T M
             (cpab_project) [-> sum over theta for shared points]
                                                         (transformer.py:128-168)
+
+``CPAB_chain_transformer`` runs a whole chain of stages (the Python loop of
+``Cpab.transform_grid_chain``, cpab/cpab.py:237-280) as one forward launch
+(cpab_chain_forward) and one backward launch (cpab_chain_backward).
 """
 import torch
 
 from ._native import native
 
-__all__ = ["CPAB_transformer"]
+__all__ = ["CPAB_transformer", "CPAB_chain_transformer"]
 
 
 def CPAB_transformer(points, theta, params, compute_points_grad=False):
@@ -157,3 +161,93 @@ class _CPABFunction(torch.autograd.Function):
         lib.project(moments.view(n_theta, -1), tab["D"], tab["d"], tab["col_ptr"],
                     tab["row_idx"], tab["vals_t"], grad_theta)
         return gp, grad_theta, None, None
+
+
+def CPAB_chain_transformer(points, theta_stages, params):
+    """Chain of CPAB transforms: stage s maps the output of stage s-1 with
+    theta_stages[s]; equal, stage by stage, to chaining ``CPAB_transformer``
+    (with compute_points_grad=True), as ``Cpab.transform_grid_chain`` does in
+    the reference (cpab/cpab.py:270-278).
+
+    Arguments:
+        points: [ndim, n_points] (shared) or [n_batch, ndim, n_points]
+        theta_stages: [n_stages, n_batch, d] (already scaled by dt if wanted)
+    Returns:
+        [n_batch, ndim, n_points]
+    """
+    assert points.is_cuda and theta_stages.is_cuda, "Only GPU tensors supported"
+    assert params.ndim in (1, 2, 3), "GPU transformer supports 1D, 2D, and 3D"
+    return _CPABChainFunction.apply(points, theta_stages, params)
+
+
+class _CPABChainFunction(torch.autograd.Function):
+    """All stages of a chain in one forward and one backward launch."""
+
+    @staticmethod
+    def forward(ctx, points, theta_stages, params):
+        if theta_stages.dim() != 3:
+            raise RuntimeError(f"theta_stages must be [n_stages, n_batch, d], got {tuple(theta_stages.shape)}")
+        K, n_batch, d = theta_stages.shape
+        batched, nP = _check_inputs(points, theta_stages[0], params)
+        lib = native()
+        dev = theta_stages.device
+        ndim, nC = params.ndim, int(params.nC)
+        tab = basis_tables(params, dev)
+        theta_c = theta_stages.detach().reshape(K * n_batch, d).contiguous()
+        points_c = points.detach().contiguous()
+
+        As = torch.empty((K * n_batch, nC, ndim, ndim + 1), device=dev, dtype=torch.float32)
+        lib.affine(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"], As)
+        nstepsolver = int(params.nstepsolver)
+        adaptive = int(getattr(params, "adaptive_substeps", False))
+        nc = [int(v) for v in params.nc]
+        Trels = None
+        if ndim > 1:
+            Trels = torch.empty_like(As)
+            lib.expm(ndim, As, 1.0 / nstepsolver, Trels)
+        grad_wanted = any(ctx.needs_input_grad[:2])
+        stage_points = (torch.empty((K - 1, n_batch, ndim, nP), device=dev, dtype=torch.float32)
+                        if grad_wanted and K > 1 else None)
+        out = torch.empty((n_batch, ndim, nP), device=dev, dtype=torch.float32)
+        lib.chain_forward(ndim, points_c, batched, n_batch, K, nP, nstepsolver, nc, adaptive,
+                          Trels, As, out, stage_points)
+
+        ctx.dims = (K, n_batch, nP)
+        ctx.nstepsolver = nstepsolver
+        ctx.nc = nc
+        ctx.adaptive_substeps = adaptive
+        ctx.params = params
+        ctx.batched = batched
+        ctx.save_for_backward(points_c, As, stage_points)
+        return out
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad):
+        points, As, stage_points = ctx.saved_tensors
+        K, n_batch, nP = ctx.dims
+        params = ctx.params
+        lib = native()
+        dev = As.device
+        nC, ndim = As.shape[1], As.shape[2]
+        ppc = ndim * (ndim + 1)
+        grad = grad.detach().to(torch.float32).contiguous()
+
+        moments = torch.empty((K * n_batch, nC, ppc), device=dev, dtype=torch.float32)
+        ws_bytes = lib.chain_backward_workspace_size(ndim, nP, n_batch, K, nC)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
+        want_points = ctx.needs_input_grad[0]
+        gp = (torch.empty((n_batch, ndim, nP), device=dev, dtype=torch.float32)
+              if want_points else None)
+        lib.chain_backward(ndim, points, ctx.batched, n_batch, K, nP, ctx.nstepsolver, ctx.nc,
+                           ctx.adaptive_substeps, stage_points, As, grad, moments, gp, ws)
+        if want_points and points.dim() == 2:
+            summed = torch.empty((ndim, nP), device=dev, dtype=torch.float32)
+            lib.sum_batch(gp, summed)
+            gp = summed
+
+        tab = basis_tables(params, dev)
+        grad_theta = torch.empty((K * n_batch, tab["d"]), device=dev, dtype=torch.float32)
+        lib.project(moments.view(K * n_batch, -1), tab["D"], tab["d"], tab["col_ptr"],
+                    tab["row_idx"], tab["vals_t"], grad_theta)
+        return gp, grad_theta.view(K, n_batch, tab["d"]), None

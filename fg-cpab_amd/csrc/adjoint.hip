@@ -233,20 +233,20 @@ __device__ __forceinline__ void flush_global(float* __restrict__ mom, bool need,
 
 
 // Segmented variant (any T).
+// One stage of one theta over this workgroup's point range: pts = the stage's
+// input points [D, nP], lam_in = dL/d(stage output) [D, nP], lam_out (may be
+// null) receives dL/d(stage input); moments go to bins / keys / mom_b.
 template <int D, bool ADAPTIVE, int BINS, typename P>
-__device__ __forceinline__ void segmented_body(P tab, int nP, int batched, int T, const Cells& g,
-                                               const float* __restrict__ points,
-                                               const float* __restrict__ grad_out, float* bins,
+__device__ __forceinline__ void segmented_body(P tab, int nP, int T, const Cells& g,
+                                               const float* __restrict__ pts,
+                                               const float* __restrict__ gout, float* bins,
                                                int* keys, float* __restrict__ mom_b,
-                                               float* __restrict__ grad_points) {
+                                               float* __restrict__ lam_out) {
   constexpr int PP = Dim<D>::P;
-  const int b = blockIdx.y;
   const float h = 1.0f / (float)T;
   const float hh = h * 0.5f;
   const float hhh = hh * h;
   const int nseg = (T + kSeg - 1) / kSeg;
-  const float* __restrict__ pts = points + (batched ? (size_t)b * D * nP : 0);
-  const float* __restrict__ gout = grad_out + (size_t)b * D * nP;
   // The loop bound is uniform so every wave stays converged (the global flush
   // needs all 64 lanes); lanes past the range replay a clamped point and
   // contribute nothing.
@@ -326,26 +326,23 @@ __device__ __forceinline__ void segmented_body(P tab, int nP, int batched, int T
     } else {
       flush_global<PP>(mom_b, valid, prev, m);
     }
-    if (grad_points && valid) {
+    if (lam_out && valid) {
 #pragma unroll
-      for (int k = 0; k < D; ++k) grad_points[(size_t)b * D * nP + pi + (size_t)k * nP] = lam[k];
+      for (int k = 0; k < D; ++k) lam_out[pi + (size_t)k * nP] = lam[k];
     }
   }
 }
 
 // Register variant: T == TS known at compile time, moments in LDS bins.
 template <int D, bool ADAPTIVE, int TS, typename P>
-__device__ __forceinline__ void register_body(P tab, int nP, int batched, const Cells& g,
-                                              const float* __restrict__ points,
-                                              const float* __restrict__ grad_out, float* bins,
-                                              float* __restrict__ grad_points) {
+__device__ __forceinline__ void register_body(P tab, int nP, const Cells& g,
+                                              const float* __restrict__ pts,
+                                              const float* __restrict__ gout, float* bins,
+                                              float* __restrict__ lam_out) {
   constexpr int PP = Dim<D>::P;
-  const int b = blockIdx.y;
   const float h = 1.0f / (float)TS;
   const float hh = h * 0.5f;
   const float hhh = hh * h;
-  const float* __restrict__ pts = points + (batched ? (size_t)b * D * nP : 0);
-  const float* __restrict__ gout = grad_out + (size_t)b * D * nP;
   int lo, hi;
   wg_range(nP, lo, hi);
   for (int base = lo; base < hi; base += blockDim.x) {
@@ -402,68 +399,89 @@ __device__ __forceinline__ void register_body(P tab, int nP, int batched, const 
       adjoint(A, traj[t], h, hh, hhh, m, lam);
     }
     if (valid) flush_lds<PP>(bins, prev, m);
-    if (grad_points && valid) {
+    if (lam_out && valid) {
 #pragma unroll
-      for (int k = 0; k < D; ++k) grad_points[(size_t)b * D * nP + pi + (size_t)k * nP] = lam[k];
+      for (int k = 0; k < D; ++k) lam_out[pi + (size_t)k * nP] = lam[k];
     }
   }
 }
 
 // TS == 0: segmented variant; TS > 0: register variant (requires full bins).
+// One workgroup = one theta (blockIdx.y) x one contiguous point range
+// (blockIdx.x).  A chain of K stages (Cpab.transform_grid_chain) runs its
+// stages last to first inside the kernel: stage k reads its input points from
+// `points` (k = 0) or stage_points[k-1], its seed from grad_out (k = K-1) or
+// the lam buffer the stage above wrote for the same points, and writes the
+// adjoint of its input to lam (k > 0) or grad_points (k = 0).  Moments of
+// stage k go to partials / moments row (k * n_batch + b).
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 __global__ __launch_bounds__(768) void backward_kernel(
-    int nP, int batched, int T, Cells g, int nC, const float* __restrict__ points,
-    const float* __restrict__ As, const float* __restrict__ grad_out,
-    float* __restrict__ moments, float* __restrict__ partials, float* __restrict__ grad_points) {
+    int nP, int batched, int T, Cells g, int nC, int K, const float* __restrict__ points,
+    const float* __restrict__ stage_points, const float* __restrict__ As,
+    const float* __restrict__ grad_out, float* __restrict__ moments, float* __restrict__ partials,
+    float* __restrict__ lam, float* __restrict__ grad_points) {
   constexpr int PP = Dim<D>::P;
   extern __shared__ float lds[];
   const int b = blockIdx.y;
+  const int n_batch = gridDim.y;
   const int R = nC * PP;
-  const float* __restrict__ Ag = As + (size_t)b * R;
-  float* __restrict__ mom_b = moments + (size_t)b * R;
+  const size_t plane = (size_t)D * nP;  // one theta's [D, nP] block
   float* ldsA = lds;
   float* after_a = lds + (LDS_A ? R : 0);
   // full bins: R floats; cache: kCacheSlots keys, then kCacheSlots * PP floats
   int* keys = reinterpret_cast<int*>(after_a);
   float* bins = BINS == kBinsCache ? after_a + kCacheSlots : after_a;
-  if (LDS_A) {
-    const float2* s2 = reinterpret_cast<const float2*>(Ag);
-    float2* d2 = reinterpret_cast<float2*>(ldsA);
-    for (int i = threadIdx.x; i < R / 2; i += blockDim.x) d2[i] = s2[i];
-  }
-  if (BINS == kBinsFull) {
-    for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
-  } else if (BINS == kBinsCache) {
-    for (int i = threadIdx.x; i < kCacheSlots; i += blockDim.x) keys[i] = -1;
-    for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) bins[i] = 0.0f;
-  }
-  if (LDS_A || BINS != kBinsGlobal) __syncthreads();
-  if constexpr (TS > 0) {
-    static_assert(BINS == kBinsFull, "the register variant accumulates in full LDS bins");
-    if (LDS_A) register_body<D, ADAPTIVE, TS>(as_lds(ldsA), nP, batched, g, points, grad_out, bins, grad_points);
-    else register_body<D, ADAPTIVE, TS>(Ag, nP, batched, g, points, grad_out, bins, grad_points);
-  } else {
-    if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(ldsA), nP, batched, T, g, points, grad_out, bins, keys, mom_b, grad_points);
-    else segmented_body<D, ADAPTIVE, BINS>(Ag, nP, batched, T, g, points, grad_out, bins, keys, mom_b, grad_points);
-  }
-  if (BINS == kBinsFull) {
-    __syncthreads();
-    float* dst = partials + ((size_t)b * gridDim.x + blockIdx.x) * R;
-    for (int i = threadIdx.x; i < R; i += blockDim.x) dst[i] = bins[i];
-  } else if (BINS == kBinsCache) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) {
-      const int slot = i / PP;
-      const int c = keys[slot];
-      if (c >= 0) unsafeAtomicAdd(mom_b + (size_t)PP * c + (i - slot * PP), bins[i]);
+  for (int k = K - 1; k >= 0; --k) {
+    const size_t row = (size_t)k * n_batch + b;
+    const float* __restrict__ Ag = As + row * R;
+    float* __restrict__ mom_b = moments + row * R;
+    const float* __restrict__ pts =
+        k == 0 ? points + (batched ? (size_t)b * plane : 0) : stage_points + ((size_t)(k - 1) * n_batch + b) * plane;
+    const float* __restrict__ gin = k == K - 1 ? grad_out + (size_t)b * plane : lam + (size_t)b * plane;
+    float* __restrict__ lout = k == 0 ? (grad_points ? grad_points + (size_t)b * plane : nullptr)
+                                      : lam + (size_t)b * plane;
+    if (LDS_A) {
+      const float2* s2 = reinterpret_cast<const float2*>(Ag);
+      float2* d2 = reinterpret_cast<float2*>(ldsA);
+      for (int i = threadIdx.x; i < R / 2; i += blockDim.x) d2[i] = s2[i];
     }
+    if (BINS == kBinsFull) {
+      for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
+    } else if (BINS == kBinsCache) {
+      for (int i = threadIdx.x; i < kCacheSlots; i += blockDim.x) keys[i] = -1;
+      for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) bins[i] = 0.0f;
+    }
+    if (LDS_A || BINS != kBinsGlobal) __syncthreads();
+    if constexpr (TS > 0) {
+      static_assert(BINS == kBinsFull, "the register variant accumulates in full LDS bins");
+      if (LDS_A) register_body<D, ADAPTIVE, TS>(as_lds(ldsA), nP, g, pts, gin, bins, lout);
+      else register_body<D, ADAPTIVE, TS>(Ag, nP, g, pts, gin, bins, lout);
+    } else {
+      if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(ldsA), nP, T, g, pts, gin, bins, keys, mom_b, lout);
+      else segmented_body<D, ADAPTIVE, BINS>(Ag, nP, T, g, pts, gin, bins, keys, mom_b, lout);
+    }
+    // Every lane is done with this stage's tables before they are written out
+    // (and, for the next stage, overwritten).
+    if (LDS_A || BINS != kBinsGlobal) __syncthreads();
+    if (BINS == kBinsFull) {
+      float* dst = partials + (row * gridDim.x + blockIdx.x) * R;
+      for (int i = threadIdx.x; i < R; i += blockDim.x) dst[i] = bins[i];
+    } else if (BINS == kBinsCache) {
+      for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) {
+        const int slot = i / PP;
+        const int c = keys[slot];
+        if (c >= 0) unsafeAtomicAdd(mom_b + (size_t)PP * c + (i - slot * PP), bins[i]);
+      }
+    }
+    if (k > 0 && (LDS_A || BINS != kBinsGlobal)) __syncthreads();
   }
 }
 
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
-hipError_t go(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int T,
-              const float* points, const float* As, const float* grad_out, float* moments,
-              float* partials, float* grad_points, const LaunchCfg& cfg, hipStream_t s) {
+hipError_t go(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int T, int K,
+              const float* points, const float* stage_points, const float* As,
+              const float* grad_out, float* moments, float* partials, float* lam,
+              float* grad_points, const LaunchCfg& cfg, hipStream_t s) {
   auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
   const size_t R = (size_t)geo.nC * Dim<D>::P;
   size_t lds = LDS_A ? R * sizeof(float) : 0;
@@ -476,19 +494,19 @@ hipError_t go(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int
   }
   const Cells g{geo.nx, geo.ny, geo.nz};
   hipLaunchKernelGGL(kernel, dim3((unsigned)cfg.chunks, (unsigned)n_theta), dim3(cfg.block), lds,
-                     s, (int)nP, batched, T, g, geo.nC, points, As, grad_out, moments, partials,
-                     grad_points);
+                     s, (int)nP, batched, T, g, geo.nC, K, points, stage_points, As, grad_out,
+                     moments, partials, lam, grad_points);
   return hipGetLastError();
 }
 
 template <int D>
-hipError_t dispatch(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int T,
-                    int adaptive, const float* points, const float* As, const float* grad_out,
-                    float* moments, float* partials, float* grad_points, const LaunchCfg& cfg,
-                    hipStream_t s) {
-#define CPAB_GO(AD, LA, LB, TS)                                                               \
-  return go<D, AD, LA, LB, TS>(geo, nP, n_theta, batched, T, points, As, grad_out, moments,   \
-                               partials, grad_points, cfg, s)
+hipError_t dispatch(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int T, int K,
+                    int adaptive, const float* points, const float* stage_points, const float* As,
+                    const float* grad_out, float* moments, float* partials, float* lam,
+                    float* grad_points, const LaunchCfg& cfg, hipStream_t s) {
+#define CPAB_GO(AD, LA, LB, TS)                                                                \
+  return go<D, AD, LA, LB, TS>(geo, nP, n_theta, batched, T, K, points, stage_points, As,     \
+                               grad_out, moments, partials, lam, grad_points, cfg, s)
   if constexpr (D <= 2) {
     if (cfg.reg_steps == kRegSteps && T == kRegSteps && cfg.lds_bins) {
       const int key = (adaptive ? 2 : 0) | (cfg.lds_table ? 1 : 0);
@@ -521,21 +539,22 @@ hipError_t dispatch(const Geometry& geo, int64_t nP, int64_t n_theta, int batche
 
 }  // namespace
 
-hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
-                           int adaptive, const float* points, const float* As,
-                           const float* grad_out, float* moments, float* partials,
-                           float* grad_points, const LaunchCfg& cfg, hipStream_t s) {
-  if (nP <= 0 || n_theta <= 0) return hipSuccess;
+hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
+                           int K, int adaptive, const float* points, const float* stage_points,
+                           const float* As, const float* grad_out, float* moments,
+                           float* partials, float* lam, float* grad_points, const LaunchCfg& cfg,
+                           hipStream_t s) {
+  if (nP <= 0 || n_batch <= 0 || K <= 0) return hipSuccess;
   switch (g.ndim) {
     case 1:
-      return dispatch<1>(g, nP, n_theta, batched, T, adaptive, points, As, grad_out, moments,
-                         partials, grad_points, cfg, s);
+      return dispatch<1>(g, nP, n_batch, batched, T, K, adaptive, points, stage_points, As,
+                         grad_out, moments, partials, lam, grad_points, cfg, s);
     case 2:
-      return dispatch<2>(g, nP, n_theta, batched, T, adaptive, points, As, grad_out, moments,
-                         partials, grad_points, cfg, s);
+      return dispatch<2>(g, nP, n_batch, batched, T, K, adaptive, points, stage_points, As,
+                         grad_out, moments, partials, lam, grad_points, cfg, s);
     default:
-      return dispatch<3>(g, nP, n_theta, batched, T, adaptive, points, As, grad_out, moments,
-                         partials, grad_points, cfg, s);
+      return dispatch<3>(g, nP, n_batch, batched, T, K, adaptive, points, stage_points, As,
+                         grad_out, moments, partials, lam, grad_points, cfg, s);
   }
 }
 

@@ -197,6 +197,116 @@ void prof_end(bool on, hipEvent_t a, const char* name, hipStream_t s) {
   g_prof_pending.push_back({name, a, b});
 }
 
+// Forward of a chain of K stages (K = 1: one transform).  ndim 1 uses the
+// closed form (Trels unused).
+int forward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int batched,
+                        int K, int nstepsolver, int ncx, int ncy, int ncz, int adaptive,
+                        const float* points, const float* Trels, const float* As, float* out,
+                        float* stage_points, void* stream) {
+  cpab::Geometry g{};
+  int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
+  if (rc) return rc;
+  if (ndim > 1 && (rc = check_steps(nstepsolver))) return rc;
+  if ((rc = check_points(nP, n_batch, ndim))) return rc;
+  if (K < 1 || K > 4096) return fail(CPAB_ERR_INVALID, "n_stages must be in [1, 4096], got %d", K);
+  if ((int64_t)K * n_batch >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "n_stages * n_batch too large");
+  if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
+  if (nP == 0 || n_batch == 0) return CPAB_OK;
+  CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(out);
+  if (ndim > 1) CPAB_REQUIRE(Trels);
+  hipStream_t s = as_stream(stream);
+  hipEvent_t ev;
+  const bool timed = prof_begin(s, &ev);
+  if (ndim == 1) {
+    rc = check_hip(cpab::launch_forward_1d(g, nP, n_batch, batched ? 1 : 0, K, points, As, out,
+                                           stage_points, s),
+                   who);
+  } else {
+    const cpab::LaunchCfg cfg = forward_cfg(g, nP, n_batch);
+    rc = check_hip(cpab::launch_forward(g, nP, n_batch, batched ? 1 : 0, nstepsolver, K, adaptive,
+                                        points, Trels, As, out, stage_points, cfg, s),
+                   who);
+  }
+  prof_end(timed, ev, "forward", s);
+  return rc;
+}
+
+
+constexpr int64_t kAlign = 256;
+
+int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+// Workspace of a K-stage backward: per-workgroup partial moment tables (full
+// LDS bins only), then the inter-stage adjoint [n_batch, ndim, nP] (K > 1).
+struct BackwardWorkspace {
+  int64_t partials_bytes, lam_offset, total;
+};
+
+BackwardWorkspace backward_workspace(const cpab::Geometry& g, int64_t nP, int64_t n_batch, int K,
+                                     const cpab::LaunchCfg& cfg) {
+  BackwardWorkspace w{};
+  w.partials_bytes = cfg.lds_bins ? (int64_t)K * n_batch * cfg.chunks * g.nC * g.ppc() * 4 : 0;
+  w.lam_offset = align_up(w.partials_bytes);
+  w.total = K > 1 ? w.lam_offset + n_batch * g.ndim * nP * 4 : w.partials_bytes;
+  return w;
+}
+
+int64_t workspace_size_impl(int ndim, int64_t nP, int64_t n_batch, int K, int nC) {
+  if (ndim < 1 || ndim > 3 || nP <= 0 || n_batch <= 0 || nC <= 0 || K < 1) return 0;
+  cpab::Geometry g{};
+  g.ndim = ndim;
+  g.nC = nC;
+  // Whichever variant runs (register or segmented) fits.
+  const int64_t a = backward_workspace(g, nP, n_batch, K, backward_cfg(g, nP, n_batch, cpab::kRegSteps)).total;
+  const int64_t b = backward_workspace(g, nP, n_batch, K, backward_cfg(g, nP, n_batch, 0)).total;
+  return std::max(a, b);
+}
+
+int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int batched, int K,
+                  int nstepsolver, int ncx, int ncy, int ncz, int adaptive, const float* points,
+                  const float* stage_points, const float* As, const float* grad_out,
+                  float* moments, float* grad_points, void* workspace, int64_t workspace_bytes,
+                  void* stream) {
+  cpab::Geometry g{};
+  int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
+  if (rc) return rc;
+  if ((rc = check_steps(nstepsolver))) return rc;
+  if ((rc = check_points(nP, n_batch, ndim))) return rc;
+  if (K < 1 || K > 4096) return fail(CPAB_ERR_INVALID, "n_stages must be in [1, 4096], got %d", K);
+  if ((int64_t)K * n_batch >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "n_stages * n_batch too large");
+  if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
+  if (n_batch == 0) return CPAB_OK;
+  CPAB_REQUIRE(moments);
+  hipStream_t s = as_stream(stream);
+  const int R = g.nC * g.ppc();
+  const int64_t rows = (int64_t)K * n_batch;
+  if (nP == 0) return check_hip(cpab::launch_fill(moments, rows * R, 0.0f, s), who);
+  CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(grad_out);
+  if (K > 1) CPAB_REQUIRE(stage_points);
+  const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_batch, nstepsolver);
+  const BackwardWorkspace w = backward_workspace(g, nP, n_batch, K, cfg);
+  if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
+    return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
+                (long long)w.total, (long long)workspace_bytes);
+  float* partials = static_cast<float*>(workspace);
+  float* lam = K > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + w.lam_offset) : nullptr;
+  if (!cfg.lds_bins) {
+    rc = check_hip(cpab::launch_fill(moments, rows * R, 0.0f, s), who);
+    if (rc) return rc;
+  }
+  hipEvent_t ev;
+  const bool timed = prof_begin(s, &ev);
+  rc = check_hip(cpab::launch_backward(g, nP, n_batch, batched ? 1 : 0, nstepsolver, K, adaptive,
+                                       points, stage_points, As, grad_out, moments, partials, lam,
+                                       grad_points, cfg, s),
+                 who);
+  prof_end(timed, ev, "backward", s);
+  if (rc) return rc;
+  if (cfg.lds_bins)
+    rc = check_hip(cpab::launch_reduce_partials(rows, cfg.chunks, R, partials, moments, s), who);
+  return rc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -231,42 +341,23 @@ int cpab_expm(int ndim, int64_t n_matrices, float dT, const float* As, float* Tr
 
 int cpab_forward_1d_closed_form(int64_t nP, int64_t n_theta, int batched, int ncx,
                                 const float* points, const float* As, float* out, void* stream) {
-  cpab::Geometry g{};
-  int rc = check_geometry(1, ncx, 1, 1, &g);
-  if (rc) return rc;
-  if ((rc = check_points(nP, n_theta, 1))) return rc;
-  if (nP == 0 || n_theta == 0) return CPAB_OK;
-  CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(out);
-  hipEvent_t ev;
-  const bool timed = prof_begin(as_stream(stream), &ev);
-  rc = check_hip(cpab::launch_forward_1d(g, nP, n_theta, batched ? 1 : 0, points, As, out,
-                                         as_stream(stream)),
-                 "cpab_forward_1d_closed_form");
-  prof_end(timed, ev, "forward", as_stream(stream));
-  return rc;
+  return forward_impl("cpab_forward_1d_closed_form", 1, nP, n_theta, batched, 1, 1, ncx, 1, 1, 0,
+                      points, nullptr, As, out, nullptr, stream);
 }
 
 int cpab_forward(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver, int ncx,
                  int ncy, int ncz, int adaptive, const float* points, const float* Trels,
                  const float* As, float* out, void* stream) {
-  if (ndim == 1)
-    return cpab_forward_1d_closed_form(nP, n_theta, batched, ncx, points, As, out, stream);
-  cpab::Geometry g{};
-  int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
-  if (rc) return rc;
-  if ((rc = check_steps(nstepsolver))) return rc;
-  if ((rc = check_points(nP, n_theta, ndim))) return rc;
-  if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
-  if (nP == 0 || n_theta == 0) return CPAB_OK;
-  CPAB_REQUIRE(points); CPAB_REQUIRE(Trels); CPAB_REQUIRE(As); CPAB_REQUIRE(out);
-  const cpab::LaunchCfg cfg = forward_cfg(g, nP, n_theta);
-  hipEvent_t ev;
-  const bool timed = prof_begin(as_stream(stream), &ev);
-  rc = check_hip(cpab::launch_forward(g, nP, n_theta, batched ? 1 : 0, nstepsolver, adaptive,
-                                      points, Trels, As, out, cfg, as_stream(stream)),
-                 "cpab_forward");
-  prof_end(timed, ev, "forward", as_stream(stream));
-  return rc;
+  return forward_impl("cpab_forward", ndim, nP, n_theta, batched, 1, nstepsolver, ncx, ncy, ncz,
+                      adaptive, points, Trels, As, out, nullptr, stream);
+}
+
+int cpab_chain_forward(int ndim, int64_t nP, int64_t n_batch, int batched, int n_stages,
+                       int nstepsolver, int ncx, int ncy, int ncz, int adaptive,
+                       const float* points, const float* Trels, const float* As, float* out,
+                       float* stage_points, void* stream) {
+  return forward_impl("cpab_chain_forward", ndim, nP, n_batch, batched, n_stages, nstepsolver, ncx,
+                      ncy, ncz, adaptive, points, Trels, As, out, stage_points, stream);
 }
 
 int cpab_trace_cells(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
@@ -287,54 +378,31 @@ int cpab_trace_cells(int ndim, int64_t nP, int64_t n_theta, int batched, int nst
 }
 
 int64_t cpab_backward_workspace_size(int ndim, int64_t nP, int64_t n_theta, int nC) {
-  if (ndim < 1 || ndim > 3 || nP <= 0 || n_theta <= 0 || nC <= 0) return 0;
-  cpab::Geometry g{};
-  g.ndim = ndim;
-  g.nC = nC;
-  // Partials: one moment table per workgroup, for whichever variant runs.
-  const cpab::LaunchCfg a = backward_cfg(g, nP, n_theta, cpab::kRegSteps);
-  const cpab::LaunchCfg b = backward_cfg(g, nP, n_theta, 0);
-  const int64_t chunks = std::max(a.lds_bins ? a.chunks : 0, b.lds_bins ? b.chunks : 0);
-  return (int64_t)n_theta * chunks * nC * g.ppc() * (int64_t)sizeof(float);
+  return workspace_size_impl(ndim, nP, n_theta, 1, nC);
+}
+
+int64_t cpab_chain_backward_workspace_size(int ndim, int64_t nP, int64_t n_batch, int n_stages,
+                                           int nC) {
+  return workspace_size_impl(ndim, nP, n_batch, n_stages, nC);
 }
 
 int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver, int ncx,
                   int ncy, int ncz, int adaptive, const float* points, const float* As,
                   const float* grad_out, float* moments, float* grad_points, void* workspace,
                   int64_t workspace_bytes, void* stream) {
-  cpab::Geometry g{};
-  int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
-  if (rc) return rc;
-  if ((rc = check_steps(nstepsolver))) return rc;
-  if ((rc = check_points(nP, n_theta, ndim))) return rc;
-  if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
-  if (n_theta == 0) return CPAB_OK;
-  CPAB_REQUIRE(moments);
-  hipStream_t s = as_stream(stream);
-  const int R = g.nC * g.ppc();
-  if (nP == 0) return check_hip(cpab::launch_fill(moments, n_theta * R, 0.0f, s), "cpab_backward");
-  CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(grad_out);
-  const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_theta, nstepsolver);
-  const int64_t need = cfg.lds_bins ? (int64_t)n_theta * cfg.chunks * R * (int64_t)sizeof(float) : 0;
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-    return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld", (long long)need,
-                (long long)workspace_bytes);
-  float* partials = static_cast<float*>(workspace);
-  if (!cfg.lds_bins) {
-    rc = check_hip(cpab::launch_fill(moments, n_theta * R, 0.0f, s), "cpab_backward(zero)");
-    if (rc) return rc;
-  }
-  hipEvent_t ev;
-  const bool timed = prof_begin(s, &ev);
-  rc = check_hip(cpab::launch_backward(g, nP, n_theta, batched ? 1 : 0, nstepsolver, adaptive,
-                                       points, As, grad_out, moments, partials, grad_points, cfg, s),
-                 "cpab_backward");
-  prof_end(timed, ev, "backward", s);
-  if (rc) return rc;
-  if (cfg.lds_bins)
-    rc = check_hip(cpab::launch_reduce_partials(n_theta, cfg.chunks, R, partials, moments, s),
-                   "cpab_backward(reduce)");
-  return rc;
+  return backward_impl("cpab_backward", ndim, nP, n_theta, batched, 1, nstepsolver, ncx, ncy, ncz,
+                       adaptive, points, nullptr, As, grad_out, moments, grad_points, workspace,
+                       workspace_bytes, stream);
+}
+
+int cpab_chain_backward(int ndim, int64_t nP, int64_t n_batch, int batched, int n_stages,
+                        int nstepsolver, int ncx, int ncy, int ncz, int adaptive,
+                        const float* points, const float* stage_points, const float* As,
+                        const float* grad_out, float* moments, float* grad_points,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
+  return backward_impl("cpab_chain_backward", ndim, nP, n_batch, batched, n_stages, nstepsolver,
+                       ncx, ncy, ncz, adaptive, points, stage_points, As, grad_out, moments,
+                       grad_points, workspace, workspace_bytes, stream);
 }
 
 int cpab_project(int64_t n_theta, int D, int d, const float* moments, const int32_t* col_ptr,

@@ -39,18 +39,24 @@ hipError_t launch_reduce_partials(int64_t n_theta, int nparts, int R, const floa
                                   float* moments, hipStream_t s);
 hipError_t launch_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, hipStream_t s);
 
-hipError_t launch_forward_1d(const Geometry& g, int64_t nP, int64_t n_theta, int batched,
-                             const float* points, const float* As, float* out, hipStream_t s);
-hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
-                          int adaptive, const float* points, const float* Trels, const float* As,
-                          float* out, const LaunchCfg& cfg, hipStream_t s);
+hipError_t launch_forward_1d(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int K,
+                             const float* points, const float* As, float* out,
+                             float* stage_points, hipStream_t s);
+// K = number of chained stages (1 = one transform); tables hold K * n_batch rows,
+// row = stage * n_batch + batch.  stage_points [K-1, n_batch, ndim, nP] may be null.
+hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
+                          int K, int adaptive, const float* points, const float* Trels,
+                          const float* As, float* out, float* stage_points, const LaunchCfg& cfg,
+                          hipStream_t s);
 hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
                               int adaptive, const float* points, const float* Trels,
                               const float* As, int32_t* cells, hipStream_t s);
-hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
-                           int adaptive, const float* points, const float* As,
-                           const float* grad_out, float* moments, float* partials,
-                           float* grad_points, const LaunchCfg& cfg, hipStream_t s);
+// lam: [n_batch, ndim, nP] scratch carrying the adjoint between stages (K > 1).
+hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
+                           int K, int adaptive, const float* points, const float* stage_points,
+                           const float* As, const float* grad_out, float* moments,
+                           float* partials, float* lam, float* grad_points, const LaunchCfg& cfg,
+                           hipStream_t s);
 
 hipError_t launch_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
                                  const int64_t* out_size, const float* data, const float* grid,

@@ -12,6 +12,7 @@
 // trajectories, so global reads and writes are fully coalesced.  The integrator
 // is fp32 VALU-bound; no MFMA is involved.
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include <math.h>
 #include "cpab_device.hpp"
 #include "cpab_launch.hpp"
@@ -69,15 +70,25 @@ __device__ float closed_form_1d(float x, float t, const float* __restrict__ A, i
   return x;
 }
 
-__global__ __launch_bounds__(256) void fwd1d_closed_kernel(int nP, int batched, int nx,
+// K > 1: chain of stages, row (s * n_batch + b) of As for stage s; inputs of
+// stages s >= 1 saved to stage_points[s-1] when it is not null.
+__global__ __launch_bounds__(256) void fwd1d_closed_kernel(int nP, int batched, int nx, int K,
                                                           const float* __restrict__ points,
                                                           const float* __restrict__ As,
-                                                          float* __restrict__ out) {
+                                                          float* __restrict__ out,
+                                                          float* __restrict__ stage_points) {
   const int b = blockIdx.y;
-  const float* A = As + (size_t)b * 2 * nx;
+  const int n_batch = gridDim.y;
   const float* pts = points + (batched ? (size_t)b * nP : 0);
-  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < nP; p += gridDim.x * blockDim.x)
-    out[(size_t)b * nP + p] = closed_form_1d(pts[p], 1.0f, A, nx);
+  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < nP; p += gridDim.x * blockDim.x) {
+    float x = pts[p];
+    for (int st = 0; st < K; ++st) {
+      const size_t row = (size_t)st * n_batch + b;
+      if (st > 0 && stage_points) stage_points[((size_t)(st - 1) * n_batch + b) * nP + p] = x;
+      x = closed_form_1d(x, 1.0f, As + row * 2 * nx, nx);
+    }
+    out[(size_t)b * nP + p] = x;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -94,19 +105,25 @@ __device__ __forceinline__ void stage(float* __restrict__ dst, const float* __re
 
 // PPT independent trajectories per lane give the scheduler two dependency
 // chains (lookup -> table read -> affine apply) to interleave.
+//
+// K > 1 runs a chain (Cpab.transform_grid_chain): stage s integrates with the
+// tables of row (s * n_batch + b) of Trels / As, starting from the previous
+// stage's result; the input of every stage s >= 1 is saved to
+// stage_points[s-1] (if not null) for the backward.  LDS staging of the table
+// is used only for K == 1.
 template <bool ADAPTIVE, bool LDS, int PPT>
 __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T, int nx, int ny,
-                                                    const float* __restrict__ points,
+                                                    int K, const float* __restrict__ points,
                                                     const float* __restrict__ Trels,
                                                     const float* __restrict__ As,
-                                                    float* __restrict__ out) {
+                                                    float* __restrict__ out,
+                                                    float* __restrict__ stage_points) {
   extern __shared__ float lds[];
   const int b = blockIdx.y;
+  const int n_batch = gridDim.y;
   const int nC = 4 * nx * ny;
-  const float* __restrict__ Tg = Trels + (size_t)b * nC * 6;
-  const float* __restrict__ Ag = As + (size_t)b * nC * 6;
   if (LDS) {
-    stage(lds, Tg, nC * 6);
+    stage(lds, Trels + (size_t)b * nC * 6, nC * 6);
     __syncthreads();
   }
   const float h = 1.0f / (float)T;
@@ -122,40 +139,56 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
       px[k] = pts[p];
       py[k] = pts[p + nP];
     }
-    // The one-step map of the current cell stays in registers; it is
-    // re-read (LDS / L1) only at steps where some lane of the wave changed
-    // cell, which keeps table traffic and LDS bank conflicts off most steps.
-    int cur[PPT];
-    Aff<2> M[PPT];
+    for (int st = 0; st < K; ++st) {
+      const size_t row = (size_t)st * n_batch + b;
+      const float* __restrict__ Tg = Trels + row * nC * 6;
+      const float* __restrict__ Ag = As + row * nC * 6;
+      if (st > 0 && stage_points) {
+        float* sp = stage_points + ((size_t)(st - 1) * n_batch + b) * 2 * nP;
 #pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      cur[k] = cell_2d(px[k], py[k], nx, ny);
-      M[k] = LDS ? load_aff2(as_lds(lds), cur[k]) : load_aff2(Tg, cur[k]);
-    }
-    for (int t = 0; t < T; ++t) {
-#pragma unroll
-      for (int k = 0; k < PPT; ++k) {
-        const int c = (t == 0) ? cur[k] : cell_2d(px[k], py[k], nx, ny);
-        if (__builtin_amdgcn_ballot_w64(c != cur[k])) {
-          if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
-          cur[k] = c;
-        }
-        float sx, sy;
-        apply2(M[k], px[k], py[k], sx, sy);
-        if (ADAPTIVE) {
-          const int ce = cell_2d(sx, sy, nx, ny);
-          if (ce != c) {
-            float v0x, v0y, v1x, v1y;
-            apply2(load_aff2(Ag, c), px[k], py[k], v0x, v0y);
-            apply2(load_aff2(Ag, ce), sx, sy, v1x, v1y);
-            sx = fmaf(hh, v0x + v1x, px[k]);
-            sy = fmaf(hh, v0y + v1y, py[k]);
+        for (int k = 0; k < PPT; ++k) {
+          const int p = p0 + k * stride;
+          if (p < nP) {
+            sp[p] = px[k];
+            sp[p + nP] = py[k];
           }
         }
-        px[k] = sx;
-        py[k] = sy;
       }
-    }
+      // The one-step map of the current cell stays in registers; it is
+      // re-read (LDS / L1) only at steps where some lane of the wave changed
+      // cell, which keeps table traffic and LDS bank conflicts off most steps.
+      int cur[PPT];
+      Aff<2> M[PPT];
+#pragma unroll
+      for (int k = 0; k < PPT; ++k) {
+        cur[k] = cell_2d(px[k], py[k], nx, ny);
+        M[k] = LDS ? load_aff2(as_lds(lds), cur[k]) : load_aff2(Tg, cur[k]);
+      }
+      for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int k = 0; k < PPT; ++k) {
+          const int c = (t == 0) ? cur[k] : cell_2d(px[k], py[k], nx, ny);
+          if (__builtin_amdgcn_ballot_w64(c != cur[k])) {
+            if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
+            cur[k] = c;
+          }
+          float sx, sy;
+          apply2(M[k], px[k], py[k], sx, sy);
+          if (ADAPTIVE) {
+            const int ce = cell_2d(sx, sy, nx, ny);
+            if (ce != c) {
+              float v0x, v0y, v1x, v1y;
+              apply2(load_aff2(Ag, c), px[k], py[k], v0x, v0y);
+              apply2(load_aff2(Ag, ce), sx, sy, v1x, v1y);
+              sx = fmaf(hh, v0x + v1x, px[k]);
+              sy = fmaf(hh, v0y + v1y, py[k]);
+            }
+          }
+          px[k] = sx;
+          py[k] = sy;
+        }
+      }
+    }  // stages
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
       const int p = p0 + k * stride;
@@ -169,17 +202,17 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
 
 template <bool ADAPTIVE, bool LDS>
 __global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T, int nx, int ny,
-                                                    int nz, const float* __restrict__ points,
+                                                    int nz, int K, const float* __restrict__ points,
                                                     const float* __restrict__ Trels,
                                                     const float* __restrict__ As,
-                                                    float* __restrict__ out) {
+                                                    float* __restrict__ out,
+                                                    float* __restrict__ stage_points) {
   extern __shared__ float lds[];
   const int b = blockIdx.y;
+  const int n_batch = gridDim.y;
   const int nC = 5 * nx * ny * nz;
-  const float* __restrict__ Tg = Trels + (size_t)b * nC * 12;
-  const float* __restrict__ Ag = As + (size_t)b * nC * 12;
   if (LDS) {
-    stage(lds, Tg, nC * 12);
+    stage(lds, Trels + (size_t)b * nC * 12, nC * 12);
     __syncthreads();
   }
   const float h = 1.0f / (float)T;
@@ -188,26 +221,37 @@ __global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T,
   float* __restrict__ o = out + (size_t)b * 3 * nP;
   for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < nP; p += gridDim.x * blockDim.x) {
     float px = pts[p], py = pts[p + nP], pz = pts[p + 2 * (size_t)nP];
-    for (int t = 0; t < T; ++t) {
-      const int c = cell_3d(px, py, pz, nx, ny, nz);
-      const Aff<3> M = LDS ? load_aff3(as_lds(lds), c) : load_aff3(Tg, c);
-      float sx, sy, sz;
-      apply3(M, px, py, pz, sx, sy, sz);
-      if (ADAPTIVE) {
-        const int ce = cell_3d(sx, sy, sz, nx, ny, nz);
-        if (ce != c) {
-          float v0x, v0y, v0z, v1x, v1y, v1z;
-          apply3(load_aff3(Ag, c), px, py, pz, v0x, v0y, v0z);
-          apply3(load_aff3(Ag, ce), sx, sy, sz, v1x, v1y, v1z);
-          sx = fmaf(hh, v0x + v1x, px);
-          sy = fmaf(hh, v0y + v1y, py);
-          sz = fmaf(hh, v0z + v1z, pz);
-        }
+    for (int st = 0; st < K; ++st) {
+      const size_t row = (size_t)st * n_batch + b;
+      const float* __restrict__ Tg = Trels + row * nC * 12;
+      const float* __restrict__ Ag = As + row * nC * 12;
+      if (st > 0 && stage_points) {
+        float* sp = stage_points + ((size_t)(st - 1) * n_batch + b) * 3 * nP;
+        sp[p] = px;
+        sp[p + nP] = py;
+        sp[p + 2 * (size_t)nP] = pz;
       }
-      px = sx;
-      py = sy;
-      pz = sz;
-    }
+      for (int t = 0; t < T; ++t) {
+        const int c = cell_3d(px, py, pz, nx, ny, nz);
+        const Aff<3> M = LDS ? load_aff3(as_lds(lds), c) : load_aff3(Tg, c);
+        float sx, sy, sz;
+        apply3(M, px, py, pz, sx, sy, sz);
+        if (ADAPTIVE) {
+          const int ce = cell_3d(sx, sy, sz, nx, ny, nz);
+          if (ce != c) {
+            float v0x, v0y, v0z, v1x, v1y, v1z;
+            apply3(load_aff3(Ag, c), px, py, pz, v0x, v0y, v0z);
+            apply3(load_aff3(Ag, ce), sx, sy, sz, v1x, v1y, v1z);
+            sx = fmaf(hh, v0x + v1x, px);
+            sy = fmaf(hh, v0y + v1y, py);
+            sz = fmaf(hh, v0z + v1z, pz);
+          }
+        }
+        px = sx;
+        py = sy;
+        pz = sz;
+      }
+    }  // stages
     o[p] = px;
     o[p + nP] = py;
     o[p + 2 * (size_t)nP] = pz;
@@ -279,51 +323,60 @@ __global__ __launch_bounds__(256) void trace_cells_kernel(int ndim, int nP, int 
   }
 }
 
-template <typename K>
-hipError_t launch_with_lds(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s,
-                           int nP, int batched, int T, int nx, int ny, const float* points,
-                           const float* Trels, const float* As, float* out) {
+template <typename Kern>
+hipError_t launch_with_lds(Kern kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                           int nP, int batched, int T, int nx, int ny, int K, const float* points,
+                           const float* Trels, const float* As, float* out, float* stage_points) {
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kernel, grid, block, lds, s, nP, batched, T, nx, ny, points, Trels, As, out);
+  hipLaunchKernelGGL(kernel, grid, block, lds, s, nP, batched, T, nx, ny, K, points, Trels, As,
+                     out, stage_points);
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_forward_1d(const Geometry& g, int64_t nP, int64_t n_theta, int batched,
-                             const float* points, const float* As, float* out, hipStream_t s) {
-  if (nP <= 0 || n_theta <= 0) return hipSuccess;
+hipError_t launch_forward_1d(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int K,
+                             const float* points, const float* As, float* out,
+                             float* stage_points, hipStream_t s) {
+  if (nP <= 0 || n_batch <= 0 || K <= 0) return hipSuccess;
   int64_t gx = (nP + 255) / 256;
   if (gx > 4096) gx = 4096;
-  hipLaunchKernelGGL(fwd1d_closed_kernel, dim3((unsigned)gx, (unsigned)n_theta), dim3(256), 0, s,
-                     (int)nP, batched, g.nx, points, As, out);
+  hipLaunchKernelGGL(fwd1d_closed_kernel, dim3((unsigned)gx, (unsigned)n_batch), dim3(256), 0, s,
+                     (int)nP, batched, g.nx, K, points, As, out, stage_points);
   return hipGetLastError();
 }
 
-hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,
-                          int adaptive, const float* points, const float* Trels, const float* As,
-                          float* out, const LaunchCfg& cfg, hipStream_t s) {
-  if (nP <= 0 || n_theta <= 0) return hipSuccess;
-  const dim3 grid((unsigned)cfg.chunks, (unsigned)n_theta), block((unsigned)cfg.block);
+hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
+                          int K, int adaptive, const float* points, const float* Trels,
+                          const float* As, float* out, float* stage_points, const LaunchCfg& cfg,
+                          hipStream_t s) {
+  if (nP <= 0 || n_batch <= 0 || K <= 0) return hipSuccess;
+  const dim3 grid((unsigned)cfg.chunks, (unsigned)n_batch), block((unsigned)cfg.block);
   const size_t tab = (size_t)g.nC * g.ppc() * sizeof(float);
-  const size_t lds = cfg.lds_table ? tab : 0;
+  const bool lds_table = cfg.lds_table && K == 1;
+  const size_t lds = lds_table ? tab : 0;
   if (g.ndim == 2) {
     if (adaptive) {
-      return cfg.lds_table
+      return lds_table
                  ? launch_with_lds(fwd2d_kernel<true, true, 1>, grid, block, lds, s, (int)nP,
-                                   batched, T, g.nx, g.ny, points, Trels, As, out)
+                                   batched, T, g.nx, g.ny, K, points, Trels, As, out, stage_points)
                  : launch_with_lds(fwd2d_kernel<true, false, 1>, grid, block, lds, s, (int)nP,
-                                   batched, T, g.nx, g.ny, points, Trels, As, out);
+                                   batched, T, g.nx, g.ny, K, points, Trels, As, out, stage_points);
     }
-    return cfg.lds_table
-               ? launch_with_lds(fwd2d_kernel<false, true, 2>, grid, block, lds, s, (int)nP,
-                                 batched, T, g.nx, g.ny, points, Trels, As, out)
-               : launch_with_lds(fwd2d_kernel<false, false, 2>, grid, block, lds, s, (int)nP,
-                                 batched, T, g.nx, g.ny, points, Trels, As, out);
+    // Two points per lane: no more workgroups than it takes to cover nP once
+    // (a lane's second point would otherwise duplicate work on a clamped index).
+    const int64_t need = (nP + 2 * (int64_t)cfg.block - 1) / (2 * (int64_t)cfg.block);
+    const dim3 grid2((unsigned)std::max<int64_t>(1, std::min<int64_t>(cfg.chunks, need)),
+                     (unsigned)n_batch);
+    return lds_table
+               ? launch_with_lds(fwd2d_kernel<false, true, 2>, grid2, block, lds, s, (int)nP,
+                                 batched, T, g.nx, g.ny, K, points, Trels, As, out, stage_points)
+               : launch_with_lds(fwd2d_kernel<false, false, 2>, grid2, block, lds, s, (int)nP,
+                                 batched, T, g.nx, g.ny, K, points, Trels, As, out, stage_points);
   }
   // 3D: the kernel takes nz as an extra argument.
   auto go = [&](auto kernel) -> hipError_t {
@@ -332,12 +385,12 @@ hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_theta, int ba
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kernel, grid, block, lds, s, (int)nP, batched, T, g.nx, g.ny, g.nz,
-                       points, Trels, As, out);
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, (int)nP, batched, T, g.nx, g.ny, g.nz, K,
+                       points, Trels, As, out, stage_points);
     return hipGetLastError();
   };
-  if (adaptive) return cfg.lds_table ? go(fwd3d_kernel<true, true>) : go(fwd3d_kernel<true, false>);
-  return cfg.lds_table ? go(fwd3d_kernel<false, true>) : go(fwd3d_kernel<false, false>);
+  if (adaptive) return lds_table ? go(fwd3d_kernel<true, true>) : go(fwd3d_kernel<true, false>);
+  return lds_table ? go(fwd3d_kernel<false, true>) : go(fwd3d_kernel<false, false>);
 }
 
 hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,

@@ -90,6 +90,40 @@ int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nsteps
                   float* grad_points, void* workspace, int64_t workspace_bytes,
                   void* stream);
 
+/* Chain of n_stages transforms (cpab/cpab.py:237-280, Cpab.transform_grid_chain:
+ * stage s maps the output of stage s-1 with theta_chain[s]; the reference runs
+ * one cpab_gpu.forward per stage from a Python loop).  Tables hold
+ * n_stages * n_batch rows, row = s * n_batch + b ([n_stages, n_batch, nC,
+ * ndim, ndim+1]); points as in cpab_forward (shared or batched) feed stage 0.
+ * out [n_batch, ndim, nP].  If stage_points is not NULL it receives the input
+ * of every stage s >= 1, [n_stages-1, n_batch, ndim, nP], which
+ * cpab_chain_backward needs.  Each stage's arithmetic is that of cpab_forward,
+ * so the result equals n_stages chained cpab_forward calls bit for bit.
+ * ndim 1 uses the closed form per stage (Trels unused, may be NULL). */
+int cpab_chain_forward(int ndim, int64_t nP, int64_t n_batch, int batched, int n_stages,
+                       int nstepsolver, int ncx, int ncy, int ncz, int adaptive,
+                       const float* points, const float* Trels, const float* As, float* out,
+                       float* stage_points, void* stream);
+
+/* Bytes of device workspace cpab_chain_backward needs (partial moment tables
+ * and the adjoint carried between stages). */
+int64_t cpab_chain_backward_workspace_size(int ndim, int64_t nP, int64_t n_batch, int n_stages,
+                                           int nC);
+
+/* Backward of cpab_chain_forward in one launch: replaces the n_stages
+ * autograd nodes of the reference's chain, each a
+ * cpab_gpu.backward_moments_and_points call (transformer_cuda.cpp:122-153)
+ * whose grad_points seeds the stage below.  moments [n_stages, n_batch, nC,
+ * ndim*(ndim+1)] (overwritten); grad_points (may be NULL) = adjoint of the
+ * stage-0 input points, [n_batch, ndim, nP] (sum over n_batch for shared
+ * points, as cpab_sum_batch does).  stage_points as written by
+ * cpab_chain_forward (may be NULL when n_stages == 1). */
+int cpab_chain_backward(int ndim, int64_t nP, int64_t n_batch, int batched, int n_stages,
+                        int nstepsolver, int ncx, int ncy, int ncz, int adaptive,
+                        const float* points, const float* stage_points, const float* As,
+                        const float* grad_out, float* moments, float* grad_points,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
 /* grad_theta[b, j] = sum_k vals[k] * moments[b, row_idx[k]] over the CSC column
  * j of B (D = rows of B).  Replaces torch.sparse.mm(B^T, M^T) in
  * cpab/pytorch/transformer.py:165-166. */

@@ -75,3 +75,17 @@ def test_trace_and_interp_validation():
 def test_missing_library_raises(tmp_path):
     with pytest.raises(RuntimeError, match="not found"):
         _native.load_library(str(tmp_path / "nope.so"))
+
+
+def test_chain_validation():
+    lib = _native.load_library()
+    p = ctypes.c_void_p(16)
+    rc = lib.cpab_chain_forward(2, 10, 1, 0, 0, 50, 4, 4, 1, 0, p, p, p, p, None, None)
+    assert rc == 1 and "n_stages" in _err(lib)
+    rc = lib.cpab_chain_backward(2, 10, 1, 0, 3, 50, 4, 4, 1, 0, p, None, p, p, p, None, None, 0,
+                                 None)
+    assert rc == 1 and "stage_points" in _err(lib)
+    rc = lib.cpab_chain_backward(2, 10, 1, 0, 5000, 50, 4, 4, 1, 0, p, p, p, p, p, None, None, 0,
+                                 None)
+    assert rc == 1 and "n_stages" in _err(lib)
+    assert lib.cpab_chain_backward_workspace_size(2, 10, 1, 0, 64) == 0

@@ -250,3 +250,61 @@ def test_interp_unaligned_grid(cuda):
     native().interp_backward(2, _dev(data, cuda), view, outs, _dev(gout, cuda), gg, None)
     rg, _ = orc.interp_backward(2, data, grid, outs, gout)
     np.testing.assert_array_equal(gg.cpu().numpy(), rg)
+
+
+@pytest.mark.parametrize("tess,kind,adaptive", [([50], "line", 0), ([16, 16], "mesh", 0),
+                                                ([16, 16], "batched", 1), ([4, 4, 4], "uniform", 0),
+                                                ([10, 10, 10], "mesh", 0)])
+def test_chain_matches_stagewise(cuda, tess, kind, adaptive):
+    # cpab_chain_forward / cpab_chain_backward against the stage-by-stage
+    # composition the reference's transform_grid_chain performs
+    # (cpab/cpab.py:270-278): stage outputs and stage inputs bit-exact, the
+    # adjoint handed from stage to stage bit-exact (grad_points), moments of
+    # every stage within tolerance.
+    T = cpab_for(tess)
+    p = T.params
+    nd = len(tess)
+    K, nb = 3, 2
+    theta = (np.random.default_rng(81).standard_normal((K * nb, p.d)) * 0.3).astype(np.float32)
+    if kind == "line":
+        pts = np.linspace(0, 1, 3000, dtype=np.float32)[None]
+    elif kind == "mesh":
+        pts = meshgrid([40, 32] if nd == 2 else [17, 13, 11])
+    elif kind == "batched":
+        pts = np.random.default_rng(82).random((nb, nd, 4000)).astype(np.float32)
+    else:
+        pts = uniform_points(nd, 5000, 83)
+    batched = pts.ndim == 3
+    nP = pts.shape[-1]
+    As = _As_gpu(T, theta, cuda)
+    Tr = torch.empty_like(As)
+    native().expm(nd, As, 1.0 / 50, Tr)
+    out = torch.empty((nb, nd, nP), device=cuda)
+    sp = torch.empty((K - 1, nb, nd, nP), device=cuda)
+    native().chain_forward(nd, _dev(pts, cuda), batched, nb, K, nP, 50, p.nc, adaptive, Tr, As,
+                           out, sp)
+    A = As.cpu().numpy().reshape(K, nb, p.nC, nd, nd + 1)
+    R = Tr.cpu().numpy().reshape(K, nb, p.nC, nd, nd + 1)
+    xs = [pts]
+    for s in range(K):
+        if nd == 1:
+            xs.append(orc.forward_closed_1d(xs[-1], A[s], p.nc))
+        else:
+            xs.append(orc.forward_trels(xs[-1], R[s], A[s], p.nc, 50, adaptive=bool(adaptive)))
+    np.testing.assert_array_equal(out.cpu().numpy(), xs[-1])
+    for s in range(1, K):
+        np.testing.assert_array_equal(sp[s - 1].cpu().numpy(), xs[s])
+
+    g = np.random.default_rng(84).standard_normal((nb, nd, nP)).astype(np.float32)
+    mom = torch.empty((K * nb, p.nC, nd * (nd + 1)), device=cuda)
+    gp = torch.empty((nb, nd, nP), device=cuda)
+    nbytes = native().chain_backward_workspace_size(nd, nP, nb, K, p.nC)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=cuda) if nbytes else None
+    native().chain_backward(nd, _dev(pts, cuda), batched, nb, K, nP, 50, p.nc, adaptive, sp, As,
+                            _dev(g, cuda), mom, gp, ws)
+    M = mom.cpu().numpy().reshape(K, nb, p.nC, -1)
+    lam = g
+    for s in reversed(range(K)):
+        ref_m, lam = orc.backward(xs[s], A[s], lam, p.nc, 50, adaptive=bool(adaptive))
+        assert_grad_close(M[s], ref_m, rtol=2e-5)
+    np.testing.assert_array_equal(gp.cpu().numpy(), lam)
