@@ -469,10 +469,12 @@ static int check_interp(int ndim, int64_t B, int64_t C, const int64_t* in_size,
   int64_t plane = 1;
   for (int k = 0; k < ndim; ++k) plane *= in_size[k];
   if (plane >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "one data channel must hold < 2^31 values");
-  if (ndim >= 2 && (out_size[ndim - 1] + 63) / 64 >= 65536)
-    return fail(CPAB_ERR_INVALID, "last output size exceeds the grid limit");
-  if (ndim >= 2 && B * (ndim == 3 ? out_size[1] : 1) >= 65536)
-    return fail(CPAB_ERR_INVALID, "n_batch * mid size exceeds the grid limit");
+  if (ndim >= 2) {
+    // one 256-thread workgroup per 32 x 64 tile, 1D grid (< 2^32 threads)
+    const int64_t tiles = div_up(out_size[0], 32) * div_up(out_size[ndim - 1], 64) * B *
+                          (ndim == 3 ? out_size[1] : 1);
+    if (tiles >= (1LL << 23)) return fail(CPAB_ERR_INVALID, "output too large for one launch");
+  }
   return CPAB_OK;
 }
 

@@ -98,7 +98,7 @@ __device__ __forceinline__ int cell_2d_outside(float px, float py, float fx, flo
 
 // Square (cx, cy) holds triangles 4*(cx + cy*nx) + {0 top, 1 right, 2 bottom, 3 left}.
 // Lanes strictly inside (0,1)^2 use the inside rule; if any lane of the wave is
-// outside, a wave-uniform branch applies the boundary rules to those lanes.
+// outside, a wave-uniform branch applies the boundary rules to all its lanes.
 __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   const float fx = (float)nx, fy = (float)ny;
   const float xc = clamp_lookup(px), yc = clamp_lookup(py);
@@ -106,10 +106,16 @@ __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   const float lx = fmaf(xc, fx, -sx), ly = fmaf(yc, fy, -sy);
   const int base = (int)fmaf(sy, fx, sx) << 2;  // exact: cx + cy*nx < 2^24
   int c = base + tri_2d(lx, ly);
-  const bool inside = (px > 0.0f) & (px < 1.0f) & (py > 0.0f) & (py < 1.0f);
-  if (__builtin_amdgcn_ballot_w64(!inside)) {
-    if (!inside) c = cell_2d_outside(px, py, fx, fy, base, lx, ly);
-  }
+  // Wave-wide "any lane outside (0,1)^2": one ballot per compare keeps the
+  // masks in SGPRs (a ballot of a combined bool would first be materialised
+  // in a VGPR and compared back).
+  const uint64_t outside = __builtin_amdgcn_ballot_w64(!(px > 0.0f)) |
+                           __builtin_amdgcn_ballot_w64(!(px < 1.0f)) |
+                           __builtin_amdgcn_ballot_w64(!(py > 0.0f)) |
+                           __builtin_amdgcn_ballot_w64(!(py < 1.0f));
+  // The boundary rules fall through to the inside rule, so lanes that are
+  // inside get the same cell back from them.
+  if (outside) c = cell_2d_outside(px, py, fx, fy, base, lx, ly);
   return c;
 }
 

@@ -26,6 +26,7 @@ constexpr int kT0 = 32;      // tile extent along i0 (grid rows are contiguous i
 constexpr int kTL = 64;      // tile extent along i_last (output rows are contiguous in i_last)
 constexpr int kThreads = 256;
 constexpr int kUnroll = 4;   // outputs in flight per lane in the compute loop
+constexpr int kXcds = 8;     // MI355X: accelerator complex dies, each with its own L2
 
 struct Axis {
   int i0, i1;   // clamped corner indices
@@ -55,6 +56,7 @@ struct Shape {
   int o0, omid, olast;
   int64_t nP;
   int vec4;      // grid rows are 16-byte aligned along i0 (o0 % 4 == 0)
+  int tiles0, tilesl;  // tiles along i0 and i_last
 };
 
 // Offset of (x, y, z) inside one [*in] plane (< 2^31, checked by the caller).
@@ -156,13 +158,26 @@ __device__ __forceinline__ void sample_grad(const Shape& s, const float* __restr
   }
 }
 
-// Tile coordinates: blockIdx.x -> i0 tile, blockIdx.y -> i_last tile,
-// blockIdx.z -> b * omid + i_mid.
-__device__ __forceinline__ void tile_origin(const Shape& s, int& b, int& im, int& t0, int& tl) {
-  b = blockIdx.z / s.omid;
-  im = blockIdx.z - b * s.omid;
-  t0 = blockIdx.x * kT0;
-  tl = blockIdx.y * kTL;
+// Tile of this workgroup, XCD-aware.  The hardware hands consecutive
+// workgroup ids to the 8 XCDs in turn, and each XCD has its own L2; the
+// remap gives XCD x the x-th eighth of the tile list, so an XCD works through
+// whole images (tiles ordered i0 tile, then i_last tile, then b * omid + i_mid)
+// and the gathers of one image share that XCD's L2.  Returns false for the
+// padding workgroups past the last tile.
+__device__ __forceinline__ bool tile_origin(const Shape& s, int& b, int& im, int& t0, int& tl) {
+  const int64_t total = (int64_t)s.tiles0 * s.tilesl * s.B * s.omid;
+  const int64_t per = (total + kXcds - 1) / kXcds;
+  const int64_t n = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  if (n >= total) return false;
+  const int64_t plane = (int64_t)s.tiles0 * s.tilesl;
+  const int z = (int)(n / plane);
+  const int r = (int)(n - (int64_t)z * plane);
+  const int ty = r / s.tiles0;
+  b = z / s.omid;
+  im = z - b * s.omid;
+  t0 = (r - ty * s.tiles0) * kT0;
+  tl = ty * kTL;
+  return true;
 }
 
 // Grid rows of this tile -> LDS crd[k][al][a0] (lanes along i0, float4 when aligned).
@@ -207,7 +222,7 @@ __global__ __launch_bounds__(kThreads) void interp_fwd_kernel(Shape s,
                                                               float* __restrict__ out) {
   __shared__ float crd[ND][kTL][kT0 + 1];
   int b, im, t0, tl;
-  tile_origin(s, b, im, t0, tl);
+  if (!tile_origin(s, b, im, t0, tl)) return;
   const int n0 = min(kT0, s.o0 - t0), nl = min(kTL, s.olast - tl);
   load_tile<ND>(s, grid, b, im, t0, tl, n0, nl, crd);
   __syncthreads();
@@ -239,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void interp_bwd_kernel(Shape s,
                                                               float* __restrict__ grad_data) {
   __shared__ float crd[ND][kTL][kT0 + 1];
   int b, im, t0, tl;
-  tile_origin(s, b, im, t0, tl);
+  if (!tile_origin(s, b, im, t0, tl)) return;
   const int n0 = min(kT0, s.o0 - t0), nl = min(kTL, s.olast - tl);
   load_tile<ND>(s, grid, b, im, t0, tl, n0, nl, crd);
   __syncthreads();
@@ -354,14 +369,16 @@ Shape make_shape(int ndim, int64_t B, int64_t C, const int64_t* in_size, const i
   s.nP = 1;
   for (int k = 0; k < ndim; ++k) s.nP *= out_size[k];
   s.vec4 = (s.o0 % 4) == 0;
+  s.tiles0 = (s.o0 + kT0 - 1) / kT0;
+  s.tilesl = (s.olast + kTL - 1) / kTL;
   return s;
 }
 
 int aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 dim3 tile_grid(const Shape& s) {
-  return dim3((unsigned)((s.o0 + kT0 - 1) / kT0), (unsigned)((s.olast + kTL - 1) / kTL),
-              (unsigned)(s.B * s.omid));
+  const int64_t total = (int64_t)s.tiles0 * s.tilesl * s.B * s.omid;
+  return dim3((unsigned)((total + kXcds - 1) / kXcds * kXcds));
 }
 
 }  // namespace
