@@ -368,8 +368,8 @@ __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g,
       const int c = (t == 0) ? cur : lookup<D>(p, g);
       if (__builtin_amdgcn_ballot_w64(c != cur)) {
         if (c != cur) A = fetch<D>(tab, c);
-        cur = c;
       }
+      cur = c;
       if (t & 1) cells[t >> 1] |= (uint32_t)c << 16;
       else cells[t >> 1] = (uint32_t)c;
 #pragma unroll
@@ -386,16 +386,15 @@ __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g,
 #pragma unroll
     for (int t = TS - 1; t >= 0; --t) {
       const int c = (int)((t & 1) ? (cells[t >> 1] >> 16) : (cells[t >> 1] & 0xffffu));
-      const bool change = c != prev;
-      if (__builtin_amdgcn_ballot_w64(change)) {
-        if (change) {
-          if (prev >= 0 && valid) flush_lds<PP>(bins, prev, m);
+      // Divergent branch: skipped by the hardware (exec = 0) at steps where no
+      // lane of the wave changes cell.
+      if (c != prev) {
+        if (prev >= 0 && valid) flush_lds<PP>(bins, prev, m);
 #pragma unroll
-          for (int k = 0; k < PP; ++k) m[k] = 0.0f;
-          A = fetch<D>(tab, c);
-        }
-        prev = c;
+        for (int k = 0; k < PP; ++k) m[k] = 0.0f;
+        A = fetch<D>(tab, c);
       }
+      prev = c;
       adjoint(A, traj[t], h, hh, hhh, m, lam);
     }
     if (valid) flush_lds<PP>(bins, prev, m);

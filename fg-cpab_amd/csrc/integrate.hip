@@ -170,8 +170,8 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
           const int c = (t == 0) ? cur[k] : cell_2d(px[k], py[k], nx, ny);
           if (__builtin_amdgcn_ballot_w64(c != cur[k])) {
             if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
-            cur[k] = c;
           }
+          cur[k] = c;
           float sx, sy;
           apply2(M[k], px[k], py[k], sx, sy);
           if (ADAPTIVE) {
