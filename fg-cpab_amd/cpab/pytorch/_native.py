@@ -41,6 +41,13 @@ _SIGNATURES = {
     "cpab_chain_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
                                      _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                      _c_vp, _c_vp, _c_i64, _c_vp]),
+    "cpab_transform_data_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int,
+                                             _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
+                                             _c_vp, _c_vp, _c_vp]),
+    "cpab_transform_data_backward_workspace_size": (_c_i64, [_c_int, _c_i64, _c_vp, _c_int]),
+    "cpab_transform_data_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int,
+                                              _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
+                                              _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp]),
     "cpab_project": (_c_int, [_c_i64, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "cpab_sum_batch": (_c_int, [_c_i64, _c_i64, _c_vp, _c_vp, _c_vp]),
     "cpab_interp_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
@@ -164,6 +171,28 @@ class Native:
                                             _ptr(moments), _ptr(grad_points), _ptr(workspace),
                                             wbytes, _stream(points.device)),
                "cpab_chain_backward")
+
+    def transform_data_forward(self, ndim, data, grid, outsize, T, nc, adaptive, Trels, As, out,
+                               final_points):
+        ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
+        _check(self.lib.cpab_transform_data_forward(
+            ndim, data.shape[0], data.shape[1], _lengths(data.shape[2:]), _lengths(outsize),
+            int(T), ncx, ncy, ncz, int(adaptive), _ptr(grid), _ptr(Trels), _ptr(As), _ptr(data),
+            _ptr(out), _ptr(final_points), _stream(data.device)), "cpab_transform_data_forward")
+
+    def transform_data_backward_workspace_size(self, ndim, n_batch, outsize, nC):
+        return int(self.lib.cpab_transform_data_backward_workspace_size(
+            ndim, n_batch, _lengths(outsize), nC))
+
+    def transform_data_backward(self, ndim, data, grid, outsize, T, nc, adaptive, final_points,
+                                As, grad_out, moments, grad_data, workspace):
+        ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
+        wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        _check(self.lib.cpab_transform_data_backward(
+            ndim, data.shape[0], data.shape[1], _lengths(data.shape[2:]), _lengths(outsize),
+            int(T), ncx, ncy, ncz, int(adaptive), _ptr(grid), _ptr(final_points), _ptr(As),
+            _ptr(data), _ptr(grad_out), _ptr(moments), _ptr(grad_data), _ptr(workspace), wbytes,
+            _stream(data.device)), "cpab_transform_data_backward")
 
     def project(self, moments, D, d, col_ptr, row_idx, vals, grad_theta):
         _check(self.lib.cpab_project(moments.shape[0], D, d, _ptr(moments), _ptr(col_ptr),

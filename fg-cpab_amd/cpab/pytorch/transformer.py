@@ -15,12 +15,18 @@ the integrated points ``[n_theta, ndim, nP]`` and differentiates w.r.t. theta
 ``CPAB_chain_transformer`` runs a whole chain of stages (the Python loop of
 ``Cpab.transform_grid_chain``, cpab/cpab.py:237-280) as one forward launch
 (cpab_chain_forward) and one backward launch (cpab_chain_backward).
+
+``CPAB_transform_data`` is ``Cpab.transform_data`` (transform_grid of the
+meshgrid, then interpolate; cpab/cpab.py:295-309) as one forward launch
+(cpab_transform_data_forward) and one backward launch
+(cpab_transform_data_backward): the warped grid never leaves the kernels except
+as the saved final points.
 """
 import torch
 
 from ._native import native
 
-__all__ = ["CPAB_transformer", "CPAB_chain_transformer"]
+__all__ = ["CPAB_transformer", "CPAB_chain_transformer", "CPAB_transform_data"]
 
 
 def CPAB_transformer(points, theta, params, compute_points_grad=False):
@@ -251,3 +257,91 @@ class _CPABChainFunction(torch.autograd.Function):
         lib.project(moments.view(K * n_batch, -1), tab["D"], tab["d"], tab["col_ptr"],
                     tab["row_idx"], tab["vals_t"], grad_theta)
         return gp, grad_theta.view(K, n_batch, tab["d"]), None
+
+
+def CPAB_transform_data(data, theta, grid, outsize, params):
+    """``interpolate(data, CPAB_transformer(grid, theta, params), outsize)`` in
+    one fused forward and one fused backward launch.
+
+    Arguments:
+        data: [n_batch, n_channels, *in_size]
+        theta: [n_batch, d]
+        grid: [ndim, prod(outsize)] meshgrid of ``outsize`` (``Cpab.uniform_meshgrid``)
+        outsize: list of ndim output sizes
+    Returns:
+        [n_batch, n_channels, *outsize]
+    """
+    assert data.is_cuda and theta.is_cuda and grid.is_cuda, "Only GPU tensors supported"
+    assert params.ndim in (1, 2, 3), "GPU transformer supports 1D, 2D, and 3D"
+    return _CPABImageFunction.apply(data, theta, grid, [int(v) for v in outsize], params)
+
+
+class _CPABImageFunction(torch.autograd.Function):
+    """Fused transform_data: integrate the meshgrid and resample in one pass."""
+
+    @staticmethod
+    def forward(ctx, data, theta, grid, outsize, params):
+        ndim, nC = params.ndim, int(params.nC)
+        if data.dtype != torch.float32 or theta.dtype != torch.float32:
+            raise RuntimeError("expected float32 data and theta")
+        if data.dim() != ndim + 2:
+            raise RuntimeError(f"data must be [n_batch, n_channels, *in_size] with {ndim} spatial axes")
+        if theta.dim() != 2 or theta.shape[1] != params.d or theta.shape[0] != data.shape[0]:
+            raise RuntimeError(f"theta must be [n_batch={data.shape[0]}, {params.d}], got {tuple(theta.shape)}")
+        nP = 1
+        for v in outsize:
+            nP *= v
+        if len(outsize) != ndim or tuple(grid.shape) != (ndim, nP):
+            raise RuntimeError("grid must be the [ndim, prod(outsize)] meshgrid of outsize")
+        lib = native()
+        dev = theta.device
+        n = theta.shape[0]
+        tab = basis_tables(params, dev)
+        data_c = data.detach().contiguous()
+        grid_c = grid.detach().contiguous()
+        As = torch.empty((n, nC, ndim, ndim + 1), device=dev, dtype=torch.float32)
+        lib.affine(ndim, theta.detach().contiguous(), nC, tab["row_ptr"], tab["col_idx"],
+                   tab["vals"], As)
+        T = int(params.nstepsolver)
+        adaptive = int(getattr(params, "adaptive_substeps", False))
+        nc = [int(v) for v in params.nc]
+        Trels = None
+        if ndim > 1:
+            Trels = torch.empty_like(As)
+            lib.expm(ndim, As, 1.0 / T, Trels)
+        grad_wanted = ctx.needs_input_grad[0] or ctx.needs_input_grad[1]
+        final = (torch.empty((n, ndim, nP), device=dev, dtype=torch.float32)
+                 if grad_wanted else None)
+        out = torch.empty((n, data.shape[1], *outsize), device=dev, dtype=torch.float32)
+        lib.transform_data_forward(ndim, data_c, grid_c, outsize, T, nc, adaptive, Trels, As, out,
+                                   final)
+        ctx.outsize = list(outsize)
+        ctx.T = T
+        ctx.nc = nc
+        ctx.adaptive = adaptive
+        ctx.params = params
+        ctx.save_for_backward(data_c, grid_c, final, As)
+        return out
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad):
+        data, grid, final, As = ctx.saved_tensors
+        params = ctx.params
+        lib = native()
+        dev = As.device
+        n, nC, ndim = As.shape[0], As.shape[1], As.shape[2]
+        grad = grad.detach().to(torch.float32).contiguous()
+        moments = torch.empty((n, nC, ndim * (ndim + 1)), device=dev, dtype=torch.float32)
+        ws_bytes = lib.transform_data_backward_workspace_size(ndim, n, ctx.outsize, nC)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
+        grad_data = torch.empty_like(data) if ctx.needs_input_grad[0] else None
+        lib.transform_data_backward(ndim, data, grid, ctx.outsize, ctx.T, ctx.nc, ctx.adaptive,
+                                    final, As, grad, moments, grad_data, ws)
+        grad_theta = None
+        if ctx.needs_input_grad[1]:
+            tab = basis_tables(params, dev)
+            grad_theta = torch.empty((n, tab["d"]), device=dev, dtype=torch.float32)
+            lib.project(moments.view(n, -1), tab["D"], tab["d"], tab["col_ptr"], tab["row_idx"],
+                        tab["vals_t"], grad_theta)
+        return grad_data, grad_theta, None, None, None

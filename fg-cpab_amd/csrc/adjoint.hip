@@ -32,6 +32,7 @@
 #include <algorithm>
 #include "cpab_device.hpp"
 #include "cpab_launch.hpp"
+#include "cpab_sample.hpp"
 
 namespace cpab {
 namespace {
@@ -232,16 +233,77 @@ __device__ __forceinline__ void flush_global(float* __restrict__ mom, bool need,
 }
 
 
+// Where the trajectories of one stage start and where their adjoint seed
+// comes from.  PlainIO: point and seed arrays [D, nP] (cpab_backward, chain
+// stages).  ImageIO: the fused transform_data backward, where point q is an
+// output pixel, the trajectory starts at its meshgrid point and the seed is
+// the resampling gradient at the integrated point (the interp backward of
+// cpab_sample.hpp, summed over channels, times size-1), as
+// interpolation.py:3-159 followed by transformer.py:128-168 computes it.
+template <int D>
+struct PlainIO {
+  const float* __restrict__ pts;
+  const float* __restrict__ gout;
+  float* __restrict__ lam_out;
+  int nP;
+  __device__ __forceinline__ void start(int i, float (&p)[D]) const {
+#pragma unroll
+    for (int k = 0; k < D; ++k) p[k] = pts[i + (size_t)k * nP];
+  }
+  __device__ __forceinline__ void seed(int i, bool, float (&lam)[D]) const {
+#pragma unroll
+    for (int k = 0; k < D; ++k) lam[k] = gout[i + (size_t)k * nP];
+  }
+  __device__ __forceinline__ void finish(int i, bool valid, const float (&lam)[D]) const {
+    if (lam_out && valid) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) lam_out[i + (size_t)k * nP] = lam[k];
+    }
+  }
+};
+
+//
+// Trajectory order: 1D/2D walk the points in image order (the seed reads are
+// coalesced, the meshgrid reads strided but L2-resident).  3D walks them in
+// meshgrid order instead: a workgroup's contiguous range is then a slab of
+// whole x-y planes, whose cells have nearly consecutive ids, which is what the
+// direct-mapped LDS cell cache needs (in image order a range spans every z
+// layer and the cache would thrash); the seed reads become the strided ones.
+template <int D>
+struct ImageIO {
+  static constexpr bool kMeshOrder = D == 3;
+  ImageShape s;
+  const float* __restrict__ grid;   // [D, nP] meshgrid (shared by all thetas)
+  const float* __restrict__ fin;    // [D, nP] integrated points of this theta, image order
+  const float* __restrict__ gout;   // [C, nP] image gradient of this theta
+  const float* __restrict__ data;   // [C, plane_in]
+  float* __restrict__ gdata;        // [C, plane_in] or null
+  __device__ __forceinline__ void start(int i, float (&p)[D]) const {
+    const int m = kMeshOrder ? i : mesh_point<D>(s, i);
+#pragma unroll
+    for (int k = 0; k < D; ++k) p[k] = grid[m + (size_t)k * s.nP];
+  }
+  __device__ __forceinline__ void seed(int i, bool valid, float (&lam)[D]) const {
+    const int q = kMeshOrder ? image_point<D>(s, i) : i;
+    const Axis ax = axis_of(fin[q], s.in[0]);
+    const Axis ay = D >= 2 ? axis_of(fin[q + (size_t)s.nP], s.in[1]) : Axis{0, 0, 0.0f};
+    const Axis az = D == 3 ? axis_of(fin[q + 2 * (size_t)s.nP], s.in[2]) : Axis{0, 0, 0.0f};
+    float dd[3] = {0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < s.C; ++c)
+      sample_grad<D>(s.in, data + c * s.plane_in, ax, ay, az, gout[(size_t)c * s.nP + q], dd,
+                     (gdata && valid) ? gdata + c * s.plane_in : nullptr);
+#pragma unroll
+    for (int k = 0; k < D; ++k) lam[k] = dd[k] * (float)(s.in[k] - 1);
+  }
+  __device__ __forceinline__ void finish(int, bool, const float (&)[D]) const {}
+};
+
 // Segmented variant (any T).
-// One stage of one theta over this workgroup's point range: pts = the stage's
-// input points [D, nP], lam_in = dL/d(stage output) [D, nP], lam_out (may be
-// null) receives dL/d(stage input); moments go to bins / keys / mom_b.
-template <int D, bool ADAPTIVE, int BINS, typename P>
-__device__ __forceinline__ void segmented_body(P tab, int nP, int T, const Cells& g,
-                                               const float* __restrict__ pts,
-                                               const float* __restrict__ gout, float* bins,
-                                               int* keys, float* __restrict__ mom_b,
-                                               float* __restrict__ lam_out) {
+// One stage of one theta over this workgroup's point range; moments go to
+// bins / keys / mom_b.
+template <int D, bool ADAPTIVE, int BINS, typename P, typename IO>
+__device__ __forceinline__ void segmented_body(P tab, int nP, int T, const Cells& g, const IO& io,
+                                               float* bins, int* keys, float* __restrict__ mom_b) {
   constexpr int PP = Dim<D>::P;
   const float h = 1.0f / (float)T;
   const float hh = h * 0.5f;
@@ -257,8 +319,7 @@ __device__ __forceinline__ void segmented_body(P tab, int nP, int T, const Cells
     const bool valid = pi0 < hi;
     const int pi = valid ? pi0 : hi - 1;
     float p[D];
-#pragma unroll
-    for (int k = 0; k < D; ++k) p[k] = pts[pi + (size_t)k * nP];
+    io.start(pi, p);
 
     // Phase 1: checkpoint (position before step seg*kSeg) pushed per segment.
     float ck[D][kMaxSeg];
@@ -275,8 +336,7 @@ __device__ __forceinline__ void segmented_body(P tab, int nP, int T, const Cells
 
     // Phase 2: reverse sweep.
     float lam[D];
-#pragma unroll
-    for (int k = 0; k < D; ++k) lam[k] = gout[pi + (size_t)k * nP];
+    io.seed(pi, valid, lam);
     float m[PP];
 #pragma unroll
     for (int k = 0; k < PP; ++k) m[k] = 0.0f;
@@ -326,19 +386,14 @@ __device__ __forceinline__ void segmented_body(P tab, int nP, int T, const Cells
     } else {
       flush_global<PP>(mom_b, valid, prev, m);
     }
-    if (lam_out && valid) {
-#pragma unroll
-      for (int k = 0; k < D; ++k) lam_out[pi + (size_t)k * nP] = lam[k];
-    }
+    io.finish(pi, valid, lam);
   }
 }
 
 // Register variant: T == TS known at compile time, moments in LDS bins.
-template <int D, bool ADAPTIVE, int TS, typename P>
-__device__ __forceinline__ void register_body(P tab, int nP, const Cells& g,
-                                              const float* __restrict__ pts,
-                                              const float* __restrict__ gout, float* bins,
-                                              float* __restrict__ lam_out) {
+template <int D, bool ADAPTIVE, int TS, typename P, typename IO>
+__device__ __forceinline__ void register_body(P tab, int nP, const Cells& g, const IO& io,
+                                              float* bins) {
   constexpr int PP = Dim<D>::P;
   const float h = 1.0f / (float)TS;
   const float hh = h * 0.5f;
@@ -350,11 +405,9 @@ __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g,
     const bool valid = pi0 < hi;
     const int pi = valid ? pi0 : hi - 1;
     float p[D];
-#pragma unroll
-    for (int k = 0; k < D; ++k) p[k] = pts[pi + (size_t)k * nP];
+    io.start(pi, p);
     float lam[D];
-#pragma unroll
-    for (int k = 0; k < D; ++k) lam[k] = gout[pi + (size_t)k * nP];
+    io.seed(pi, valid, lam);
 
     // Phase 1: the whole midpoint trajectory, positions and cells in VGPRs.
     // The current cell's affine block stays in registers and is re-read only
@@ -377,8 +430,7 @@ __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g,
       replay_step_with<D, ADAPTIVE>(tab, A, c, p, h, hh, g);
     }
 
-    // Phase 2: reverse sweep.  The flush test is skipped wave-wide when no
-    // lane changes cell at this step.
+    // Phase 2: reverse sweep.
     float m[PP];
 #pragma unroll
     for (int k = 0; k < PP; ++k) m[k] = 0.0f;
@@ -398,10 +450,68 @@ __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g,
       adjoint(A, traj[t], h, hh, hhh, m, lam);
     }
     if (valid) flush_lds<PP>(bins, prev, m);
-    if (lam_out && valid) {
-#pragma unroll
-      for (int k = 0; k < D; ++k) lam_out[pi + (size_t)k * nP] = lam[k];
+    io.finish(pi, valid, lam);
+  }
+}
+
+// LDS layout of a backward workgroup: [A table (LDS_A)] then either the full
+// bins (R floats) or the cache (kCacheSlots keys, then kCacheSlots * PP floats).
+template <int D, bool LDS_A, int BINS>
+struct StageLds {
+  float* ldsA;
+  int* keys;
+  float* bins;
+  __device__ __forceinline__ StageLds(float* lds, int R) {
+    ldsA = lds;
+    float* after_a = lds + (LDS_A ? R : 0);
+    keys = reinterpret_cast<int*>(after_a);
+    bins = BINS == kBinsCache ? after_a + kCacheSlots : after_a;
+  }
+  // Stage the table, clear the bins / cache.
+  __device__ __forceinline__ void begin(const float* __restrict__ Ag, int R) const {
+    constexpr int PP = Dim<D>::P;
+    if (LDS_A) {
+      const float2* s2 = reinterpret_cast<const float2*>(Ag);
+      float2* d2 = reinterpret_cast<float2*>(ldsA);
+      for (int i = threadIdx.x; i < R / 2; i += blockDim.x) d2[i] = s2[i];
     }
+    if (BINS == kBinsFull) {
+      for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
+    } else if (BINS == kBinsCache) {
+      for (int i = threadIdx.x; i < kCacheSlots; i += blockDim.x) keys[i] = -1;
+      for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) bins[i] = 0.0f;
+    }
+    if (LDS_A || BINS != kBinsGlobal) __syncthreads();
+  }
+  // After every lane is done: full bins -> this workgroup's partial (plain
+  // stores); cache -> HBM atomics of the occupied slots.
+  __device__ __forceinline__ void end(float* __restrict__ partial, float* __restrict__ mom_b,
+                                      int R) const {
+    constexpr int PP = Dim<D>::P;
+    if (LDS_A || BINS != kBinsGlobal) __syncthreads();
+    if (BINS == kBinsFull) {
+      for (int i = threadIdx.x; i < R; i += blockDim.x) partial[i] = bins[i];
+    } else if (BINS == kBinsCache) {
+      for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) {
+        const int slot = i / PP;
+        const int c = keys[slot];
+        if (c >= 0) unsafeAtomicAdd(mom_b + (size_t)PP * c + (i - slot * PP), bins[i]);
+      }
+    }
+  }
+};
+
+template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS, typename IO>
+__device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, const float* Ag,
+                                          int nP, int T, const Cells& g, const IO& io,
+                                          float* __restrict__ mom_b) {
+  if constexpr (TS > 0) {
+    static_assert(BINS == kBinsFull, "the register variant accumulates in full LDS bins");
+    if (LDS_A) register_body<D, ADAPTIVE, TS>(as_lds(L.ldsA), nP, g, io, L.bins);
+    else register_body<D, ADAPTIVE, TS>(Ag, nP, g, io, L.bins);
+  } else {
+    if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(L.ldsA), nP, T, g, io, L.bins, L.keys, mom_b);
+    else segmented_body<D, ADAPTIVE, BINS>(Ag, nP, T, g, io, L.bins, L.keys, mom_b);
   }
 }
 
@@ -419,95 +529,113 @@ __global__ __launch_bounds__(768) void backward_kernel(
     const float* __restrict__ stage_points, const float* __restrict__ As,
     const float* __restrict__ grad_out, float* __restrict__ moments, float* __restrict__ partials,
     float* __restrict__ lam, float* __restrict__ grad_points) {
-  constexpr int PP = Dim<D>::P;
   extern __shared__ float lds[];
   const int b = blockIdx.y;
   const int n_batch = gridDim.y;
-  const int R = nC * PP;
+  const int R = nC * Dim<D>::P;
   const size_t plane = (size_t)D * nP;  // one theta's [D, nP] block
-  float* ldsA = lds;
-  float* after_a = lds + (LDS_A ? R : 0);
-  // full bins: R floats; cache: kCacheSlots keys, then kCacheSlots * PP floats
-  int* keys = reinterpret_cast<int*>(after_a);
-  float* bins = BINS == kBinsCache ? after_a + kCacheSlots : after_a;
+  const StageLds<D, LDS_A, BINS> L(lds, R);
   for (int k = K - 1; k >= 0; --k) {
     const size_t row = (size_t)k * n_batch + b;
     const float* __restrict__ Ag = As + row * R;
-    float* __restrict__ mom_b = moments + row * R;
-    const float* __restrict__ pts =
-        k == 0 ? points + (batched ? (size_t)b * plane : 0) : stage_points + ((size_t)(k - 1) * n_batch + b) * plane;
-    const float* __restrict__ gin = k == K - 1 ? grad_out + (size_t)b * plane : lam + (size_t)b * plane;
-    float* __restrict__ lout = k == 0 ? (grad_points ? grad_points + (size_t)b * plane : nullptr)
-                                      : lam + (size_t)b * plane;
-    if (LDS_A) {
-      const float2* s2 = reinterpret_cast<const float2*>(Ag);
-      float2* d2 = reinterpret_cast<float2*>(ldsA);
-      for (int i = threadIdx.x; i < R / 2; i += blockDim.x) d2[i] = s2[i];
-    }
-    if (BINS == kBinsFull) {
-      for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
-    } else if (BINS == kBinsCache) {
-      for (int i = threadIdx.x; i < kCacheSlots; i += blockDim.x) keys[i] = -1;
-      for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) bins[i] = 0.0f;
-    }
-    if (LDS_A || BINS != kBinsGlobal) __syncthreads();
-    if constexpr (TS > 0) {
-      static_assert(BINS == kBinsFull, "the register variant accumulates in full LDS bins");
-      if (LDS_A) register_body<D, ADAPTIVE, TS>(as_lds(ldsA), nP, g, pts, gin, bins, lout);
-      else register_body<D, ADAPTIVE, TS>(Ag, nP, g, pts, gin, bins, lout);
-    } else {
-      if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(ldsA), nP, T, g, pts, gin, bins, keys, mom_b, lout);
-      else segmented_body<D, ADAPTIVE, BINS>(Ag, nP, T, g, pts, gin, bins, keys, mom_b, lout);
-    }
+    PlainIO<D> io;
+    io.nP = nP;
+    io.pts = k == 0 ? points + (batched ? (size_t)b * plane : 0)
+                    : stage_points + ((size_t)(k - 1) * n_batch + b) * plane;
+    io.gout = k == K - 1 ? grad_out + (size_t)b * plane : lam + (size_t)b * plane;
+    io.lam_out = k == 0 ? (grad_points ? grad_points + (size_t)b * plane : nullptr)
+                        : lam + (size_t)b * plane;
+    L.begin(Ag, R);
+    run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, nP, T, g, io, moments + row * R);
     // Every lane is done with this stage's tables before they are written out
     // (and, for the next stage, overwritten).
-    if (LDS_A || BINS != kBinsGlobal) __syncthreads();
-    if (BINS == kBinsFull) {
-      float* dst = partials + (row * gridDim.x + blockIdx.x) * R;
-      for (int i = threadIdx.x; i < R; i += blockDim.x) dst[i] = bins[i];
-    } else if (BINS == kBinsCache) {
-      for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) {
-        const int slot = i / PP;
-        const int c = keys[slot];
-        if (c >= 0) unsafeAtomicAdd(mom_b + (size_t)PP * c + (i - slot * PP), bins[i]);
-      }
-    }
+    L.end(partials + (row * gridDim.x + blockIdx.x) * R, moments + row * R, R);
     if (k > 0 && (LDS_A || BINS != kBinsGlobal)) __syncthreads();
   }
 }
 
+// Fused transform_data backward: one workgroup = one theta x one contiguous
+// range of output positions.
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
-hipError_t go(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int T, int K,
-              const float* points, const float* stage_points, const float* As,
-              const float* grad_out, float* moments, float* partials, float* lam,
-              float* grad_points, const LaunchCfg& cfg, hipStream_t s) {
-  auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
-  const size_t R = (size_t)geo.nC * Dim<D>::P;
+__global__ __launch_bounds__(768) void image_backward_kernel(
+    ImageShape s, int T, Cells g, int nC, const float* __restrict__ grid,
+    const float* __restrict__ final_points, const float* __restrict__ As,
+    const float* __restrict__ data, const float* __restrict__ grad_out,
+    float* __restrict__ moments, float* __restrict__ partials, float* __restrict__ grad_data) {
+  extern __shared__ float lds[];
+  const int b = blockIdx.y;
+  const int R = nC * Dim<D>::P;
+  const StageLds<D, LDS_A, BINS> L(lds, R);
+  const float* __restrict__ Ag = As + (size_t)b * R;
+  ImageIO<D> io;
+  io.s = s;
+  io.grid = grid;
+  io.fin = final_points + (size_t)b * D * s.nP;
+  io.gout = grad_out + (size_t)b * s.C * s.nP;
+  io.data = data + (size_t)b * s.C * s.plane_in;
+  io.gdata = grad_data ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
+  L.begin(Ag, R);
+  run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, s.nP, T, g, io, moments + (size_t)b * R);
+  L.end(partials + ((size_t)b * gridDim.x + blockIdx.x) * R, moments + (size_t)b * R, R);
+}
+
+template <int D, bool LDS_A, int BINS>
+size_t stage_lds_bytes(int nC) {
+  const size_t R = (size_t)nC * Dim<D>::P;
   size_t lds = LDS_A ? R * sizeof(float) : 0;
   if (BINS == kBinsFull) lds += R * sizeof(float);
   if (BINS == kBinsCache) lds += (size_t)kCacheSlots * (Dim<D>::P + 1) * sizeof(float);
-  if (lds > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  return lds;
+}
+
+template <typename Kern>
+hipError_t allow_lds(Kern kernel, size_t lds) {
+  if (lds <= 65536) return hipSuccess;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+}
+
+// Problem handed to one backward launch (a plain / chain backward, or the fused
+// transform_data backward when `image` is set).
+struct BackwardJob {
+  Geometry geo;
+  int64_t nP, n_batch;
+  int batched, T, K;
+  const float *points, *stage_points, *As, *grad_out;
+  float *moments, *partials, *lam, *grad_points;
+  const ImageShape* image;
+  const float *grid, *final_points, *data;
+  float* grad_data;
+};
+
+template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
+hipError_t go(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
+  const size_t lds = stage_lds_bytes<D, LDS_A, BINS>(j.geo.nC);
+  const Cells g{j.geo.nx, j.geo.ny, j.geo.nz};
+  const dim3 grid((unsigned)cfg.chunks, (unsigned)j.n_batch), block((unsigned)cfg.block);
+  if (j.image) {
+    auto kernel = image_backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
+    hipError_t e = allow_lds(kernel, lds);
     if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, *j.image, j.T, g, j.geo.nC, j.grid,
+                       j.final_points, j.As, j.data, j.grad_out, j.moments, j.partials,
+                       j.grad_data);
+  } else {
+    auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
+    hipError_t e = allow_lds(kernel, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, (int)j.nP, j.batched, j.T, g, j.geo.nC, j.K,
+                       j.points, j.stage_points, j.As, j.grad_out, j.moments, j.partials, j.lam,
+                       j.grad_points);
   }
-  const Cells g{geo.nx, geo.ny, geo.nz};
-  hipLaunchKernelGGL(kernel, dim3((unsigned)cfg.chunks, (unsigned)n_theta), dim3(cfg.block), lds,
-                     s, (int)nP, batched, T, g, geo.nC, K, points, stage_points, As, grad_out,
-                     moments, partials, lam, grad_points);
   return hipGetLastError();
 }
 
 template <int D>
-hipError_t dispatch(const Geometry& geo, int64_t nP, int64_t n_theta, int batched, int T, int K,
-                    int adaptive, const float* points, const float* stage_points, const float* As,
-                    const float* grad_out, float* moments, float* partials, float* lam,
-                    float* grad_points, const LaunchCfg& cfg, hipStream_t s) {
-#define CPAB_GO(AD, LA, LB, TS)                                                                \
-  return go<D, AD, LA, LB, TS>(geo, nP, n_theta, batched, T, K, points, stage_points, As,     \
-                               grad_out, moments, partials, lam, grad_points, cfg, s)
+hipError_t dispatch(const BackwardJob& j, int adaptive, const LaunchCfg& cfg, hipStream_t s) {
+#define CPAB_GO(AD, LA, LB, TS) return go<D, AD, LA, LB, TS>(j, cfg, s)
   if constexpr (D <= 2) {
-    if (cfg.reg_steps == kRegSteps && T == kRegSteps && cfg.lds_bins) {
+    if (cfg.reg_steps == kRegSteps && j.T == kRegSteps && cfg.lds_bins) {
       const int key = (adaptive ? 2 : 0) | (cfg.lds_table ? 1 : 0);
       switch (key) {
         case 0: CPAB_GO(false, false, kBinsFull, kRegSteps);
@@ -536,6 +664,15 @@ hipError_t dispatch(const Geometry& geo, int64_t nP, int64_t n_theta, int batche
 #undef CPAB_GO
 }
 
+hipError_t dispatch_any(const BackwardJob& j, int adaptive, const LaunchCfg& cfg, hipStream_t s) {
+  if (j.nP <= 0 || j.n_batch <= 0 || j.K <= 0) return hipSuccess;
+  switch (j.geo.ndim) {
+    case 1: return dispatch<1>(j, adaptive, cfg, s);
+    case 2: return dispatch<2>(j, adaptive, cfg, s);
+    default: return dispatch<3>(j, adaptive, cfg, s);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
@@ -543,18 +680,45 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
                            const float* As, const float* grad_out, float* moments,
                            float* partials, float* lam, float* grad_points, const LaunchCfg& cfg,
                            hipStream_t s) {
-  if (nP <= 0 || n_batch <= 0 || K <= 0) return hipSuccess;
-  switch (g.ndim) {
-    case 1:
-      return dispatch<1>(g, nP, n_batch, batched, T, K, adaptive, points, stage_points, As,
-                         grad_out, moments, partials, lam, grad_points, cfg, s);
-    case 2:
-      return dispatch<2>(g, nP, n_batch, batched, T, K, adaptive, points, stage_points, As,
-                         grad_out, moments, partials, lam, grad_points, cfg, s);
-    default:
-      return dispatch<3>(g, nP, n_batch, batched, T, K, adaptive, points, stage_points, As,
-                         grad_out, moments, partials, lam, grad_points, cfg, s);
-  }
+  BackwardJob j{};
+  j.geo = g;
+  j.nP = nP;
+  j.n_batch = n_batch;
+  j.batched = batched;
+  j.T = T;
+  j.K = K;
+  j.points = points;
+  j.stage_points = stage_points;
+  j.As = As;
+  j.grad_out = grad_out;
+  j.moments = moments;
+  j.partials = partials;
+  j.lam = lam;
+  j.grad_points = grad_points;
+  return dispatch_any(j, adaptive, cfg, s);
+}
+
+hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
+                                 int adaptive, const float* grid, const float* final_points,
+                                 const float* As, const float* data, const float* grad_out,
+                                 float* moments, float* partials, float* grad_data,
+                                 const LaunchCfg& cfg, hipStream_t s) {
+  BackwardJob j{};
+  j.geo = g;
+  j.nP = img.nP;
+  j.n_batch = n_batch;
+  j.T = T;
+  j.K = 1;
+  j.As = As;
+  j.grad_out = grad_out;
+  j.moments = moments;
+  j.partials = partials;
+  j.image = &img;
+  j.grid = grid;
+  j.final_points = final_points;
+  j.data = data;
+  j.grad_data = grad_data;
+  return dispatch_any(j, adaptive, cfg, s);
 }
 
 }  // namespace cpab

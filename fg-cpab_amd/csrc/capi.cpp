@@ -307,6 +307,33 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   return rc;
 }
 
+// Image geometry of the fused transform_data calls (validated like the
+// resampling entry points, plus the integrator's limits).
+int image_shape(int ndim, int64_t n_batch, int64_t C, const int64_t* in_size,
+                const int64_t* out_size, cpab::ImageShape* img) {
+  if (ndim < 1 || ndim > 3) return fail(CPAB_ERR_INVALID, "ndim must be 1, 2 or 3, got %d", ndim);
+  CPAB_REQUIRE(in_size); CPAB_REQUIRE(out_size);
+  if (n_batch < 0 || C < 1) return fail(CPAB_ERR_INVALID, "need n_batch >= 0 and n_channels >= 1");
+  if (n_batch >= 65536) return fail(CPAB_ERR_INVALID, "n_batch=%lld exceeds the grid limit 65535", (long long)n_batch);
+  int64_t nP = 1, plane = 1;
+  for (int k = 0; k < ndim; ++k) {
+    if (in_size[k] < 1 || out_size[k] < 1) return fail(CPAB_ERR_INVALID, "sizes must be >= 1 (axis %d)", k);
+    nP *= out_size[k];
+    plane *= in_size[k];
+    if (nP >= (1LL << 31) || plane >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "image too large");
+  }
+  if (n_batch * C * std::max(nP, plane) >= (1LL << 40)) return fail(CPAB_ERR_INVALID, "problem too large");
+  *img = cpab::ImageShape{};
+  for (int k = 0; k < 3; ++k) {
+    img->o[k] = k < ndim ? (int)out_size[k] : 1;
+    img->in[k] = k < ndim ? (int)in_size[k] : 1;
+  }
+  img->C = (int)C;
+  img->nP = (int)nP;
+  img->plane_in = plane;
+  return CPAB_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -403,6 +430,87 @@ int cpab_chain_backward(int ndim, int64_t nP, int64_t n_batch, int batched, int 
   return backward_impl("cpab_chain_backward", ndim, nP, n_batch, batched, n_stages, nstepsolver,
                        ncx, ncy, ncz, adaptive, points, stage_points, As, grad_out, moments,
                        grad_points, workspace, workspace_bytes, stream);
+}
+
+int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
+                                const int64_t* in_size, const int64_t* out_size, int nstepsolver,
+                                int ncx, int ncy, int ncz, int adaptive, const float* grid,
+                                const float* Trels, const float* As, const float* data,
+                                float* out, float* final_points, void* stream) {
+  cpab::Geometry g{};
+  int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
+  if (rc) return rc;
+  if (ndim > 1 && (rc = check_steps(nstepsolver))) return rc;
+  if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
+  cpab::ImageShape img;
+  if ((rc = image_shape(ndim, n_batch, n_channels, in_size, out_size, &img))) return rc;
+  if (n_batch == 0) return CPAB_OK;
+  CPAB_REQUIRE(grid); CPAB_REQUIRE(As); CPAB_REQUIRE(data); CPAB_REQUIRE(out);
+  if (ndim > 1) CPAB_REQUIRE(Trels);
+  hipStream_t s = as_stream(stream);
+  const cpab::LaunchCfg cfg = forward_cfg(g, img.nP, n_batch);
+  hipEvent_t ev;
+  const bool timed = prof_begin(s, &ev);
+  rc = check_hip(cpab::launch_image_forward(g, img, n_batch, nstepsolver, adaptive, grid, Trels,
+                                            As, data, out, final_points, cfg, s),
+                 "cpab_transform_data_forward");
+  prof_end(timed, ev, "image_forward", s);
+  return rc;
+}
+
+int64_t cpab_transform_data_backward_workspace_size(int ndim, int64_t n_batch,
+                                                    const int64_t* out_size, int nC) {
+  if (ndim < 1 || ndim > 3 || out_size == nullptr) return 0;
+  int64_t nP = 1;
+  for (int k = 0; k < ndim; ++k) nP *= std::max<int64_t>(out_size[k], 0);
+  return workspace_size_impl(ndim, nP, n_batch, 1, nC);
+}
+
+int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
+                                 const int64_t* in_size, const int64_t* out_size, int nstepsolver,
+                                 int ncx, int ncy, int ncz, int adaptive, const float* grid,
+                                 const float* final_points, const float* As, const float* data,
+                                 const float* grad_out, float* moments, float* grad_data,
+                                 void* workspace, int64_t workspace_bytes, void* stream) {
+  cpab::Geometry g{};
+  int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
+  if (rc) return rc;
+  if ((rc = check_steps(nstepsolver))) return rc;
+  if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
+  cpab::ImageShape img;
+  if ((rc = image_shape(ndim, n_batch, n_channels, in_size, out_size, &img))) return rc;
+  if (n_batch == 0) return CPAB_OK;
+  CPAB_REQUIRE(grid); CPAB_REQUIRE(final_points); CPAB_REQUIRE(As); CPAB_REQUIRE(data);
+  CPAB_REQUIRE(grad_out); CPAB_REQUIRE(moments);
+  hipStream_t s = as_stream(stream);
+  const int R = g.nC * g.ppc();
+  const cpab::LaunchCfg cfg = backward_cfg(g, img.nP, n_batch, nstepsolver);
+  const BackwardWorkspace w = backward_workspace(g, img.nP, n_batch, 1, cfg);
+  if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
+    return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
+                (long long)w.total, (long long)workspace_bytes);
+  if (!cfg.lds_bins) {
+    rc = check_hip(cpab::launch_fill(moments, n_batch * R, 0.0f, s), "cpab_transform_data_backward");
+    if (rc) return rc;
+  }
+  if (grad_data) {
+    rc = check_hip(cpab::launch_fill(grad_data, n_batch * n_channels * img.plane_in, 0.0f, s),
+                   "cpab_transform_data_backward");
+    if (rc) return rc;
+  }
+  hipEvent_t ev;
+  const bool timed = prof_begin(s, &ev);
+  rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, grid,
+                                             final_points, As, data, grad_out, moments,
+                                             static_cast<float*>(workspace), grad_data, cfg, s),
+                 "cpab_transform_data_backward");
+  prof_end(timed, ev, "image_backward", s);
+  if (rc) return rc;
+  if (cfg.lds_bins)
+    rc = check_hip(cpab::launch_reduce_partials(n_batch, cfg.chunks, R,
+                                                static_cast<float*>(workspace), moments, s),
+                   "cpab_transform_data_backward");
+  return rc;
 }
 
 int cpab_project(int64_t n_theta, int D, int d, const float* moments, const int32_t* col_ptr,

@@ -4,6 +4,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "cpab_sample.hpp"
 
 namespace cpab {
 
@@ -57,6 +58,17 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
                            const float* As, const float* grad_out, float* moments,
                            float* partials, float* lam, float* grad_points, const LaunchCfg& cfg,
                            hipStream_t s);
+
+// Fused transform_data (image-ordered outputs; see cpab_sample.hpp ImageShape).
+hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
+                                int adaptive, const float* grid, const float* Trels,
+                                const float* As, const float* data, float* out,
+                                float* final_points, const LaunchCfg& cfg, hipStream_t s);
+hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
+                                 int adaptive, const float* grid, const float* final_points,
+                                 const float* As, const float* data, const float* grad_out,
+                                 float* moments, float* partials, float* grad_data,
+                                 const LaunchCfg& cfg, hipStream_t s);
 
 hipError_t launch_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
                                  const int64_t* out_size, const float* data, const float* grid,

@@ -16,6 +16,7 @@
 #include <math.h>
 #include "cpab_device.hpp"
 #include "cpab_launch.hpp"
+#include "cpab_sample.hpp"
 
 namespace cpab {
 namespace {
@@ -103,6 +104,77 @@ __device__ __forceinline__ void stage(float* __restrict__ dst, const float* __re
   for (int i = threadIdx.x; i < n / 2; i += blockDim.x) d2[i] = s2[i];
 }
 
+// T fixed steps of one transform for PPT points per lane (2D).  The one-step
+// map of the current cell stays in registers; it is re-read (LDS / L1) only at
+// steps where some lane of the wave changed cell, which keeps table traffic and
+// LDS bank conflicts off most steps.  With adaptive_substeps a step that
+// leaves its cell is redone with Heun's rule (cpab_ops_2d.cu:202-219).
+template <bool ADAPTIVE, bool LDS, int PPT>
+__device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT], float* lds,
+                                         const float* __restrict__ Tg,
+                                         const float* __restrict__ Ag, int T, int nx, int ny,
+                                         float hh) {
+  int cur[PPT];
+  Aff<2> M[PPT];
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    cur[k] = cell_2d(px[k], py[k], nx, ny);
+    M[k] = LDS ? load_aff2(as_lds(lds), cur[k]) : load_aff2(Tg, cur[k]);
+  }
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int c = (t == 0) ? cur[k] : cell_2d(px[k], py[k], nx, ny);
+      if (__builtin_amdgcn_ballot_w64(c != cur[k])) {
+        if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
+      }
+      cur[k] = c;
+      float sx, sy;
+      apply2(M[k], px[k], py[k], sx, sy);
+      if (ADAPTIVE) {
+        const int ce = cell_2d(sx, sy, nx, ny);
+        if (ce != c) {
+          float v0x, v0y, v1x, v1y;
+          apply2(load_aff2(Ag, c), px[k], py[k], v0x, v0y);
+          apply2(load_aff2(Ag, ce), sx, sy, v1x, v1y);
+          sx = fmaf(hh, v0x + v1x, px[k]);
+          sy = fmaf(hh, v0y + v1y, py[k]);
+        }
+      }
+      px[k] = sx;
+      py[k] = sy;
+    }
+  }
+}
+
+// T fixed steps of one transform for one point (3D, cpab_ops_3d.cu:169-241).
+template <bool ADAPTIVE, bool LDS>
+__device__ __forceinline__ void steps_3d(float& px, float& py, float& pz, float* lds,
+                                         const float* __restrict__ Tg,
+                                         const float* __restrict__ Ag, int T, int nx, int ny,
+                                         int nz, float hh) {
+  for (int t = 0; t < T; ++t) {
+    const int c = cell_3d(px, py, pz, nx, ny, nz);
+    const Aff<3> M = LDS ? load_aff3(as_lds(lds), c) : load_aff3(Tg, c);
+    float sx, sy, sz;
+    apply3(M, px, py, pz, sx, sy, sz);
+    if (ADAPTIVE) {
+      const int ce = cell_3d(sx, sy, sz, nx, ny, nz);
+      if (ce != c) {
+        float v0x, v0y, v0z, v1x, v1y, v1z;
+        apply3(load_aff3(Ag, c), px, py, pz, v0x, v0y, v0z);
+        apply3(load_aff3(Ag, ce), sx, sy, sz, v1x, v1y, v1z);
+        sx = fmaf(hh, v0x + v1x, px);
+        sy = fmaf(hh, v0y + v1y, py);
+        sz = fmaf(hh, v0z + v1z, pz);
+      }
+    }
+    px = sx;
+    py = sy;
+    pz = sz;
+  }
+}
+
 // PPT independent trajectories per lane give the scheduler two dependency
 // chains (lookup -> table read -> affine apply) to interleave.
 //
@@ -154,40 +226,7 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
           }
         }
       }
-      // The one-step map of the current cell stays in registers; it is
-      // re-read (LDS / L1) only at steps where some lane of the wave changed
-      // cell, which keeps table traffic and LDS bank conflicts off most steps.
-      int cur[PPT];
-      Aff<2> M[PPT];
-#pragma unroll
-      for (int k = 0; k < PPT; ++k) {
-        cur[k] = cell_2d(px[k], py[k], nx, ny);
-        M[k] = LDS ? load_aff2(as_lds(lds), cur[k]) : load_aff2(Tg, cur[k]);
-      }
-      for (int t = 0; t < T; ++t) {
-#pragma unroll
-        for (int k = 0; k < PPT; ++k) {
-          const int c = (t == 0) ? cur[k] : cell_2d(px[k], py[k], nx, ny);
-          if (__builtin_amdgcn_ballot_w64(c != cur[k])) {
-            if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
-          }
-          cur[k] = c;
-          float sx, sy;
-          apply2(M[k], px[k], py[k], sx, sy);
-          if (ADAPTIVE) {
-            const int ce = cell_2d(sx, sy, nx, ny);
-            if (ce != c) {
-              float v0x, v0y, v1x, v1y;
-              apply2(load_aff2(Ag, c), px[k], py[k], v0x, v0y);
-              apply2(load_aff2(Ag, ce), sx, sy, v1x, v1y);
-              sx = fmaf(hh, v0x + v1x, px[k]);
-              sy = fmaf(hh, v0y + v1y, py[k]);
-            }
-          }
-          px[k] = sx;
-          py[k] = sy;
-        }
-      }
+      steps_2d<ADAPTIVE, LDS, PPT>(px, py, lds, Tg, Ag, T, nx, ny, hh);
     }  // stages
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
@@ -231,26 +270,7 @@ __global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T,
         sp[p + nP] = py;
         sp[p + 2 * (size_t)nP] = pz;
       }
-      for (int t = 0; t < T; ++t) {
-        const int c = cell_3d(px, py, pz, nx, ny, nz);
-        const Aff<3> M = LDS ? load_aff3(as_lds(lds), c) : load_aff3(Tg, c);
-        float sx, sy, sz;
-        apply3(M, px, py, pz, sx, sy, sz);
-        if (ADAPTIVE) {
-          const int ce = cell_3d(sx, sy, sz, nx, ny, nz);
-          if (ce != c) {
-            float v0x, v0y, v0z, v1x, v1y, v1z;
-            apply3(load_aff3(Ag, c), px, py, pz, v0x, v0y, v0z);
-            apply3(load_aff3(Ag, ce), sx, sy, sz, v1x, v1y, v1z);
-            sx = fmaf(hh, v0x + v1x, px);
-            sy = fmaf(hh, v0y + v1y, py);
-            sz = fmaf(hh, v0z + v1z, pz);
-          }
-        }
-        px = sx;
-        py = sy;
-        pz = sz;
-      }
+      steps_3d<ADAPTIVE, LDS>(px, py, pz, lds, Tg, Ag, T, nx, ny, nz, hh);
     }  // stages
     o[p] = px;
     o[p + nP] = py;
@@ -258,6 +278,55 @@ __global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T,
   }
 }
 
+
+// Fused transform_data forward (cpab/cpab.py:295-309): output position q
+// (image order, last axis fastest) integrates its meshgrid point under theta b
+// exactly as cpab_forward / the 1D closed form does, then samples every
+// channel of data there exactly as cpab_interp_forward does.  Lanes run along
+// the image's fast axis, so the image stores (and final_points, kept in the
+// same order for the backward) are coalesced; the meshgrid reads are strided
+// but hit L2 (the grid is shared by all thetas).
+template <int ND, bool ADAPTIVE>
+__global__ __launch_bounds__(1024) void image_forward_kernel(
+    ImageShape s, int T, int nx, int ny, int nz, const float* __restrict__ grid,
+    const float* __restrict__ Trels, const float* __restrict__ As,
+    const float* __restrict__ data, float* __restrict__ out, float* __restrict__ final_points) {
+  const int b = blockIdx.y;
+  constexpr int P = ND * (ND + 1);
+  const int nC = ND == 1 ? nx : (ND == 2 ? 4 * nx * ny : 5 * nx * ny * nz);
+  const float* __restrict__ Tg = Trels + (size_t)b * nC * P;
+  const float* __restrict__ Ag = As + (size_t)b * nC * P;
+  const float hh = 0.5f / (float)T;
+  const float* __restrict__ dat = data + (size_t)b * s.C * s.plane_in;
+  float* __restrict__ o = out + (size_t)b * s.C * s.nP;
+  float* __restrict__ fin = final_points ? final_points + (size_t)b * ND * s.nP : nullptr;
+  for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < s.nP; q += gridDim.x * blockDim.x) {
+    const int m = mesh_point<ND>(s, q);
+    float x[3];
+    x[0] = grid[m];
+    x[1] = ND >= 2 ? grid[m + (size_t)s.nP] : 0.0f;
+    x[2] = ND == 3 ? grid[m + 2 * (size_t)s.nP] : 0.0f;
+    if (ND == 1) {
+      x[0] = closed_form_1d(x[0], 1.0f, Ag, nx);
+    } else if (ND == 2) {
+      float px[1] = {x[0]}, py[1] = {x[1]};
+      steps_2d<ADAPTIVE, false, 1>(px, py, nullptr, Tg, Ag, T, nx, ny, hh);
+      x[0] = px[0];
+      x[1] = py[0];
+    } else {
+      steps_3d<ADAPTIVE, false>(x[0], x[1], x[2], nullptr, Tg, Ag, T, nx, ny, nz, hh);
+    }
+    if (fin) {
+#pragma unroll
+      for (int k = 0; k < ND; ++k) fin[q + (size_t)k * s.nP] = x[k];
+    }
+    const Axis ax = axis_of(x[0], s.in[0]);
+    const Axis ay = ND >= 2 ? axis_of(x[1], s.in[1]) : Axis{0, 0, 0.0f};
+    const Axis az = ND == 3 ? axis_of(x[2], s.in[2]) : Axis{0, 0, 0.0f};
+    for (int c = 0; c < s.C; ++c)
+      o[(size_t)c * s.nP + q] = sample<ND>(s.in, dat + c * s.plane_in, ax, ay, az);
+  }
+}
 
 // Cell index visited at every step of the fixed-step forward, for parity tests
 // of the visited-cell sequence (same stepping as fwd2d/fwd3d, table read from
@@ -391,6 +460,30 @@ hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_batch, int ba
   };
   if (adaptive) return lds_table ? go(fwd3d_kernel<true, true>) : go(fwd3d_kernel<true, false>);
   return lds_table ? go(fwd3d_kernel<false, true>) : go(fwd3d_kernel<false, false>);
+}
+
+hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
+                                int adaptive, const float* grid, const float* Trels,
+                                const float* As, const float* data, float* out,
+                                float* final_points, const LaunchCfg& cfg, hipStream_t s) {
+  if (img.nP <= 0 || n_batch <= 0) return hipSuccess;
+  const int64_t need = (img.nP + (int64_t)cfg.block - 1) / cfg.block;
+  const dim3 blocks((unsigned)std::max<int64_t>(1, std::min<int64_t>(cfg.chunks, need)),
+                    (unsigned)n_batch);
+  const dim3 threads((unsigned)cfg.block);
+  auto go = [&](auto kernel) -> hipError_t {
+    hipLaunchKernelGGL(kernel, blocks, threads, 0, s, img, T, g.nx, g.ny, g.nz, grid, Trels, As,
+                       data, out, final_points);
+    return hipGetLastError();
+  };
+  switch (g.ndim * 2 + (adaptive ? 1 : 0)) {
+    case 2: return go(image_forward_kernel<1, false>);
+    case 3: return go(image_forward_kernel<1, true>);
+    case 4: return go(image_forward_kernel<2, false>);
+    case 5: return go(image_forward_kernel<2, true>);
+    case 6: return go(image_forward_kernel<3, false>);
+    default: return go(image_forward_kernel<3, true>);
+  }
 }
 
 hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, int batched, int T,

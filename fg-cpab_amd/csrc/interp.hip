@@ -11,13 +11,11 @@
 // coalesced along i0 into LDS, and computes/writes with i_last across the
 // lanes (coalesced output and, for smooth warps, near-contiguous data rows).
 // The backward does the same transpose in the other direction for grad_grid.
-//
-// Arithmetic follows the reference's eager torch ops one by one (no fused
-// multiply-add): x = g*(W-1); x0 = clamp(floor(x)); xd = x - x0;
-// lerp(a, b, t) = a*(1-t) + b*t with the axes reduced x, then y, then z.
+// The per-sample arithmetic lives in cpab_sample.hpp.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include "cpab_launch.hpp"
+#include "cpab_sample.hpp"
 
 namespace cpab {
 namespace {
@@ -28,27 +26,6 @@ constexpr int kThreads = 256;
 constexpr int kUnroll = 4;   // outputs in flight per lane in the compute loop
 constexpr int kXcds = 8;     // MI355X: accelerator complex dies, each with its own L2
 
-struct Axis {
-  int i0, i1;   // clamped corner indices
-  float t;      // fractional weight of i1
-};
-
-__device__ __forceinline__ Axis axis_of(float g, int size) {
-  const float x = g * (float)(size - 1);
-  const float f = floorf(x);
-  const float hi = (float)(size - 1);
-  // floor -> clamp to [0, size-1] (integer semantics of the reference; done in
-  // float first so out-of-range values cannot overflow the conversion).
-  const int a = (int)fminf(fmaxf(f, 0.0f), hi);
-  const int b = (int)fminf(fmaxf(f + 1.0f, 0.0f), hi);
-  return {a, b, x - (float)a};
-}
-
-__device__ __forceinline__ float lerp_ref(float a, float b, float t) {
-  const float u = 1.0f - t;
-  return __fadd_rn(__fmul_rn(a, u), __fmul_rn(b, t));
-}
-
 struct Shape {
   int ndim;
   int B, C;
@@ -58,105 +35,6 @@ struct Shape {
   int vec4;      // grid rows are 16-byte aligned along i0 (o0 % 4 == 0)
   int tiles0, tilesl;  // tiles along i0 and i_last
 };
-
-// Offset of (x, y, z) inside one [*in] plane (< 2^31, checked by the caller).
-template <int ND>
-__device__ __forceinline__ int plane_index(const Shape& s, int x, int y, int z) {
-  if (ND == 2) return x * s.in[1] + y;
-  return (x * s.in[1] + y) * s.in[2] + z;
-}
-
-template <int ND>
-__device__ __forceinline__ float sample(const Shape& s, const float* __restrict__ d,
-                                        const Axis& ax, const Axis& ay, const Axis& az) {
-  if (ND == 2) {
-    const float c00 = d[plane_index<2>(s, ax.i0, ay.i0, 0)];
-    const float c01 = d[plane_index<2>(s, ax.i0, ay.i1, 0)];
-    const float c10 = d[plane_index<2>(s, ax.i1, ay.i0, 0)];
-    const float c11 = d[plane_index<2>(s, ax.i1, ay.i1, 0)];
-    return lerp_ref(lerp_ref(c00, c10, ax.t), lerp_ref(c01, c11, ax.t), ay.t);
-  }
-  float c[2][2][2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int e = 0; e < 2; ++e)
-        c[a][b][e] = d[plane_index<3>(s, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, e ? az.i1 : az.i0)];
-  const float c00 = lerp_ref(c[0][0][0], c[1][0][0], ax.t);
-  const float c01 = lerp_ref(c[0][0][1], c[1][0][1], ax.t);
-  const float c10 = lerp_ref(c[0][1][0], c[1][1][0], ax.t);
-  const float c11 = lerp_ref(c[0][1][1], c[1][1][1], ax.t);
-  return lerp_ref(lerp_ref(c00, c10, ay.t), lerp_ref(c01, c11, ay.t), az.t);
-}
-
-// d out / d (x, y, z) for one channel with upstream gradient g (before the
-// (size-1) chain factor), and the corner scatter for grad_data.
-template <int ND>
-__device__ __forceinline__ void sample_grad(const Shape& s, const float* __restrict__ d,
-                                            const Axis& ax, const Axis& ay, const Axis& az,
-                                            float g, float* dxyz, float* __restrict__ gd) {
-  const float ux = 1.0f - ax.t, uy = 1.0f - ay.t, uz = 1.0f - az.t;
-  if (ND == 2) {
-    const int i00 = plane_index<2>(s, ax.i0, ay.i0, 0), i01 = plane_index<2>(s, ax.i0, ay.i1, 0);
-    const int i10 = plane_index<2>(s, ax.i1, ay.i0, 0), i11 = plane_index<2>(s, ax.i1, ay.i1, 0);
-    if (dxyz) {
-      const float c00 = d[i00], c01 = d[i01], c10 = d[i10], c11 = d[i11];
-      const float c0 = lerp_ref(c00, c10, ax.t), c1 = lerp_ref(c01, c11, ax.t);
-      dxyz[0] += g * uy * (c10 - c00) + g * ay.t * (c11 - c01);
-      dxyz[1] += g * (c1 - c0);
-    }
-    if (gd) {
-      const float g0 = g * uy, g1 = g * ay.t;
-      unsafeAtomicAdd(gd + i00, g0 * ux);
-      unsafeAtomicAdd(gd + i10, g0 * ax.t);
-      unsafeAtomicAdd(gd + i01, g1 * ux);
-      unsafeAtomicAdd(gd + i11, g1 * ax.t);
-    }
-    return;
-  }
-  int idx[2][2][2];
-  float c[2][2][2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        idx[a][b][e] = plane_index<3>(s, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, e ? az.i1 : az.i0);
-        c[a][b][e] = dxyz ? d[idx[a][b][e]] : 0.0f;
-      }
-  if (dxyz) {
-    // Along x: the four (y, z) lines; along y: the two z planes; along z: the two halves.
-    const float wyz[2][2] = {{uy * uz, uy * az.t}, {ay.t * uz, ay.t * az.t}};
-    float gx = 0.0f;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int e = 0; e < 2; ++e) gx += wyz[b][e] * (c[1][b][e] - c[0][b][e]);
-    const float c00 = lerp_ref(c[0][0][0], c[1][0][0], ax.t);
-    const float c01 = lerp_ref(c[0][0][1], c[1][0][1], ax.t);
-    const float c10 = lerp_ref(c[0][1][0], c[1][1][0], ax.t);
-    const float c11 = lerp_ref(c[0][1][1], c[1][1][1], ax.t);
-    const float gy = uz * (c10 - c00) + az.t * (c11 - c01);
-    const float gz = lerp_ref(c01, c11, ay.t) - lerp_ref(c00, c10, ay.t);
-    dxyz[0] += g * gx;
-    dxyz[1] += g * gy;
-    dxyz[2] += g * gz;
-  }
-  if (gd) {
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float w = (a ? ax.t : ux) * (b ? ay.t : uy) * (e ? az.t : uz);
-          unsafeAtomicAdd(gd + idx[a][b][e], g * w);
-        }
-  }
-}
 
 // Tile of this workgroup, XCD-aware.  The hardware hands consecutive
 // workgroup ids to the 8 XCDs in turn, and each XCD has its own L2; the
@@ -240,7 +118,7 @@ __global__ __launch_bounds__(kThreads) void interp_fwd_kernel(Shape s,
       const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
       const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
       const Axis az = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
-      o[(int64_t)(t0 + a0) * s.omid * s.olast] = sample<ND>(s, d, ax, ay, az);
+      o[(int64_t)(t0 + a0) * s.omid * s.olast] = sample<ND>(s.in, d, ax, ay, az);
     }
   }
 }
@@ -272,7 +150,7 @@ __global__ __launch_bounds__(kThreads) void interp_bwd_kernel(Shape s,
       float dd[3] = {0.0f, 0.0f, 0.0f};
       for (int ch = 0; ch < s.C; ++ch) {
         const int64_t bc = (int64_t)b * s.C + ch;
-        sample_grad<ND>(s, data + bc * plane_in, ax, ay, az, grad_out[bc * plane_out + o],
+        sample_grad<ND>(s.in, data + bc * plane_in, ax, ay, az, grad_out[bc * plane_out + o],
                         grad_grid ? dd : nullptr, grad_data ? grad_data + bc * plane_in : nullptr);
       }
       if (grad_grid) {

@@ -135,6 +135,42 @@ int cpab_project(int64_t n_theta, int D, int d, const float* moments,
  * shared points, cpab/pytorch/transformer.py:151-152. */
 int cpab_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, void* stream);
 
+/* Fused Cpab.transform_data forward (cpab/cpab.py:295-309: uniform_meshgrid ->
+ * transform_grid -> interpolate, i.e. cpab_forward followed by
+ * cpab_interp_forward).  grid: the meshgrid [ndim, prod(out_size)], coordinate 0
+ * fastest (uniform_meshgrid's layout), shared by all n_batch thetas; Trels / As
+ * [n_batch, nC, ndim, ndim+1] (Trels unused in 1D, may be NULL); data
+ * [n_batch, C, *in_size]; out [n_batch, C, *out_size].  Each output pixel
+ * integrates its meshgrid point with cpab_forward's arithmetic and samples
+ * data there with cpab_interp_forward's, so out equals the unfused pair bit
+ * for bit.  final_points (may be NULL): the integrated points
+ * [n_batch, ndim, prod(out_size)] in IMAGE order (last output axis fastest),
+ * which cpab_transform_data_backward takes.  No counterpart entry point in
+ * the reference, whose transform_data is three separate steps. */
+int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
+                                const int64_t* in_size, const int64_t* out_size, int nstepsolver,
+                                int ncx, int ncy, int ncz, int adaptive, const float* grid,
+                                const float* Trels, const float* As, const float* data,
+                                float* out, float* final_points, void* stream);
+
+/* Bytes of device workspace cpab_transform_data_backward needs. */
+int64_t cpab_transform_data_backward_workspace_size(int ndim, int64_t n_batch,
+                                                    const int64_t* out_size, int nC);
+
+/* Backward of cpab_transform_data_forward in one launch: the resampling
+ * gradient at each final point (the interp backward, summed over channels)
+ * seeds the adjoint of that pixel's trajectory, as the reference's autograd
+ * does through interpolate's backward and cpab_gpu.backward_moments_and_points
+ * (transformer_cuda.cpp:122-153).  moments [n_batch, nC, ndim*(ndim+1)]
+ * (overwritten); grad_data [n_batch, C, *in_size] (may be NULL; overwritten).
+ * grad_out is the image gradient [n_batch, C, *out_size]. */
+int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
+                                 const int64_t* in_size, const int64_t* out_size, int nstepsolver,
+                                 int ncx, int ncy, int ncz, int adaptive, const float* grid,
+                                 const float* final_points, const float* As, const float* data,
+                                 const float* grad_out, float* moments, float* grad_data,
+                                 void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Border-clamped linear/bilinear/trilinear resampling of data
  * [n_batch, C, *in_size] at grid [n_batch, ndim, prod(out_size)] (coordinate 0
  * fastest) into out [n_batch, C, *out_size].
@@ -156,7 +192,8 @@ int cpab_interp_backward(int ndim, int64_t n_batch, int64_t n_channels, const in
  * While enabled, HIP events are recorded on the launch stream around the
  * hot kernels ("forward": the forward integrator, fixed-step or 1D closed form;
  * "backward": the fused replay/adjoint kernel; "interp_forward" /
- * "interp_backward": the resampling kernels).  cpab_profile_read waits for and sums the
+ * "interp_backward": the resampling kernels; "image_forward" /
+ * "image_backward": the fused transform_data kernels).  cpab_profile_read waits for and sums the
  * recorded launches of one kernel and forgets them. */
 void cpab_profile_enable(int on);
 int cpab_profile_read(const char* kernel, double* total_ms, int64_t* launches);

@@ -94,6 +94,33 @@ def test_transform_data(cuda, tess, ins):
     assert_grad_close(th.grad.cpu().numpy(), ref_gth, rtol=1e-3, atol_frac=1e-4)
 
 
+def test_transform_data_data_gradient(cuda):
+    # data and theta both require grad (e.g. a learned template image): the
+    # fused backward returns both.
+    T = cpab_for([6, 6])
+    B, C, ins, outs = 2, 3, (30, 26), [24, 28]
+    rng = np.random.default_rng(35)
+    data = rng.random((B, C, *ins)).astype(np.float32)
+    theta = seeded_theta(T, B, 0.5, 36)
+    d_t = torch.tensor(data, device=cuda, requires_grad=True)
+    th = torch.tensor(theta, device=cuda, requires_grad=True)
+    out = T.transform_data(d_t, th, outs)
+    gout = rng.standard_normal(out.shape).astype(np.float32)
+    out.backward(torch.tensor(gout, device=cuda))
+    grid = T.uniform_meshgrid(outs).cpu().numpy()
+    p = T.params
+    As = orc.affine(theta, p.basis).reshape(B, p.nC, 2, 3)
+    grid_t = orc.forward_trels(grid, orc.expm(2, As, 1 / 50), As, p.nc, 50)
+    _, rd = orc.interp_backward(2, data, grid_t, outs, gout)
+    _, mag = orc.interp_backward(2, data, grid_t, outs, np.abs(gout), dtype=np.float64)
+    err = np.abs(d_t.grad.cpu().numpy().astype(np.float64) - rd)
+    assert (err <= 1e-4 * mag + 1e-12).all()
+    assert th.grad is not None and torch.isfinite(th.grad).all()
+    # theta only (data without grad) and no grad at all also run
+    out2 = T.transform_data(torch.tensor(data, device=cuda), th.detach(), outs)
+    np.testing.assert_array_equal(out2.cpu().numpy(), out.detach().cpu().numpy())
+
+
 def test_transform_grid_chain(cuda):
     T = cpab_for([16, 16])
     K = 8

@@ -308,3 +308,60 @@ def test_chain_matches_stagewise(cuda, tess, kind, adaptive):
         ref_m, lam = orc.backward(xs[s], A[s], lam, p.nc, 50, adaptive=bool(adaptive))
         assert_grad_close(M[s], ref_m, rtol=2e-5)
     np.testing.assert_array_equal(gp.cpu().numpy(), lam)
+
+
+def _image_order(x, outs):
+    """[B, nd, prod(outs)] in meshgrid order (coordinate 0 fastest) -> image order
+    (last axis fastest), the layout of cpab_transform_data_forward's final points."""
+    B, nd = x.shape[:2]
+    sp = x.reshape(B, nd, *outs[::-1])
+    return np.ascontiguousarray(sp.transpose(0, 1, *range(nd + 1, 1, -1))).reshape(B, nd, -1)
+
+
+@pytest.mark.parametrize("tess,ins,outs,adaptive", [([10], (50,), (70,), 0),
+                                                    ([6, 5], (40, 48), (36, 44), 0),
+                                                    ([6, 5], (40, 48), (36, 44), 1),
+                                                    ([3, 3, 3], (10, 12, 9), (11, 9, 13), 0)])
+def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive):
+    # cpab_transform_data_forward / _backward against the unfused composition
+    # the reference runs (transform_grid of the meshgrid, interpolate, and the
+    # autograd backward through both): image and final points bit-exact,
+    # moments and grad_data within tolerance.
+    T = cpab_for(tess)
+    p = T.params
+    nd = len(tess)
+    B, C = 2, 2
+    theta = seeded_theta(T, B, 0.5, 91)
+    rng = np.random.default_rng(92)
+    data = rng.random((B, C, *ins)).astype(np.float32)
+    grid = T.uniform_meshgrid(list(outs))
+    grid_np = grid.cpu().numpy()
+    As = _As_gpu(T, theta, cuda)
+    Tr = torch.empty_like(As)
+    native().expm(nd, As, 1.0 / 50, Tr)
+    out = torch.empty((B, C, *outs), device=cuda)
+    nP = int(np.prod(outs))
+    fin = torch.empty((B, nd, nP), device=cuda)
+    native().transform_data_forward(nd, _dev(data, cuda), grid, list(outs), 50, p.nc, adaptive,
+                                    Tr, As, out, fin)
+    A = As.cpu().numpy()
+    if nd == 1:
+        xT = orc.forward_closed_1d(grid_np, A, p.nc)
+    else:
+        xT = orc.forward_trels(grid_np, Tr.cpu().numpy(), A, p.nc, 50, adaptive=bool(adaptive))
+    np.testing.assert_array_equal(fin.cpu().numpy(), _image_order(xT, outs))
+    np.testing.assert_array_equal(out.cpu().numpy(), orc.interp_forward(nd, data, xT, outs))
+
+    gout = rng.standard_normal((B, C, *outs)).astype(np.float32)
+    mom = torch.empty((B, p.nC, nd * (nd + 1)), device=cuda)
+    gd = torch.empty((B, C, *ins), device=cuda)
+    nbytes = native().transform_data_backward_workspace_size(nd, B, list(outs), p.nC)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=cuda) if nbytes else None
+    native().transform_data_backward(nd, _dev(data, cuda), grid, list(outs), 50, p.nc, adaptive,
+                                     fin, As, _dev(gout, cuda), mom, gd, ws)
+    rg, rd = orc.interp_backward(nd, data, xT, outs, gout)
+    ref_m, _ = orc.backward(grid_np, A, rg, p.nc, 50, adaptive=bool(adaptive))
+    assert_grad_close(mom.cpu().numpy(), ref_m, rtol=2e-5)
+    _, mag = orc.interp_backward(nd, data, xT, outs, np.abs(gout), dtype=np.float64)
+    err = np.abs(gd.cpu().numpy().astype(np.float64) - rd)
+    assert (err <= 1e-4 * mag + 1e-12).all(), float((err / (mag + 1e-30)).max())
