@@ -419,9 +419,8 @@ __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g, con
 #pragma unroll
     for (int t = 0; t < TS; ++t) {
       const int c = (t == 0) ? cur : lookup<D>(p, g);
-      if (__builtin_amdgcn_ballot_w64(c != cur)) {
-        if (c != cur) A = fetch<D>(tab, c);
-      }
+      // Divergent branch, skipped (exec = 0) when no lane changed cell.
+      if (c != cur) A = fetch<D>(tab, c);
       cur = c;
       if (t & 1) cells[t >> 1] |= (uint32_t)c << 16;
       else cells[t >> 1] = (uint32_t)c;

@@ -128,6 +128,7 @@ cpab::LaunchCfg forward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta
   c.chunks = std::max(1, env_int("CPAB_FWD_CHUNKS", (int)chunks));
   c.lds_bins = 0;
   c.lds_cache = 0;
+  c.lds_chain = env_int("CPAB_FWD_LDS_CHAIN", 1) ? dev.lds : 0;
   c.reg_steps = 0;
   return c;
 }

@@ -79,21 +79,23 @@ __device__ __forceinline__ int tri_2d(float lx, float ly) {
 // Out-of-domain rules (cpab_ops_2d.cu:97-117): the boundary triangle of the
 // nearest square; beyond a corner the diagonal through the corner decides.
 // Falls through to the inside rule exactly as the reference does (NaN input).
+// Written as selects: a wave with points on the domain boundary (every row of
+// a meshgrid has two) takes this path at every step, and the nested branches
+// of the rule tree cost far more than evaluating all of it.  The products are
+// the reference's, term for term.
 __device__ __forceinline__ int cell_2d_outside(float px, float py, float fx, float fy,
                                                          int base, float lx, float ly) {
-  if (px <= 0.0f) {
-    if (py <= 0.0f && py * fy < px * fx) return base;
-    if (py >= 1.0f && fmaf(py, fy, -fy) > (-px) * fx) return base + 2;
-    return base + 3;
-  }
-  if (px >= 1.0f) {
-    if (py <= 0.0f && (-py) * fy > fmaf(px, fx, -fx)) return base;
-    if (py >= 1.0f && fmaf(py, fy, -fy) > fmaf(px, fx, -fx)) return base + 2;
-    return base + 1;
-  }
-  if (py <= 0.0f) return base;
-  if (py >= 1.0f) return base + 2;
-  return base + tri_2d(lx, ly);
+  const bool xl = px <= 0.0f, xh = px >= 1.0f, yl = py <= 0.0f, yh = py >= 1.0f;
+  const float pyfy = py * fy, pxfx = px * fx;
+  const float nyfy = (-py) * fy, nxfx = (-px) * fx;
+  const float yhi = fmaf(py, fy, -fy), xhi = fmaf(px, fx, -fx);
+  // px <= 0: below-left corner -> 0, above-left corner -> 2, else 3
+  const int tl = (yl & (pyfy < pxfx)) ? 0 : ((yh & (yhi > nxfx)) ? 2 : 3);
+  // px >= 1: below-right corner -> 0, above-right corner -> 2, else 1
+  const int th = (yl & (nyfy > xhi)) ? 0 : ((yh & (yhi > xhi)) ? 2 : 1);
+  // 0 < px < 1 (or NaN): bottom -> 0, top -> 2, else the inside rule
+  const int tm = yl ? 0 : (yh ? 2 : tri_2d(lx, ly));
+  return base + (xl ? tl : (xh ? th : tm));
 }
 
 // Square (cx, cy) holds triangles 4*(cx + cy*nx) + {0 top, 1 right, 2 bottom, 3 left}.

@@ -23,6 +23,7 @@ struct LaunchCfg {
   int lds_bins;     // accumulate moments in full LDS bins (per-workgroup partials)
   int lds_cache;    // else: accumulate in the hashed LDS cell cache (else global atomics)
   int reg_steps;    // backward: compile-time step count of the register variant (0 = segmented)
+  int lds_chain;    // forward: LDS bytes available for the per-stage table of a 2D chain (0 = off)
 };
 
 int device_cu_count();

@@ -125,9 +125,8 @@ __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT], flo
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
       const int c = (t == 0) ? cur[k] : cell_2d(px[k], py[k], nx, ny);
-      if (__builtin_amdgcn_ballot_w64(c != cur[k])) {
-        if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
-      }
+      // Divergent branch, skipped (exec = 0) when no lane changed cell.
+      if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
       cur[k] = c;
       float sx, sy;
       apply2(M[k], px[k], py[k], sx, sy);
@@ -235,6 +234,65 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
         o[p] = px[k];
         o[p + nP] = py[k];
       }
+    }
+  }
+}
+
+// Chain forward (K > 1) with each stage's table staged in LDS.  The grid
+// covers every point in one pass (PPT per lane), so the stage loop is uniform
+// across the workgroup and the table can be swapped between stages; a chain
+// over few points has only a handful of waves per SIMD, and LDS latency
+// instead of L1/L2 latency on the frequent per-wave table re-reads is what
+// keeps them busy.
+template <bool ADAPTIVE, int PPT>
+__global__ __launch_bounds__(1024) void chain2d_lds_kernel(int nP, int batched, int T, int nx,
+                                                          int ny, int K,
+                                                          const float* __restrict__ points,
+                                                          const float* __restrict__ Trels,
+                                                          const float* __restrict__ As,
+                                                          float* __restrict__ out,
+                                                          float* __restrict__ stage_points) {
+  extern __shared__ float lds[];
+  const int b = blockIdx.y;
+  const int n_batch = gridDim.y;
+  const int nC = 4 * nx * ny;
+  const float hh = 0.5f / (float)T;
+  const float* __restrict__ pts = points + (batched ? (size_t)b * 2 * nP : 0);
+  const int stride = gridDim.x * blockDim.x;
+  const int p0 = blockIdx.x * blockDim.x + threadIdx.x;
+  float px[PPT], py[PPT];
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    const int p = min(p0 + k * stride, nP - 1);
+    px[k] = pts[p];
+    py[k] = pts[p + nP];
+  }
+  for (int st = 0; st < K; ++st) {
+    const size_t row = (size_t)st * n_batch + b;
+    if (st > 0) __syncthreads();  // every lane is done with the previous table
+    stage(lds, Trels + row * nC * 6, nC * 6);
+    __syncthreads();
+    if (st > 0 && stage_points) {
+      float* sp = stage_points + ((size_t)(st - 1) * n_batch + b) * 2 * nP;
+#pragma unroll
+      for (int k = 0; k < PPT; ++k) {
+        const int p = p0 + k * stride;
+        if (p < nP) {
+          sp[p] = px[k];
+          sp[p + nP] = py[k];
+        }
+      }
+    }
+    steps_2d<ADAPTIVE, true, PPT>(px, py, lds, Trels + row * nC * 6, As + row * nC * 6, T, nx,
+                                  ny, hh);
+  }
+  float* __restrict__ o = out + (size_t)b * 2 * nP;
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    const int p = p0 + k * stride;
+    if (p < nP) {
+      o[p] = px[k];
+      o[p + nP] = py[k];
     }
   }
 }
@@ -428,6 +486,18 @@ hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_batch, int ba
   const size_t tab = (size_t)g.nC * g.ppc() * sizeof(float);
   const bool lds_table = cfg.lds_table && K == 1;
   const size_t lds = lds_table ? tab : 0;
+  if (g.ndim == 2 && K > 1 && cfg.lds_chain && tab <= (size_t)cfg.lds_chain) {
+    // one pass over the points: grid.x * block * PPT >= nP
+    const int ppt = adaptive ? 1 : 2;
+    const int64_t need = (nP + (int64_t)ppt * cfg.block - 1) / ((int64_t)ppt * cfg.block);
+    const dim3 gridc((unsigned)need, (unsigned)n_batch);
+    return adaptive ? launch_with_lds(chain2d_lds_kernel<true, 1>, gridc, block, tab, s, (int)nP,
+                                      batched, T, g.nx, g.ny, K, points, Trels, As, out,
+                                      stage_points)
+                    : launch_with_lds(chain2d_lds_kernel<false, 2>, gridc, block, tab, s, (int)nP,
+                                      batched, T, g.nx, g.ny, K, points, Trels, As, out,
+                                      stage_points);
+  }
   if (g.ndim == 2) {
     if (adaptive) {
       return lds_table
