@@ -156,3 +156,37 @@ def test_identity_theta_is_identity(cuda):
         pts = uniform_points(nd, 4000, 7)
         out = T.transform_grid(torch.tensor(pts, device=cuda), T.identity(3))
         np.testing.assert_array_equal(out.cpu().numpy(), np.broadcast_to(pts, (3, nd, 4000)))
+
+
+def test_stn_cpabwarp_style_composition(cuda):
+    # stn/stn.py:68-86 (CpabWarp.transform) calls the drop-in exactly like this:
+    # pixel grid in [-1, 1] flipped to CPAB order, then
+    # CPAB_transformer(points, theta, params, points.requires_grad) for each warp
+    # of a composition, the last warp first.  Check the composed output and both
+    # thetas' gradients against the oracle's stage-by-stage reverse mode.
+    from cpab.pytorch.transformer import CPAB_transformer
+    T = cpab_for([4, 5])
+    p = T.params
+    B, H, W = 2, 20, 24
+    ys, xs = torch.linspace(-1, 1, H, device=cuda), torch.linspace(-1, 1, W, device=cuda)
+    pix = torch.stack(torch.meshgrid(ys, xs, indexing="ij")[::-1]).flatten(1)  # [2, P] (x, y)
+    th1 = torch.tensor(seeded_theta(T, B, 0.4, 41), device=cuda, requires_grad=True)
+    th2 = torch.tensor(seeded_theta(T, B, 0.4, 42), device=cuda, requires_grad=True)
+    pts = (pix.flip(-2) + 1) / 2
+    for th in (th2, th1):  # T_K acts first
+        pts = CPAB_transformer(pts, th, p, pts.requires_grad)
+    out = (pts * 2 - 1).flip(-2)
+    g = np.random.default_rng(43).standard_normal(out.shape).astype(np.float32)
+    out.backward(torch.tensor(g, device=cuda))
+
+    x0 = ((pix.flip(-2) + 1) / 2).cpu().numpy()
+    A2 = orc.affine(th2.detach().cpu().numpy(), p.basis).reshape(B, p.nC, 2, 3)
+    A1 = orc.affine(th1.detach().cpu().numpy(), p.basis).reshape(B, p.nC, 2, 3)
+    x1 = orc.forward_trels(x0, orc.expm(2, A2, 1 / 50), A2, p.nc, 50)
+    x2 = orc.forward_trels(x1, orc.expm(2, A1, 1 / 50), A1, p.nc, 50)
+    np.testing.assert_allclose(out.detach().cpu().numpy(), (x2 * 2 - 1)[:, ::-1], atol=2e-6, rtol=0)
+    lam = (2 * g[:, ::-1]).astype(np.float32)  # d out / d x2 through the flip and scale
+    m1, lam1 = orc.backward(x1, A1, lam, p.nc, 50)
+    m2, _ = orc.backward(x0, A2, lam1, p.nc, 50)
+    assert_grad_close(th1.grad.cpu().numpy(), orc.project(m1.reshape(B, -1), p.basis, dtype=np.float64))
+    assert_grad_close(th2.grad.cpu().numpy(), orc.project(m2.reshape(B, -1), p.basis, dtype=np.float64))
