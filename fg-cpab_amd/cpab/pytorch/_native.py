@@ -90,8 +90,13 @@ def _ptr(t):
 
 
 def _stream(device):
+    """Raw hipStream_t of torch's current stream on ``device`` (the launch stream)."""
     import torch
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return ctypes.c_void_p(raw(idx))
+    return ctypes.c_void_p(torch.cuda.current_stream(idx).cuda_stream)
 
 
 def _check(rc, what):

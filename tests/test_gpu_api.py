@@ -190,3 +190,18 @@ def test_stn_cpabwarp_style_composition(cuda):
     m2, _ = orc.backward(x0, A2, lam1, p.nc, 50)
     assert_grad_close(th1.grad.cpu().numpy(), orc.project(m1.reshape(B, -1), p.basis, dtype=np.float64))
     assert_grad_close(th2.grad.cpu().numpy(), orc.project(m2.reshape(B, -1), p.basis, dtype=np.float64))
+
+
+def test_runs_on_current_stream(cuda):
+    # Kernels are enqueued on torch's current stream: results computed inside a
+    # side stream (default priority) match the default stream's.
+    T = cpab_for([8, 8])
+    pts = torch.tensor(uniform_points(2, 5000, 51), device=cuda)
+    th = torch.tensor(seeded_theta(T, 3, 0.5, 52), device=cuda)
+    ref = T.transform_grid(pts, th)
+    side = torch.cuda.Stream(device=cuda)
+    side.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(side):
+        out = T.transform_grid(pts, th)
+    side.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), ref.cpu().numpy())
