@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -177,11 +178,11 @@ struct Timed {
   hipEvent_t start, stop;
 };
 std::mutex g_prof_mu;
-bool g_prof_on = false;
+std::atomic<bool> g_prof_on{false};
 std::vector<Timed> g_prof_pending;
 
 bool prof_begin(hipStream_t s, hipEvent_t* a) {
-  if (!g_prof_on) return false;
+  if (!g_prof_on.load(std::memory_order_relaxed)) return false;
   if (hipEventCreate(a) != hipSuccess) return false;
   if (hipEventRecord(*a, s) != hipSuccess) {
     (void)hipEventDestroy(*a);
@@ -200,10 +201,10 @@ void prof_end(bool on, hipEvent_t a, const char* name, hipStream_t s) {
 
 // Forward of a chain of K stages (K = 1: one transform).  ndim 1 uses the
 // closed form (Trels unused).
-int forward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int batched,
-                        int K, int nstepsolver, int ncx, int ncy, int ncz, int adaptive,
-                        const float* points, const float* Trels, const float* As, float* out,
-                        float* stage_points, void* stream) {
+int forward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int batched, int K,
+                 int nstepsolver, int ncx, int ncy, int ncz, int adaptive, const float* points,
+                 const float* Trels, const float* As, float* out, float* stage_points,
+                 void* stream) {
   cpab::Geometry g{};
   int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
   if (rc) return rc;
@@ -536,7 +537,7 @@ int cpab_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, voi
 
 void cpab_profile_enable(int on) {
   std::lock_guard<std::mutex> lock(g_prof_mu);
-  g_prof_on = on != 0;
+  g_prof_on.store(on != 0, std::memory_order_relaxed);
 }
 
 int cpab_profile_read(const char* kernel, double* total_ms, int64_t* launches) {
@@ -544,22 +545,28 @@ int cpab_profile_read(const char* kernel, double* total_ms, int64_t* launches) {
   std::lock_guard<std::mutex> lock(g_prof_mu);
   double tot = 0.0;
   int64_t n = 0;
+  hipError_t first = hipSuccess;
   std::vector<Timed> keep;
   for (const Timed& t : g_prof_pending) {
     if (std::strcmp(t.name, kernel) != 0) { keep.push_back(t); continue; }
+    // Every matching record is consumed (and its events released) even if one
+    // of them fails, so nothing is left pointing at destroyed events.
     float ms = 0.0f;
     hipError_t e = hipEventSynchronize(t.stop);
     if (e == hipSuccess) e = hipEventElapsedTime(&ms, t.start, t.stop);
     (void)hipEventDestroy(t.start);
     (void)hipEventDestroy(t.stop);
-    if (e != hipSuccess) return check_hip(e, "cpab_profile_read");
+    if (e != hipSuccess) {
+      if (first == hipSuccess) first = e;
+      continue;
+    }
     tot += ms;
     ++n;
   }
   g_prof_pending.swap(keep);
   *total_ms = tot;
   *launches = n;
-  return CPAB_OK;
+  return check_hip(first, "cpab_profile_read");
 }
 
 static int check_interp(int ndim, int64_t B, int64_t C, const int64_t* in_size,
