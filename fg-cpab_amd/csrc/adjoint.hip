@@ -390,10 +390,11 @@ __device__ __forceinline__ void segmented_body(P tab, int nP, int T, const Cells
   }
 }
 
-// Register variant: T == TS known at compile time, moments in LDS bins.
-template <int D, bool ADAPTIVE, int TS, typename P, typename IO>
+// Register variant: T == TS known at compile time, moments in full LDS bins
+// or (3D) in the LDS cell cache.
+template <int D, bool ADAPTIVE, int BINS, int TS, typename P, typename IO>
 __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g, const IO& io,
-                                              float* bins) {
+                                              float* bins, int* keys, float* __restrict__ mom_b) {
   constexpr int PP = Dim<D>::P;
   const float h = 1.0f / (float)TS;
   const float hh = h * 0.5f;
@@ -440,7 +441,10 @@ __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g, con
       // Divergent branch: skipped by the hardware (exec = 0) at steps where no
       // lane of the wave changes cell.
       if (c != prev) {
-        if (prev >= 0 && valid) flush_lds<PP>(bins, prev, m);
+        if (prev >= 0 && valid) {
+          if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, prev, m);
+          else flush_lds<PP>(bins, prev, m);
+        }
 #pragma unroll
         for (int k = 0; k < PP; ++k) m[k] = 0.0f;
         A = fetch<D>(tab, c);
@@ -448,7 +452,10 @@ __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g, con
       prev = c;
       adjoint(A, traj[t], h, hh, hhh, m, lam);
     }
-    if (valid) flush_lds<PP>(bins, prev, m);
+    if (valid) {
+      if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, prev, m);
+      else flush_lds<PP>(bins, prev, m);
+    }
     io.finish(pi, valid, lam);
   }
 }
@@ -505,9 +512,9 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
                                           int nP, int T, const Cells& g, const IO& io,
                                           float* __restrict__ mom_b) {
   if constexpr (TS > 0) {
-    static_assert(BINS == kBinsFull, "the register variant accumulates in full LDS bins");
-    if (LDS_A) register_body<D, ADAPTIVE, TS>(as_lds(L.ldsA), nP, g, io, L.bins);
-    else register_body<D, ADAPTIVE, TS>(Ag, nP, g, io, L.bins);
+    static_assert(BINS != kBinsGlobal, "the register variant accumulates in LDS");
+    if (LDS_A) register_body<D, ADAPTIVE, BINS, TS>(as_lds(L.ldsA), nP, g, io, L.bins, L.keys, mom_b);
+    else register_body<D, ADAPTIVE, BINS, TS>(Ag, nP, g, io, L.bins, L.keys, mom_b);
   } else {
     if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(L.ldsA), nP, T, g, io, L.bins, L.keys, mom_b);
     else segmented_body<D, ADAPTIVE, BINS>(Ag, nP, T, g, io, L.bins, L.keys, mom_b);
@@ -522,8 +529,14 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
 // the lam buffer the stage above wrote for the same points, and writes the
 // adjoint of its input to lam (k > 0) or grad_points (k = 0).  Moments of
 // stage k go to partials / moments row (k * n_batch + b).
+// Launch bound: 768 threads (3 waves per SIMD, up to 168 VGPRs), or 512 (2 waves
+// per SIMD, 256 VGPRs) for the 3D register variant whose trajectory alone takes
+// 150 VGPRs.
+template <int D, int TS>
+constexpr int kBwdThreads = (D == 3 && TS > 0) ? 512 : 768;
+
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
-__global__ __launch_bounds__(768) void backward_kernel(
+__global__ __launch_bounds__((kBwdThreads<D, TS>)) void backward_kernel(
     int nP, int batched, int T, Cells g, int nC, int K, const float* __restrict__ points,
     const float* __restrict__ stage_points, const float* __restrict__ As,
     const float* __restrict__ grad_out, float* __restrict__ moments, float* __restrict__ partials,
@@ -556,7 +569,7 @@ __global__ __launch_bounds__(768) void backward_kernel(
 // Fused transform_data backward: one workgroup = one theta x one contiguous
 // range of output positions.
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
-__global__ __launch_bounds__(768) void image_backward_kernel(
+__global__ __launch_bounds__((kBwdThreads<D, TS>)) void image_backward_kernel(
     ImageShape s, int T, Cells g, int nC, const float* __restrict__ grid,
     const float* __restrict__ final_points, const float* __restrict__ As,
     const float* __restrict__ data, const float* __restrict__ grad_out,
@@ -642,6 +655,13 @@ hipError_t dispatch(const BackwardJob& j, int adaptive, const LaunchCfg& cfg, hi
         case 2: CPAB_GO(true, false, kBinsFull, kRegSteps);
         default: CPAB_GO(true, true, kBinsFull, kRegSteps);
       }
+    }
+  } else {
+    // 3D: 150 VGPRs of trajectory; the adaptive step does not fit beside it.
+    if (!adaptive && cfg.reg_steps == kRegSteps && j.T == kRegSteps &&
+        (cfg.lds_bins || cfg.lds_cache)) {
+      if (cfg.lds_bins) CPAB_GO(false, false, kBinsFull, kRegSteps);
+      CPAB_GO(false, false, kBinsCache, kRegSteps);
     }
   }
   const int bins = cfg.lds_bins ? kBinsFull : (cfg.lds_cache ? kBinsCache : kBinsGlobal);

@@ -134,35 +134,38 @@ cpab::LaunchCfg forward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta
   return c;
 }
 
-cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta, int T) {
+cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta, int T,
+                             int adaptive) {
   const DeviceInfo dev = device_info();
   const int64_t table = (int64_t)g.nC * g.ppc() * 4;
   cpab::LaunchCfg c{};
   c.lds_bins = (table <= dev.lds) ? env_int("CPAB_BWD_LDS_BINS", 1) : 0;
-  // Register variant: whole trajectory in VGPRs (~168 per lane -> 3 waves per
-  // SIMD = 12 waves per CU), one 768-thread workgroup per CU; the per-cell
-  // table is read through L1/L2 (re-read only when a lane changes cell).
-  const bool reg = g.ndim <= 2 && T == cpab::kRegSteps && c.lds_bins && g.nC <= 65535 &&
-                   env_int("CPAB_BWD_REG", 1);
-  c.reg_steps = reg ? cpab::kRegSteps : 0;
   // Table too large for LDS: hashed cell cache in LDS, flushed to HBM at the end.
   const int64_t cache = (int64_t)cpab::kCacheSlots * (g.ppc() + 1) * 4;
   c.lds_cache = (!c.lds_bins && cache <= dev.lds) ? env_int("CPAB_BWD_CACHE", 1) : 0;
+  // Register variant: whole trajectory in VGPRs, one workgroup per CU; the
+  // per-cell table is read through L1/L2 (re-read only when a lane changes
+  // cell).  1D/2D: ~168 VGPRs per lane -> 3 waves per SIMD, 768 threads.  3D
+  // (not adaptive): ~254 VGPRs -> 2 waves per SIMD, 512 threads.
+  const bool reg = T == cpab::kRegSteps && g.nC <= 65535 && env_int("CPAB_BWD_REG", 1) &&
+                   (g.ndim <= 2 ? c.lds_bins != 0 : (!adaptive && (c.lds_bins || c.lds_cache)));
+  c.reg_steps = reg ? cpab::kRegSteps : 0;
   const int64_t used = c.lds_bins ? table : (c.lds_cache ? cache : 0);
   c.lds_table = (used + table <= dev.lds) ? env_int("CPAB_BWD_LDS_TABLE", reg ? 0 : 1) : 0;
   const int64_t lds = used + (c.lds_table ? table : 0);
+  const int limit = (reg && g.ndim == 3) ? 512 : 768;  // kernel launch bound
   int wg_per_cu;
   if (reg) {
-    c.block = env_int("CPAB_BWD_BLOCK", 768);
-    wg_per_cu = std::max(1, 768 / c.block);
+    c.block = env_int("CPAB_BWD_BLOCK", limit);
+    wg_per_cu = std::max(1, limit / std::max(1, c.block));
   } else {
     // The cache variant runs one workgroup per CU (104 KiB of LDS in 3D): make
     // it 12 waves.
     c.block = env_int("CPAB_BWD_BLOCK", c.lds_cache ? 768 : 512);
-    wg_per_cu = std::max(1, 2048 / c.block);  // 32 waves per CU
+    wg_per_cu = std::max(1, 2048 / std::max(1, c.block));  // 32 waves per CU
     if (lds > 0) wg_per_cu = (int)std::max<int64_t>(1, std::min<int64_t>(wg_per_cu, dev.lds / lds));
   }
-  c.block = std::min(768, std::max(64, c.block / 64 * 64));  // kernel launch bound
+  c.block = std::min(limit, std::max(64, c.block / 64 * 64));
   const int64_t want = (int64_t)dev.cus * wg_per_cu;
   int64_t chunks = std::max<int64_t>(1, div_up(want, std::max<int64_t>(n_theta, 1)));
   chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
@@ -259,8 +262,8 @@ int64_t workspace_size_impl(int ndim, int64_t nP, int64_t n_batch, int K, int nC
   g.ndim = ndim;
   g.nC = nC;
   // Whichever variant runs (register or segmented) fits.
-  const int64_t a = backward_workspace(g, nP, n_batch, K, backward_cfg(g, nP, n_batch, cpab::kRegSteps)).total;
-  const int64_t b = backward_workspace(g, nP, n_batch, K, backward_cfg(g, nP, n_batch, 0)).total;
+  const int64_t a = backward_workspace(g, nP, n_batch, K, backward_cfg(g, nP, n_batch, cpab::kRegSteps, 0)).total;
+  const int64_t b = backward_workspace(g, nP, n_batch, K, backward_cfg(g, nP, n_batch, 0, 1)).total;
   return std::max(a, b);
 }
 
@@ -285,7 +288,7 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   if (nP == 0) return check_hip(cpab::launch_fill(moments, rows * R, 0.0f, s), who);
   CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(grad_out);
   if (K > 1) CPAB_REQUIRE(stage_points);
-  const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_batch, nstepsolver);
+  const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_batch, nstepsolver, adaptive);
   const BackwardWorkspace w = backward_workspace(g, nP, n_batch, K, cfg);
   if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
@@ -486,7 +489,7 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   CPAB_REQUIRE(grad_out); CPAB_REQUIRE(moments);
   hipStream_t s = as_stream(stream);
   const int R = g.nC * g.ppc();
-  const cpab::LaunchCfg cfg = backward_cfg(g, img.nP, n_batch, nstepsolver);
+  const cpab::LaunchCfg cfg = backward_cfg(g, img.nP, n_batch, nstepsolver, adaptive);
   const BackwardWorkspace w = backward_workspace(g, img.nP, n_batch, 1, cfg);
   if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
