@@ -90,3 +90,37 @@ def test_cell_centers():
     assert c.shape == (16, 2)
     # cell 0: triangle (centre (0.25, 0.25), (0, 0), (0.5, 0))
     np.testing.assert_allclose(c[0], [0.25, 0.25 / 3], atol=1e-12)
+
+
+def test_fused_paths_reject_cpu_tensors():
+    from cpab.pytorch.transformer import CPAB_chain_transformer, CPAB_transform_data
+    T = Cpab([3, 3])
+    with pytest.raises(AssertionError, match="Only GPU tensors supported"):
+        CPAB_chain_transformer(torch.zeros(2, 10), torch.zeros(2, 1, T.params.d), T.params)
+    with pytest.raises(AssertionError, match="Only GPU tensors supported"):
+        CPAB_transform_data(torch.zeros(1, 1, 4, 4), torch.zeros(1, T.params.d),
+                            torch.zeros(2, 16), [4, 4], T.params)
+
+
+def test_transform_data_checks_before_device_work():
+    # The fused transform_data validates shapes on the host and raises
+    # RuntimeError (as the reference's TORCH_CHECKs do) before any launch.
+    from cpab.pytorch import transformer as tr
+    T = Cpab([3, 3])
+    with pytest.raises(RuntimeError, match="theta must be"):
+        tr._CPABImageFunction.forward(_Ctx(), torch.zeros(2, 1, 4, 4), torch.zeros(3, T.params.d),
+                                      torch.zeros(2, 16), [4, 4], T.params)
+    with pytest.raises(RuntimeError, match="meshgrid of outsize"):
+        tr._CPABImageFunction.forward(_Ctx(), torch.zeros(2, 1, 4, 4), torch.zeros(2, T.params.d),
+                                      torch.zeros(2, 15), [4, 4], T.params)
+    with pytest.raises(RuntimeError, match="float32"):
+        tr._CPABImageFunction.forward(_Ctx(), torch.zeros(2, 1, 4, 4, dtype=torch.float64),
+                                      torch.zeros(2, T.params.d), torch.zeros(2, 16), [4, 4],
+                                      T.params)
+
+
+class _Ctx:
+    needs_input_grad = (False, False, False, False, False)
+
+    def save_for_backward(self, *a):
+        pass
