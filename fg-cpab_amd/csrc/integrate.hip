@@ -146,15 +146,20 @@ __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT], flo
   }
 }
 
-// T fixed steps of one transform for one point (3D, cpab_ops_3d.cu:169-241).
+// T fixed steps of one transform for one point (3D, cpab_ops_3d.cu:169-241),
+// with the same cell-change caching of the one-step map as steps_2d.
 template <bool ADAPTIVE, bool LDS>
 __device__ __forceinline__ void steps_3d(float& px, float& py, float& pz, float* lds,
                                          const float* __restrict__ Tg,
                                          const float* __restrict__ Ag, int T, int nx, int ny,
                                          int nz, float hh) {
+  int cur = cell_3d(px, py, pz, nx, ny, nz);
+  Aff<3> M = LDS ? load_aff3(as_lds(lds), cur) : load_aff3(Tg, cur);
   for (int t = 0; t < T; ++t) {
-    const int c = cell_3d(px, py, pz, nx, ny, nz);
-    const Aff<3> M = LDS ? load_aff3(as_lds(lds), c) : load_aff3(Tg, c);
+    const int c = (t == 0) ? cur : cell_3d(px, py, pz, nx, ny, nz);
+    // Divergent branch, skipped (exec = 0) when no lane changed cell.
+    if (c != cur) M = LDS ? load_aff3(as_lds(lds), c) : load_aff3(Tg, c);
+    cur = c;
     float sx, sy, sz;
     apply3(M, px, py, pz, sx, sy, sz);
     if (ADAPTIVE) {
