@@ -128,14 +128,18 @@ __device__ __forceinline__ int cell_3d(float px, float py, float pz, int nx, int
   const float ox = (fabsf(px - 0.5f) - 0.5f) * fx;
   const float oy = (fabsf(py - 0.5f) - 0.5f) * fy;
   const float oz = (fabsf(pz - 0.5f) - 0.5f) * fz;
-  if (ox > 0.0f && oy > 0.0f && oz > 0.0f) {
-    // Beyond a corner: move the axis with the smallest overshoot half a cell inside.
-    if (ox <= oy && ox <= oz) {
-      px = (px < 0.5f) ? 0.5f / fx : 1.0f - 0.5f / fx;
-    } else if (oy <= oz) {
-      py = (py < 0.5f) ? 0.5f / fy : 1.0f - 0.5f / fy;
-    } else {
-      pz = (pz < 0.5f) ? 0.5f / fz : 1.0f - 0.5f / fz;
+  // Beyond a corner (rare): move the axis with the smallest overshoot half a
+  // cell inside.  Wave-uniform branch, so the common case pays one ballot.
+  const bool corner = (ox > 0.0f) & (oy > 0.0f) & (oz > 0.0f);
+  if (__builtin_amdgcn_ballot_w64(corner)) {
+    if (corner) {
+      if (ox <= oy && ox <= oz) {
+        px = (px < 0.5f) ? 0.5f / fx : 1.0f - 0.5f / fx;
+      } else if (oy <= oz) {
+        py = (py < 0.5f) ? 0.5f / fy : 1.0f - 0.5f / fy;
+      } else {
+        pz = (pz < 0.5f) ? 0.5f / fz : 1.0f - 0.5f / fz;
+      }
     }
   }
   const float xc = fminf(fmaxf(px, 0.0f), 1.0f);
@@ -153,11 +157,14 @@ __device__ __forceinline__ int cell_3d(float px, float py, float pz, int nx, int
     x = y;
     y = 1.0f - t;
   }
-  if (z - (x + y) >= 0.0f) return c + 1;  // ((-x) - y) + z, rounded identically
-  if (((x + y) + z) - 2.0f >= 0.0f) return c + 2;
-  if ((y - x) - z >= 0.0f) return c + 3;  // ((-x) + y) - z
-  if ((x - y) - z >= 0.0f) return c + 4;
-  return c;
+  // First matching test wins, as in the reference's if-chain; evaluated as
+  // selects (every lane needs all four tests anyway).
+  const float s = x + y;
+  int t = ((x - y) - z >= 0.0f) ? 4 : 0;
+  t = ((y - x) - z >= 0.0f) ? 3 : t;         // ((-x) + y) - z
+  t = ((s + z) - 2.0f >= 0.0f) ? 2 : t;
+  t = (z - s >= 0.0f) ? 1 : t;               // ((-x) - y) + z, rounded identically
+  return c + t;
 }
 
 // ---------------------------------------------------------------------------
