@@ -109,6 +109,14 @@ int check_points(int64_t nP, int64_t n_theta, int ndim) {
 #define CPAB_REQUIRE(ptr) \
   do { if (!(ptr)) return fail(CPAB_ERR_INVALID, "%s must not be NULL", #ptr); } while (0)
 
+// Per-cell tables are read as 8- and 16-byte vectors; every float array must
+// be at least float-aligned.
+#define CPAB_ALIGNED(ptr, bytes)                                                      \
+  do {                                                                                \
+    if ((ptr) && (reinterpret_cast<uintptr_t>(ptr) % (bytes)) != 0)                  \
+      return fail(CPAB_ERR_INVALID, "%s must be %d-byte aligned", #ptr, (int)(bytes)); \
+  } while (0)
+
 // ---- launch-shape policy ---------------------------------------------------
 
 cpab::LaunchCfg forward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta) {
@@ -219,6 +227,7 @@ int forward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int bat
   if (nP == 0 || n_batch == 0) return CPAB_OK;
   CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(out);
   if (ndim > 1) CPAB_REQUIRE(Trels);
+  CPAB_ALIGNED(As, 16); CPAB_ALIGNED(Trels, 16); CPAB_ALIGNED(points, 4);
   hipStream_t s = as_stream(stream);
   hipEvent_t ev;
   const bool timed = prof_begin(s, &ev);
@@ -287,6 +296,8 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   const int64_t rows = (int64_t)K * n_batch;
   if (nP == 0) return check_hip(cpab::launch_fill(moments, rows * R, 0.0f, s), who);
   CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(grad_out);
+  CPAB_ALIGNED(As, 16); CPAB_ALIGNED(points, 4); CPAB_ALIGNED(grad_out, 4);
+  CPAB_ALIGNED(workspace, 16);
   if (K > 1) CPAB_REQUIRE(stage_points);
   const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_batch, nstepsolver, adaptive);
   const BackwardWorkspace w = backward_workspace(g, nP, n_batch, K, cfg);
@@ -367,6 +378,7 @@ int cpab_expm(int ndim, int64_t n_matrices, float dT, const float* As, float* Tr
   if (n_matrices < 0) return fail(CPAB_ERR_INVALID, "negative n_matrices");
   if (n_matrices == 0) return CPAB_OK;
   CPAB_REQUIRE(As); CPAB_REQUIRE(Trels);
+  CPAB_ALIGNED(As, 16); CPAB_ALIGNED(Trels, 16);
   return check_hip(cpab::launch_expm(ndim, n_matrices, dT, As, Trels, as_stream(stream)),
                    "cpab_expm");
 }
@@ -404,6 +416,7 @@ int cpab_trace_cells(int ndim, int64_t nP, int64_t n_theta, int batched, int nst
   if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
   if (nP == 0 || n_theta == 0) return CPAB_OK;
   CPAB_REQUIRE(points); CPAB_REQUIRE(Trels); CPAB_REQUIRE(As); CPAB_REQUIRE(cells);
+  CPAB_ALIGNED(As, 16); CPAB_ALIGNED(Trels, 16);
   return check_hip(cpab::launch_trace_cells(g, nP, n_theta, batched ? 1 : 0, nstepsolver, adaptive,
                                             points, Trels, As, cells, as_stream(stream)),
                    "cpab_trace_cells");
@@ -452,6 +465,7 @@ int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
   if (n_batch == 0) return CPAB_OK;
   CPAB_REQUIRE(grid); CPAB_REQUIRE(As); CPAB_REQUIRE(data); CPAB_REQUIRE(out);
   if (ndim > 1) CPAB_REQUIRE(Trels);
+  CPAB_ALIGNED(As, 16); CPAB_ALIGNED(Trels, 16);
   hipStream_t s = as_stream(stream);
   const cpab::LaunchCfg cfg = forward_cfg(g, img.nP, n_batch);
   hipEvent_t ev;
@@ -486,6 +500,7 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   if ((rc = image_shape(ndim, n_batch, n_channels, in_size, out_size, &img))) return rc;
   if (n_batch == 0) return CPAB_OK;
   CPAB_REQUIRE(grid); CPAB_REQUIRE(final_points); CPAB_REQUIRE(As); CPAB_REQUIRE(data);
+  CPAB_ALIGNED(As, 16); CPAB_ALIGNED(workspace, 16);
   CPAB_REQUIRE(grad_out); CPAB_REQUIRE(moments);
   hipStream_t s = as_stream(stream);
   const int R = g.nC * g.ppc();

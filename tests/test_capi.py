@@ -89,3 +89,13 @@ def test_chain_validation():
                                  None)
     assert rc == 1 and "n_stages" in _err(lib)
     assert lib.cpab_chain_backward_workspace_size(2, 10, 1, 0, 64) == 0
+
+
+def test_misaligned_tables_rejected():
+    lib = _native.load_library()
+    p = ctypes.c_void_p(64)
+    bad = ctypes.c_void_p(68)  # float-aligned, not 16-byte aligned
+    rc = lib.cpab_forward(2, 10, 1, 0, 50, 4, 4, 1, 0, p, p, bad, p, None)
+    assert rc == 1 and "aligned" in _err(lib)
+    rc = lib.cpab_expm(2, 4, 0.02, bad, p, None)
+    assert rc == 1 and "aligned" in _err(lib)
