@@ -6,7 +6,9 @@
  * calls and the torch interpolation ops around it.  Conventions:
  *
  *   - every pointer is a device pointer to contiguous float32 (or int32 index)
- *     memory owned by the caller; nothing is allocated by the library;
+ *     memory owned by the caller; nothing is allocated by the library; the
+ *     per-cell tables (As, Trels) and workspaces must be 16-byte aligned (they
+ *     are read as vectors; misaligned ones are rejected with CPAB_ERR_INVALID);
  *   - `stream` is a hipStream_t (pass 0 for the null stream); all work is
  *     enqueued asynchronously on it;
  *   - the return value is CPAB_OK or an error code; argument checking happens
