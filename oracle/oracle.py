@@ -7,6 +7,26 @@ the product path (fg-cpab_amd/cpab) never imports it.
 Every function takes / returns numpy arrays.  ``*_f32`` routines restate the
 reference kernels op for op in float32; ``*_f64`` twins run the same scheme in
 float64 to pin the mathematics (finite differences, closed forms).
+
+How each function is pinned (tests/test_oracle.py unless noted; the reference
+ships no tests or golden vectors for this path, and its CUDA cannot run here):
+  cells               barycentric containment in the tessellation's cells;
+                      boundary-projection rule for points outside (2D/3D)
+  expm                scipy.linalg.expm (float64) at three norm ranges, incl.
+                      the squaring branch; A = 0 gives I exactly
+  affine, project     dense B @ theta and B^T @ M
+  forward_trels       one uniform field in every cell: T steps = expm(A) p
+  forward_midpoint    second-order convergence to the exact flow
+  forward_closed_1d   scipy solve_ivp of the ODE; order preservation
+  backward            float64 finite differences of the midpoint scheme
+                      (1D/2D/3D); closed form at theta = 0; linearity in the seed
+  interp_forward/     textbook bilinear; torch grid_sample (align_corners=True,
+  interp_backward     border padding); finite differences
+  (basis, host code)  fixtures written by the reference's tesselation.py
+                      (tests/test_basis_golden.py)
+No function is left "parity unpinned".  What stays unpinned is the exact
+bits of the reference's own CUDA build (nvcc contraction choices, cuSPARSE
+summation order, CUDA expf/logf), which no GPU here can produce.
 """
 import ctypes
 import os
