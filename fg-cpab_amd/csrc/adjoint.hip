@@ -10,9 +10,13 @@
 //             in a VGPR shift register; phase 2 replays each segment from its
 //             checkpoint into registers and walks it backwards (the
 //             reference's scheme, cpab_ops_2d.cu:236-263).
-// In both, phase 2 propagates lambda and accumulates the 2x3 (1x2, 3x4) moment
-// of the current cell, flushing it whenever the cell changes, exactly as the
-// reference groups its flushes.
+// In both, phase 2 propagates lambda and accumulates the 2x3 (1x2, 3x4) sum
+// S = sum lam (x) [p; 1] of the current cell, flushing it whenever the cell
+// changes, as the reference groups its moment flushes.  The reverse step is the
+// factored form of cpab_ops_2d.cu:334-382 (cpab_device.hpp, adjoint_s*): lam is
+// advanced with the per-cell increment G = h A + (h^2/2) A^2 and the moments
+// are formed from S once per cell after the partial tables are summed
+// (basis.hip, finish_moments_kernel).
 //
 // Moment accumulation on MI355X: each workgroup serves ONE theta and one
 // contiguous range of points (spatially coherent for meshgrid inputs).
@@ -69,6 +73,11 @@ template <int D, typename P> __device__ __forceinline__ Aff<D> fetch(P tab, int 
   return Fetch<D>::at(tab, c);
 }
 
+template <int D> __device__ __forceinline__ Adj<D> fetch_adj(const float* tab, int c);
+template <> __device__ __forceinline__ Adj<1> fetch_adj<1>(const float* tab, int c) { return load_adj1(tab, c); }
+template <> __device__ __forceinline__ Adj<2> fetch_adj<2>(const float* tab, int c) { return load_adj2(tab, c); }
+template <> __device__ __forceinline__ Adj<3> fetch_adj<3>(const float* tab, int c) { return load_adj3(tab, c); }
+
 __device__ __forceinline__ void velocity(const Aff<1>& A, const float (&p)[1], float (&v)[1]) {
   v[0] = fmaf(A.a, p[0], A.b);
 }
@@ -89,17 +98,17 @@ __device__ __forceinline__ void midpoint(const Aff<3>& A, float (&p)[3], float h
   midpoint3(A, p[0], p[1], p[2], h, hh);
 }
 
-__device__ __forceinline__ void adjoint(const Aff<1>& A, const float (&p)[1], float h, float hh,
-                                        float hhh, float (&m)[2], float (&l)[1]) {
-  adjoint1(A, p[0], h, hh, hhh, m, l[0]);
+__device__ __forceinline__ void adjoint(const Adj<1>& G, const float (&p)[1], float (&s)[2],
+                                        float (&l)[1]) {
+  adjoint_s1(G, p[0], s, l[0]);
 }
-__device__ __forceinline__ void adjoint(const Aff<2>& A, const float (&p)[2], float h, float hh,
-                                        float hhh, float (&m)[6], float (&l)[2]) {
-  adjoint2(A, p[0], p[1], h, hh, hhh, m, l[0], l[1]);
+__device__ __forceinline__ void adjoint(const Adj<2>& G, const float (&p)[2], float (&s)[6],
+                                        float (&l)[2]) {
+  adjoint_s2(G, p[0], p[1], s, l[0], l[1]);
 }
-__device__ __forceinline__ void adjoint(const Aff<3>& A, const float (&p)[3], float h, float hh,
-                                        float hhh, float (&m)[12], float (&l)[3]) {
-  adjoint3(A, p[0], p[1], p[2], h, hh, hhh, m, l[0], l[1], l[2]);
+__device__ __forceinline__ void adjoint(const Adj<3>& G, const float (&p)[3], float (&s)[12],
+                                        float (&l)[3]) {
+  adjoint_s3(G, p[0], p[1], p[2], s, l[0], l[1], l[2]);
 }
 
 // One replay step from p in cell c (already looked up): explicit midpoint, or
@@ -302,12 +311,12 @@ struct ImageIO {
 // One stage of one theta over this workgroup's point range; moments go to
 // bins / keys / mom_b.
 template <int D, bool ADAPTIVE, int BINS, typename P, typename IO>
-__device__ __forceinline__ void segmented_body(P tab, int nP, int T, const Cells& g, const IO& io,
-                                               float* bins, int* keys, float* __restrict__ mom_b) {
+__device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ gtab, int nP, int T,
+                                               const Cells& g, const IO& io, float* bins,
+                                               int* keys, float* __restrict__ mom_b) {
   constexpr int PP = Dim<D>::P;
   const float h = 1.0f / (float)T;
   const float hh = h * 0.5f;
-  const float hhh = hh * h;
   const int nseg = (T + kSeg - 1) / kSeg;
   // The loop bound is uniform so every wave stays converged (the global flush
   // needs all 64 lanes); lanes past the range replay a clamped point and
@@ -375,7 +384,7 @@ __device__ __forceinline__ void segmented_body(P tab, int nP, int T, const Cells
             for (int k = 0; k < PP; ++k) m[k] = 0.0f;
             prev = c;
           }
-          adjoint(fetch<D>(tab, c), sp[s], h, hh, hhh, m, lam);
+          adjoint(fetch_adj<D>(gtab, c), sp[s], m, lam);
         }
       }
     }
@@ -393,12 +402,12 @@ __device__ __forceinline__ void segmented_body(P tab, int nP, int T, const Cells
 // Register variant: T == TS known at compile time, moments in full LDS bins
 // or (3D) in the LDS cell cache.
 template <int D, bool ADAPTIVE, int BINS, int TS, typename P, typename IO>
-__device__ __forceinline__ void register_body(P tab, int nP, const Cells& g, const IO& io,
-                                              float* bins, int* keys, float* __restrict__ mom_b) {
+__device__ __forceinline__ void register_body(P tab, const float* __restrict__ gtab, int nP,
+                                              const Cells& g, const IO& io, float* bins,
+                                              int* keys, float* __restrict__ mom_b) {
   constexpr int PP = Dim<D>::P;
   const float h = 1.0f / (float)TS;
   const float hh = h * 0.5f;
-  const float hhh = hh * h;
   int lo, hi;
   wg_range(nP, lo, hi);
   for (int base = lo; base < hi; base += blockDim.x) {
@@ -435,6 +444,7 @@ __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g, con
 #pragma unroll
     for (int k = 0; k < PP; ++k) m[k] = 0.0f;
     int prev = -1;
+    Adj<D> G;
 #pragma unroll
     for (int t = TS - 1; t >= 0; --t) {
       const int c = (int)((t & 1) ? (cells[t >> 1] >> 16) : (cells[t >> 1] & 0xffffu));
@@ -447,10 +457,10 @@ __device__ __forceinline__ void register_body(P tab, int nP, const Cells& g, con
         }
 #pragma unroll
         for (int k = 0; k < PP; ++k) m[k] = 0.0f;
-        A = fetch<D>(tab, c);
+        G = fetch_adj<D>(gtab, c);
       }
       prev = c;
-      adjoint(A, traj[t], h, hh, hhh, m, lam);
+      adjoint(G, traj[t], m, lam);
     }
     if (valid) {
       if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, prev, m);
@@ -509,15 +519,15 @@ struct StageLds {
 
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS, typename IO>
 __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, const float* Ag,
-                                          int nP, int T, const Cells& g, const IO& io,
-                                          float* __restrict__ mom_b) {
+                                          const float* Gg, int nP, int T, const Cells& g,
+                                          const IO& io, float* __restrict__ mom_b) {
   if constexpr (TS > 0) {
     static_assert(BINS != kBinsGlobal, "the register variant accumulates in LDS");
-    if (LDS_A) register_body<D, ADAPTIVE, BINS, TS>(as_lds(L.ldsA), nP, g, io, L.bins, L.keys, mom_b);
-    else register_body<D, ADAPTIVE, BINS, TS>(Ag, nP, g, io, L.bins, L.keys, mom_b);
+    if (LDS_A) register_body<D, ADAPTIVE, BINS, TS>(as_lds(L.ldsA), Gg, nP, g, io, L.bins, L.keys, mom_b);
+    else register_body<D, ADAPTIVE, BINS, TS>(Ag, Gg, nP, g, io, L.bins, L.keys, mom_b);
   } else {
-    if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(L.ldsA), nP, T, g, io, L.bins, L.keys, mom_b);
-    else segmented_body<D, ADAPTIVE, BINS>(Ag, nP, T, g, io, L.bins, L.keys, mom_b);
+    if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(L.ldsA), Gg, nP, T, g, io, L.bins, L.keys, mom_b);
+    else segmented_body<D, ADAPTIVE, BINS>(Ag, Gg, nP, T, g, io, L.bins, L.keys, mom_b);
   }
 }
 
@@ -528,7 +538,8 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
 // `points` (k = 0) or stage_points[k-1], its seed from grad_out (k = K-1) or
 // the lam buffer the stage above wrote for the same points, and writes the
 // adjoint of its input to lam (k > 0) or grad_points (k = 0).  Moments of
-// stage k go to partials / moments row (k * n_batch + b).
+// stage k go to partials / moments row (k * n_batch + b); the adjoint
+// increment table G holds the same rows (AdjStride<D>::S floats per cell).
 // Launch bound: 768 threads (3 waves per SIMD, up to 168 VGPRs), or 512 (2 waves
 // per SIMD, 256 VGPRs) for the 3D register variant whose trajectory alone takes
 // 150 VGPRs.
@@ -539,7 +550,7 @@ template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 __global__ __launch_bounds__((kBwdThreads<D, TS>)) void backward_kernel(
     int nP, int batched, int T, Cells g, int nC, int K, const float* __restrict__ points,
     const float* __restrict__ stage_points, const float* __restrict__ As,
-    const float* __restrict__ grad_out, float* __restrict__ moments, float* __restrict__ partials,
+    const float* __restrict__ Gs, const float* __restrict__ grad_out, float* __restrict__ moments, float* __restrict__ partials,
     float* __restrict__ lam, float* __restrict__ grad_points) {
   extern __shared__ float lds[];
   const int b = blockIdx.y;
@@ -550,6 +561,7 @@ __global__ __launch_bounds__((kBwdThreads<D, TS>)) void backward_kernel(
   for (int k = K - 1; k >= 0; --k) {
     const size_t row = (size_t)k * n_batch + b;
     const float* __restrict__ Ag = As + row * R;
+    const float* __restrict__ Gg = Gs + row * nC * AdjStride<D>::S;
     PlainIO<D> io;
     io.nP = nP;
     io.pts = k == 0 ? points + (batched ? (size_t)b * plane : 0)
@@ -558,7 +570,7 @@ __global__ __launch_bounds__((kBwdThreads<D, TS>)) void backward_kernel(
     io.lam_out = k == 0 ? (grad_points ? grad_points + (size_t)b * plane : nullptr)
                         : lam + (size_t)b * plane;
     L.begin(Ag, R);
-    run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, nP, T, g, io, moments + row * R);
+    run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, nP, T, g, io, moments + row * R);
     // Every lane is done with this stage's tables before they are written out
     // (and, for the next stage, overwritten).
     L.end(partials + (row * gridDim.x + blockIdx.x) * R, moments + row * R, R);
@@ -572,13 +584,14 @@ template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 __global__ __launch_bounds__((kBwdThreads<D, TS>)) void image_backward_kernel(
     ImageShape s, int T, Cells g, int nC, const float* __restrict__ grid,
     const float* __restrict__ final_points, const float* __restrict__ As,
-    const float* __restrict__ data, const float* __restrict__ grad_out,
+    const float* __restrict__ Gs, const float* __restrict__ data, const float* __restrict__ grad_out,
     float* __restrict__ moments, float* __restrict__ partials, float* __restrict__ grad_data) {
   extern __shared__ float lds[];
   const int b = blockIdx.y;
   const int R = nC * Dim<D>::P;
   const StageLds<D, LDS_A, BINS> L(lds, R);
   const float* __restrict__ Ag = As + (size_t)b * R;
+  const float* __restrict__ Gg = Gs + (size_t)b * nC * AdjStride<D>::S;
   ImageIO<D> io;
   io.s = s;
   io.grid = grid;
@@ -587,7 +600,7 @@ __global__ __launch_bounds__((kBwdThreads<D, TS>)) void image_backward_kernel(
   io.data = data + (size_t)b * s.C * s.plane_in;
   io.gdata = grad_data ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
   L.begin(Ag, R);
-  run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, s.nP, T, g, io, moments + (size_t)b * R);
+  run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, s.nP, T, g, io, moments + (size_t)b * R);
   L.end(partials + ((size_t)b * gridDim.x + blockIdx.x) * R, moments + (size_t)b * R, R);
 }
 
@@ -613,7 +626,7 @@ struct BackwardJob {
   Geometry geo;
   int64_t nP, n_batch;
   int batched, T, K;
-  const float *points, *stage_points, *As, *grad_out;
+  const float *points, *stage_points, *As, *G, *grad_out;
   float *moments, *partials, *lam, *grad_points;
   const ImageShape* image;
   const float *grid, *final_points, *data;
@@ -630,15 +643,15 @@ hipError_t go(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
     hipError_t e = allow_lds(kernel, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, grid, block, lds, s, *j.image, j.T, g, j.geo.nC, j.grid,
-                       j.final_points, j.As, j.data, j.grad_out, j.moments, j.partials,
+                       j.final_points, j.As, j.G, j.data, j.grad_out, j.moments, j.partials,
                        j.grad_data);
   } else {
     auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
     hipError_t e = allow_lds(kernel, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, grid, block, lds, s, (int)j.nP, j.batched, j.T, g, j.geo.nC, j.K,
-                       j.points, j.stage_points, j.As, j.grad_out, j.moments, j.partials, j.lam,
-                       j.grad_points);
+                       j.points, j.stage_points, j.As, j.G, j.grad_out, j.moments, j.partials,
+                       j.lam, j.grad_points);
   }
   return hipGetLastError();
 }
@@ -696,7 +709,7 @@ hipError_t dispatch_any(const BackwardJob& j, int adaptive, const LaunchCfg& cfg
 
 hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
                            int K, int adaptive, const float* points, const float* stage_points,
-                           const float* As, const float* grad_out, float* moments,
+                           const float* As, const float* G, const float* grad_out, float* moments,
                            float* partials, float* lam, float* grad_points, const LaunchCfg& cfg,
                            hipStream_t s) {
   BackwardJob j{};
@@ -709,6 +722,7 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
   j.points = points;
   j.stage_points = stage_points;
   j.As = As;
+  j.G = G;
   j.grad_out = grad_out;
   j.moments = moments;
   j.partials = partials;
@@ -719,9 +733,9 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
 
 hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
                                  int adaptive, const float* grid, const float* final_points,
-                                 const float* As, const float* data, const float* grad_out,
-                                 float* moments, float* partials, float* grad_data,
-                                 const LaunchCfg& cfg, hipStream_t s) {
+                                 const float* As, const float* G, const float* data,
+                                 const float* grad_out, float* moments, float* partials,
+                                 float* grad_data, const LaunchCfg& cfg, hipStream_t s) {
   BackwardJob j{};
   j.geo = g;
   j.nP = img.nP;
@@ -729,6 +743,7 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
   j.T = T;
   j.K = 1;
   j.As = As;
+  j.G = G;
   j.grad_out = grad_out;
   j.moments = moments;
   j.partials = partials;

@@ -2,7 +2,9 @@
 //   affine   A = B theta          (replaces torch.sparse.mm, cpab/pytorch/transformer.py:84)
 //   expm     Trels = expm(dT A)   (cpab_ops_1d.cu:404-429, 2d.cu:537-653, 3d.cu:538-674)
 //   project  dtheta = B^T vec(M)  (replaces torch.sparse.mm, transformer.py:165-166)
-//   reduce   moments = sum of per-workgroup partial moment tables
+//   adjoint table   G = h A + (h^2/2) A^2 per cell (the factored reverse step)
+//   finish   moments from the per-cell sums S of the reverse sweep, after
+//            summing the per-workgroup partial tables
 //   sum      grad_points.sum(0)   (transformer.py:151-152)
 // These are latency-sized (µs) next to the integrator; they exist so the
 // whole path stays on HIP with fixed, reproducible summation orders.
@@ -53,18 +55,54 @@ __global__ void project_kernel(int64_t n_theta, int D, int d, const float* __res
   grad[i] = acc;
 }
 
-// moments[b, r] = sum_w partials[b, w, r], w ascending (deterministic).
-__global__ void reduce_partials_kernel(int64_t n_theta, int nparts, int R,
-                                       const float* __restrict__ partials,
-                                       float* __restrict__ moments) {
+// One thread per cell row of the table: G[i] = h A_lin + (h^2/2) A_lin^2 of
+// cell i (cpab_device.hpp, adjoint_increment).
+template <int D>
+__global__ void adjoint_table_kernel(int64_t n_cells, float h, const float* __restrict__ As,
+                                     float* __restrict__ G) {
+  constexpr int P = D * (D + 1);
+  constexpr int S = AdjStride<D>::S;
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= n_theta * R) return;
-  const int64_t b = i / R;
-  const int r = (int)(i - b * R);
-  const float* src = partials + b * (int64_t)nparts * R + r;
-  float acc = 0.0f;
-  for (int w = 0; w < nparts; ++w) acc += src[(int64_t)w * R];
-  moments[i] = acc;
+  if (i >= n_cells) return;
+  float a[P], g[S];
+#pragma unroll
+  for (int k = 0; k < P; ++k) a[k] = As[i * P + k];
+  adjoint_increment<D>(a, h, (h * 0.5f) * h, g);
+#pragma unroll
+  for (int k = 0; k < S; ++k) G[i * S + k] = g[k];
+}
+
+// One thread per (row, cell): S = sum_w partials[row, w, cell] (w ascending,
+// deterministic), or S read in place from `moments` when nparts == 0; then the
+// cell's moments from S and its A (cpab_device.hpp, moments_from_s).
+template <int D>
+__global__ void finish_moments_kernel(int64_t n_cells, int nC, int nparts, float h,
+                                      const float* __restrict__ partials,
+                                      const float* __restrict__ As, float* __restrict__ moments) {
+  constexpr int P = D * (D + 1);
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n_cells) return;
+  float s[P];
+  if (nparts > 0) {
+    const int64_t R = (int64_t)nC * P;
+    const int64_t row = i / nC;
+    const float* src = partials + row * nparts * R + (i - row * nC) * P;
+#pragma unroll
+    for (int k = 0; k < P; ++k) s[k] = 0.0f;
+    for (int w = 0; w < nparts; ++w) {
+#pragma unroll
+      for (int k = 0; k < P; ++k) s[k] += src[w * R + k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < P; ++k) s[k] = moments[i * P + k];
+  }
+  float a[P], m[P];
+#pragma unroll
+  for (int k = 0; k < P; ++k) a[k] = As[i * P + k];
+  moments_from_s<D>(a, s, h, (h * 0.5f) * h, m);
+#pragma unroll
+  for (int k = 0; k < P; ++k) moments[i * P + k] = m[k];
 }
 
 // dst[i] = sum_b src[b, i], b ascending.
@@ -295,12 +333,30 @@ hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
   return hipGetLastError();
 }
 
-hipError_t launch_reduce_partials(int64_t n_theta, int nparts, int R, const float* partials,
-                                  float* moments, hipStream_t s) {
-  const int64_t n = n_theta * R;
+hipError_t launch_adjoint_table(int ndim, int64_t n_cells, int T, const float* As, float* G,
+                                hipStream_t s) {
+  if (n_cells <= 0) return hipSuccess;
+  const float h = 1.0f / (float)T;
+  const dim3 g(grid_for(n_cells, 256)), b(256);
+  if (ndim == 1) hipLaunchKernelGGL(adjoint_table_kernel<1>, g, b, 0, s, n_cells, h, As, G);
+  else if (ndim == 2) hipLaunchKernelGGL(adjoint_table_kernel<2>, g, b, 0, s, n_cells, h, As, G);
+  else hipLaunchKernelGGL(adjoint_table_kernel<3>, g, b, 0, s, n_cells, h, As, G);
+  return hipGetLastError();
+}
+
+hipError_t launch_finish_moments(int ndim, int64_t rows, int nC, int nparts, int T,
+                                 const float* partials, const float* As, float* moments,
+                                 hipStream_t s) {
+  const int64_t n = rows * nC;
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(reduce_partials_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, n_theta,
-                     nparts, R, partials, moments);
+  const float h = 1.0f / (float)T;
+  const dim3 g(grid_for(n, 256)), b(256);
+  if (ndim == 1)
+    hipLaunchKernelGGL(finish_moments_kernel<1>, g, b, 0, s, n, nC, nparts, h, partials, As, moments);
+  else if (ndim == 2)
+    hipLaunchKernelGGL(finish_moments_kernel<2>, g, b, 0, s, n, nC, nparts, h, partials, As, moments);
+  else
+    hipLaunchKernelGGL(finish_moments_kernel<3>, g, b, 0, s, n, nC, nparts, h, partials, As, moments);
   return hipGetLastError();
 }
 

@@ -250,18 +250,22 @@ constexpr int64_t kAlign = 256;
 
 int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
-// Workspace of a K-stage backward: per-workgroup partial moment tables (full
-// LDS bins only), then the inter-stage adjoint [n_batch, ndim, nP] (K > 1).
+// Workspace of a K-stage backward: per-workgroup partial tables (full LDS bins
+// only), the inter-stage adjoint [n_batch, ndim, nP] (K > 1), then the adjoint
+// increment table G [K * n_batch, nC, 1|4|12].
 struct BackwardWorkspace {
-  int64_t partials_bytes, lam_offset, total;
+  int64_t partials_bytes, lam_offset, g_offset, total;
 };
+
+int adj_stride(int ndim) { return ndim == 1 ? 1 : (ndim == 2 ? 4 : 12); }
 
 BackwardWorkspace backward_workspace(const cpab::Geometry& g, int64_t nP, int64_t n_batch, int K,
                                      const cpab::LaunchCfg& cfg) {
   BackwardWorkspace w{};
   w.partials_bytes = cfg.lds_bins ? (int64_t)K * n_batch * cfg.chunks * g.nC * g.ppc() * 4 : 0;
   w.lam_offset = align_up(w.partials_bytes);
-  w.total = K > 1 ? w.lam_offset + n_batch * g.ndim * nP * 4 : w.partials_bytes;
+  w.g_offset = K > 1 ? align_up(w.lam_offset + n_batch * g.ndim * nP * 4) : w.lam_offset;
+  w.total = w.g_offset + (int64_t)K * n_batch * g.nC * adj_stride(g.ndim) * 4;
   return w;
 }
 
@@ -304,23 +308,27 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
                 (long long)w.total, (long long)workspace_bytes);
-  float* partials = static_cast<float*>(workspace);
-  float* lam = K > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + w.lam_offset) : nullptr;
+  char* ws = static_cast<char*>(workspace);
+  float* partials = reinterpret_cast<float*>(ws);
+  float* lam = K > 1 ? reinterpret_cast<float*>(ws + w.lam_offset) : nullptr;
+  float* G = reinterpret_cast<float*>(ws + w.g_offset);
   if (!cfg.lds_bins) {
     rc = check_hip(cpab::launch_fill(moments, rows * R, 0.0f, s), who);
     if (rc) return rc;
   }
+  rc = check_hip(cpab::launch_adjoint_table(ndim, rows * g.nC, nstepsolver, As, G, s), who);
+  if (rc) return rc;
   hipEvent_t ev;
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_backward(g, nP, n_batch, batched ? 1 : 0, nstepsolver, K, adaptive,
-                                       points, stage_points, As, grad_out, moments, partials, lam,
-                                       grad_points, cfg, s),
+                                       points, stage_points, As, G, grad_out, moments, partials,
+                                       lam, grad_points, cfg, s),
                  who);
   prof_end(timed, ev, "backward", s);
   if (rc) return rc;
-  if (cfg.lds_bins)
-    rc = check_hip(cpab::launch_reduce_partials(rows, cfg.chunks, R, partials, moments, s), who);
-  return rc;
+  return check_hip(cpab::launch_finish_moments(ndim, rows, g.nC, cfg.lds_bins ? cfg.chunks : 0,
+                                               nstepsolver, partials, As, moments, s),
+                   who);
 }
 
 // Image geometry of the fused transform_data calls (validated like the
@@ -509,10 +517,15 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
                 (long long)w.total, (long long)workspace_bytes);
+  float* partials = static_cast<float*>(workspace);
+  float* G = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.g_offset);
   if (!cfg.lds_bins) {
     rc = check_hip(cpab::launch_fill(moments, n_batch * R, 0.0f, s), "cpab_transform_data_backward");
     if (rc) return rc;
   }
+  rc = check_hip(cpab::launch_adjoint_table(ndim, n_batch * g.nC, nstepsolver, As, G, s),
+                 "cpab_transform_data_backward");
+  if (rc) return rc;
   if (grad_data) {
     rc = check_hip(cpab::launch_fill(grad_data, n_batch * n_channels * img.plane_in, 0.0f, s),
                    "cpab_transform_data_backward");
@@ -521,16 +534,14 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   hipEvent_t ev;
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, grid,
-                                             final_points, As, data, grad_out, moments,
-                                             static_cast<float*>(workspace), grad_data, cfg, s),
+                                             final_points, As, G, data, grad_out, moments,
+                                             partials, grad_data, cfg, s),
                  "cpab_transform_data_backward");
   prof_end(timed, ev, "image_backward", s);
   if (rc) return rc;
-  if (cfg.lds_bins)
-    rc = check_hip(cpab::launch_reduce_partials(n_batch, cfg.chunks, R,
-                                                static_cast<float*>(workspace), moments, s),
+  return check_hip(cpab::launch_finish_moments(ndim, n_batch, g.nC, cfg.lds_bins ? cfg.chunks : 0,
+                                               nstepsolver, partials, As, moments, s),
                    "cpab_transform_data_backward");
-  return rc;
 }
 
 int cpab_project(int64_t n_theta, int D, int d, const float* moments, const int32_t* col_ptr,

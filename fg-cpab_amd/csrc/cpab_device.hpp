@@ -345,4 +345,117 @@ __device__ __forceinline__ void adjoint3(const Aff<3>& A, float px, float py, fl
   lz = fmaf(h, atz, lz);
 }
 
+// ---------------------------------------------------------------------------
+// Factored adjoint sweep.  With Ã = [A; 0] the (ndim+1)^2 augmented field and
+// p̃ = [p; 1], the step above is, in exact arithmetic,
+//   lam <- lam + G^T lam,            G = h A_lin + (h^2/2) A_lin^2
+//   M   += h lam p̃^T (I + (h/2) Ã^T) + (h^2/2) A_lin^T lam p̃^T
+// (p_mid = p + (h/2) Ã p̃, and lam + h A^T (lam + (h/2) A^T lam) = (I + G)^T lam).
+// M is linear in lam p̃^T and A is constant inside a cell, so the sweep only
+// accumulates S = sum lam p̃^T per cell and the moments follow once per cell
+// after all trajectories are summed:
+//   M = h S + (h^2/2) (S Ã^T + A_lin^T S)                       (moments_from_s)
+// The adjoint step reads G from a per-cell table (adjoint_increment).  Same
+// mathematics as cpab_ops_2d.cu:334-382; the rounding differs from the
+// reference's op order by a few ulp.
+// ---------------------------------------------------------------------------
+
+// Row stride (floats) of the G table: 1x1, 2x2, 3x3 padded to 3 rows of 4.
+template <int D> struct AdjStride;
+template <> struct AdjStride<1> { static constexpr int S = 1; };
+template <> struct AdjStride<2> { static constexpr int S = 4; };
+template <> struct AdjStride<3> { static constexpr int S = 12; };
+
+template <int D> struct Adj;
+template <> struct Adj<1> { float g; };
+template <> struct Adj<2> { float g[4]; };   // row-major g00 g01 g10 g11
+template <> struct Adj<3> { float g[9]; };   // row-major, stored with a zero 4th column
+
+__device__ __forceinline__ Adj<1> load_adj1(const float* tab, int c) { return {tab[c]}; }
+__device__ __forceinline__ Adj<2> load_adj2(const float* tab, int c) {
+  const v4f v = reinterpret_cast<const v4f*>(tab)[c];
+  return {{v.x, v.y, v.z, v.w}};
+}
+__device__ __forceinline__ Adj<3> load_adj3(const float* tab, int c) {
+  const v4f* q = reinterpret_cast<const v4f*>(tab) + 3 * (int64_t)c;
+  const v4f a = q[0], b = q[1], d = q[2];
+  return {{a.x, a.y, a.z, b.x, b.y, b.z, d.x, d.y, d.z}};
+}
+
+// One reverse step: S += lam (x) [p; 1], then lam += G^T lam.
+__device__ __forceinline__ void adjoint_s1(const Adj<1>& G, float px, float s[2], float& lam) {
+  s[0] = fmaf(lam, px, s[0]);
+  s[1] = s[1] + lam;
+  lam = fmaf(G.g, lam, lam);
+}
+__device__ __forceinline__ void adjoint_s2(const Adj<2>& G, float px, float py, float s[6],
+                                           float& lx, float& ly) {
+  s[0] = fmaf(lx, px, s[0]);
+  s[1] = fmaf(lx, py, s[1]);
+  s[2] = s[2] + lx;
+  s[3] = fmaf(ly, px, s[3]);
+  s[4] = fmaf(ly, py, s[4]);
+  s[5] = s[5] + ly;
+  const float nx = fmaf(G.g[0], lx, fmaf(G.g[2], ly, lx));
+  const float ny = fmaf(G.g[1], lx, fmaf(G.g[3], ly, ly));
+  lx = nx;
+  ly = ny;
+}
+__device__ __forceinline__ void adjoint_s3(const Adj<3>& G, float px, float py, float pz,
+                                           float s[12], float& lx, float& ly, float& lz) {
+  const float l[3] = {lx, ly, lz};
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    s[4 * k + 0] = fmaf(l[k], px, s[4 * k + 0]);
+    s[4 * k + 1] = fmaf(l[k], py, s[4 * k + 1]);
+    s[4 * k + 2] = fmaf(l[k], pz, s[4 * k + 2]);
+    s[4 * k + 3] = s[4 * k + 3] + l[k];
+  }
+  const float* g = G.g;
+  lx = fmaf(g[0], l[0], fmaf(g[3], l[1], fmaf(g[6], l[2], l[0])));
+  ly = fmaf(g[1], l[0], fmaf(g[4], l[1], fmaf(g[7], l[2], l[1])));
+  lz = fmaf(g[2], l[0], fmaf(g[5], l[1], fmaf(g[8], l[2], l[2])));
+}
+
+// G = h A_lin + (h^2/2) A_lin^2 of one cell; `a` is the row-major [D, D+1]
+// block of A, `hhh` = (h/2)*h.  Writes AdjStride<D>::S floats.
+template <int D>
+__device__ __forceinline__ void adjoint_increment(const float* a, float h, float hhh, float* g) {
+  constexpr int W = D + 1;
+  constexpr int RS = D == 3 ? 4 : D;  // row stride inside the table entry
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      float sq = 0.0f;
+#pragma unroll
+      for (int r = 0; r < D; ++r) sq = fmaf(a[i * W + r], a[r * W + j], sq);
+      g[i * RS + j] = fmaf(h, a[i * W + j], hhh * sq);
+    }
+    if (RS > D) g[i * RS + D] = 0.0f;
+  }
+}
+
+// Moments of one cell from its accumulated S (both row-major [D, D+1]):
+//   M_kq = h S_kq + hhh (sum_{r<D} S_kr A_qr + S_kD A_qD [q<D] + sum_j A_jk S_jq)
+template <int D>
+__device__ __forceinline__ void moments_from_s(const float* a, const float* s, float h, float hhh,
+                                               float* m) {
+  constexpr int W = D + 1;
+#pragma unroll
+  for (int k = 0; k < D; ++k) {
+#pragma unroll
+    for (int q = 0; q < W; ++q) {
+      float t = 0.0f;
+      if (q < D) {
+#pragma unroll
+        for (int r = 0; r < W; ++r) t = fmaf(s[k * W + r], a[q * W + r], t);
+      }
+#pragma unroll
+      for (int j = 0; j < D; ++j) t = fmaf(a[j * W + k], s[j * W + q], t);
+      m[k * W + q] = fmaf(h, s[k * W + q], hhh * t);
+    }
+  }
+}
+
 }  // namespace cpab

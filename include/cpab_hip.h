@@ -77,13 +77,18 @@ int cpab_trace_cells(int ndim, int64_t nP, int64_t n_theta, int batched, int nst
                      int ncx, int ncy, int ncz, int adaptive, const float* points,
                      const float* Trels, const float* As, int32_t* cells, void* stream);
 
-/* Bytes of device workspace cpab_backward needs for this problem (may be 0). */
+/* Bytes of device workspace cpab_backward needs for this problem: per-cell
+ * adjoint increments h*A + (h^2/2)*A^2 (1, 4 or 12 floats per cell and theta)
+ * and, where the moments are privatised per workgroup, the partial tables. */
 int64_t cpab_backward_workspace_size(int ndim, int64_t nP, int64_t n_theta, int nC);
 
 /* Fused backward: cell moments [n_theta, nC, ndim*(ndim+1)] (overwritten, no
  * need to zero them) and, if grad_points != NULL, the point adjoints
  * [n_theta, ndim, nP].  `workspace` must hold
- * cpab_backward_workspace_size(...) bytes (NULL if that is 0).
+ * cpab_backward_workspace_size(...) bytes.  The reverse sweep is the
+ * reference's discrete adjoint (cpab_ops_2d.cu:334-382) in factored form, so
+ * moments and point adjoints agree with it to rounding (a few ulp per step),
+ * not bit for bit; the replayed trajectory and its cells are bit-exact.
  * Replaces cpab_gpu.backward_moments (transformer_cuda.cpp:92-116) and
  * cpab_gpu.backward_moments_and_points (transformer_cuda.cpp:122-153). */
 int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
@@ -107,8 +112,8 @@ int cpab_chain_forward(int ndim, int64_t nP, int64_t n_batch, int batched, int n
                        const float* points, const float* Trels, const float* As, float* out,
                        float* stage_points, void* stream);
 
-/* Bytes of device workspace cpab_chain_backward needs (partial moment tables
- * and the adjoint carried between stages). */
+/* Bytes of device workspace cpab_chain_backward needs (adjoint increments,
+ * partial tables and the adjoint carried between stages). */
 int64_t cpab_chain_backward_workspace_size(int ndim, int64_t nP, int64_t n_batch, int n_stages,
                                            int nC);
 

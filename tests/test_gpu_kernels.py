@@ -1,8 +1,8 @@
 """Kernel-level parity: HIP library (through its C ABI) vs the CPU oracle on the
 same seeded inputs.  Bit-exact for the fixed-step integrators, cell sequences,
-the 1D closed form, point adjoints, affine map, expm and projection; within
-tolerance only for the moment sums (float atomics, no fixed order) and the
-interpolation backward."""
+the 1D closed form, affine map, expm and projection; within tolerance for the
+moment sums (float atomics, no fixed order, and the factored reverse sweep),
+the point adjoints (factored reverse sweep) and the interpolation backward."""
 import numpy as np
 import pytest
 import torch
@@ -11,7 +11,8 @@ from cpab.pytorch._native import native
 from cpab.pytorch.transformer import basis_tables
 from oracle import oracle as orc
 
-from helpers import assert_grad_close, cpab_for, meshgrid, seeded_theta, uniform_points
+from helpers import (assert_adjoint_close, assert_grad_close, cpab_for, meshgrid, seeded_theta,
+                     uniform_points)
 
 pytestmark = pytest.mark.gpu
 
@@ -156,7 +157,30 @@ def test_backward_parity(cuda, tess, kind, n, adaptive):
     g = np.random.default_rng(62).standard_normal((3, nd, pts.shape[-1])).astype(np.float32)
     As, mom, gp = _backward_case(T, theta, pts, g, cuda, adaptive=adaptive)
     ref_m, ref_gp = orc.backward(pts, As, g, tess, 50, adaptive=bool(adaptive))
-    np.testing.assert_array_equal(gp, ref_gp)
+    assert_adjoint_close(gp, ref_gp)
+    assert_grad_close(mom, ref_m, rtol=2e-5)
+
+
+@pytest.mark.parametrize("tess,kind,nstep", [([50], "line", 20), ([20, 20], "uniform", 37),
+                                             ([30, 30], "mesh", 100), ([4, 4, 4], "uniform", 20),
+                                             ([10, 10, 10], "mesh", 37)])
+def test_backward_segmented_steps(cuda, tess, kind, nstep):
+    # nstepsolver != 50 runs the segmented replay (a checkpoint every 8 steps,
+    # replayed per segment; 37 and 20 leave a partial last segment; 100 is the
+    # step cap).
+    T = cpab_for(tess)
+    nd = len(tess)
+    theta = seeded_theta(T, 2, 0.5, 90 + nd)
+    if kind == "line":
+        pts = np.linspace(0, 1, 4000, dtype=np.float32)[None]
+    elif kind == "uniform":
+        pts = uniform_points(nd, 6000, 91)
+    else:
+        pts = meshgrid([48, 40] if nd == 2 else [23, 19, 17])
+    g = np.random.default_rng(92).standard_normal((2, nd, pts.shape[-1])).astype(np.float32)
+    As, mom, gp = _backward_case(T, theta, pts, g, cuda, nstep=nstep)
+    ref_m, ref_gp = orc.backward(pts, As, g, tess, nstep)
+    assert_adjoint_close(gp, ref_gp)
     assert_grad_close(mom, ref_m, rtol=2e-5)
 
 
@@ -176,7 +200,7 @@ def test_backward_3d_moment_paths(cuda, monkeypatch, mode, kind, n):
     g = np.random.default_rng(73).standard_normal((1, 3, pts.shape[-1])).astype(np.float32)
     As, mom, gp = _backward_case(T, theta, pts, g, cuda)
     ref_m, ref_gp = orc.backward(pts, As, g, [10, 10, 10], 50)
-    np.testing.assert_array_equal(gp, ref_gp)
+    assert_adjoint_close(gp, ref_gp)
     assert_grad_close(mom, ref_m, rtol=2e-5)
 
 
@@ -258,9 +282,9 @@ def test_interp_unaligned_grid(cuda):
 def test_chain_matches_stagewise(cuda, tess, kind, adaptive):
     # cpab_chain_forward / cpab_chain_backward against the stage-by-stage
     # composition the reference's transform_grid_chain performs
-    # (cpab/cpab.py:270-278): stage outputs and stage inputs bit-exact, the
-    # adjoint handed from stage to stage bit-exact (grad_points), moments of
-    # every stage within tolerance.
+    # (cpab/cpab.py:270-278): stage outputs and stage inputs bit-exact; the
+    # adjoint handed from stage to stage (grad_points) and the moments of every
+    # stage within tolerance.
     T = cpab_for(tess)
     p = T.params
     nd = len(tess)
@@ -307,7 +331,7 @@ def test_chain_matches_stagewise(cuda, tess, kind, adaptive):
     for s in reversed(range(K)):
         ref_m, lam = orc.backward(xs[s], A[s], lam, p.nc, 50, adaptive=bool(adaptive))
         assert_grad_close(M[s], ref_m, rtol=2e-5)
-    np.testing.assert_array_equal(gp.cpu().numpy(), lam)
+    assert_adjoint_close(gp.cpu().numpy(), lam)
 
 
 def _image_order(x, outs):
