@@ -21,15 +21,24 @@
 // Moment accumulation on MI355X: each workgroup serves ONE theta and one
 // contiguous range of points (spatially coherent for meshgrid inputs).
 //   full bins  the nC x ppc table fits in LDS: the workgroup keeps a private
-//              copy of that theta's moments there (ds_add_f32, no HBM
-//              atomics) and writes it as one partial with plain coalesced
-//              stores; a separate pass sums the partials in a fixed order.
+//              copy of that theta's sums there (ds_add_f32, no HBM atomics
+//              while integrating).  At the end a workgroup that touched at
+//              least a quarter of the cells (random points: every workgroup
+//              touches nearly every cell) stores its whole table as its
+//              partial (plain coalesced stores) and sets its bit in the row's
+//              dense-part mask; one that touched fewer (meshgrids, chains:
+//              few workgroups share a cell) adds its cells' sums to the HBM
+//              table with global atomics instead.  A separate pass adds the
+//              dense partials, in ascending order, to the HBM sums and forms
+//              the moments.  Cross-XCD atomics on shared addresses are what
+//              the dense case avoids.
 //   cache      the table does not fit (3D at 10x10x10: 234 KiB): a
 //              direct-mapped LDS cache of kCacheSlots cells (linear probing,
 //              kCacheProbes slots) collects the flushes of the cells the
 //              workgroup touches; at the end each occupied slot is added to
-//              the moments with global atomics.  Flushes that find no slot
-//              go straight to HBM.
+//              HBM with global atomics.  Flushes that find no slot go
+//              straight to HBM.  The HBM table holds sums S; a separate pass
+//              forms the moments in place.
 //   global     every flush is a global_atomic_add_f32, pre-aggregated across
 //              the wave for lanes that share a cell.
 #include <hip/hip_runtime.h>
@@ -483,8 +492,8 @@ struct StageLds {
     keys = reinterpret_cast<int*>(after_a);
     bins = BINS == kBinsCache ? after_a + kCacheSlots : after_a;
   }
-  // Stage the table, clear the bins / cache.
-  __device__ __forceinline__ void begin(const float* __restrict__ Ag, int R) const {
+  // Stage the table, clear the bins / cache (and the touched-cell counter).
+  __device__ __forceinline__ void begin(const float* __restrict__ Ag, int R, int* touched_cnt) const {
     constexpr int PP = Dim<D>::P;
     if (LDS_A) {
       const float2* s2 = reinterpret_cast<const float2*>(Ag);
@@ -493,20 +502,46 @@ struct StageLds {
     }
     if (BINS == kBinsFull) {
       for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
+      if (threadIdx.x == 0) *touched_cnt = 0;
     } else if (BINS == kBinsCache) {
       for (int i = threadIdx.x; i < kCacheSlots; i += blockDim.x) keys[i] = -1;
       for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) bins[i] = 0.0f;
     }
     if (LDS_A || BINS != kBinsGlobal) __syncthreads();
   }
-  // After every lane is done: full bins -> this workgroup's partial (plain
-  // stores); cache -> HBM atomics of the occupied slots.
-  __device__ __forceinline__ void end(float* __restrict__ partial, float* __restrict__ mom_b,
-                                      int R) const {
+  // After every lane is done: full bins -> a dense workgroup's table into its
+  // partial (and its bit `part` into the row's dense-part mask), a sparse
+  // one's touched cells added to the HBM sums; cache -> HBM atomics of the
+  // occupied slots' sums.  `touched_cnt` is an LDS counter that begin() cleared.
+  __device__ __forceinline__ void end(float* __restrict__ partial,
+                                      uint64_t* __restrict__ dense_parts, int part,
+                                      float* __restrict__ mom_b, int nC, int* touched_cnt) const {
     constexpr int PP = Dim<D>::P;
     if (LDS_A || BINS != kBinsGlobal) __syncthreads();
     if (BINS == kBinsFull) {
-      for (int i = threadIdx.x; i < R; i += blockDim.x) partial[i] = bins[i];
+      auto cell_touched = [&](int i) {
+        bool t = false;
+#pragma unroll
+        for (int k = 0; k < PP; ++k) t |= bins[i * PP + k] != 0.0f;
+        return t;
+      };
+      int cnt = 0;
+      for (int i = threadIdx.x; i < nC; i += blockDim.x) cnt += cell_touched(i) ? 1 : 0;
+      if (cnt) __hip_atomic_fetch_add(touched_cnt, cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __syncthreads();
+      const bool dense = 4 * *touched_cnt >= nC;
+      if (dense) {
+        for (int i = threadIdx.x; i < nC * PP; i += blockDim.x) partial[i] = bins[i];
+        if (threadIdx.x == 0)
+          __hip_atomic_fetch_or(dense_parts + part / 64, 1ull << (part & 63), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        for (int i = threadIdx.x; i < nC; i += blockDim.x) {
+          if (!cell_touched(i)) continue;
+#pragma unroll
+          for (int k = 0; k < PP; ++k) unsafeAtomicAdd(mom_b + (size_t)i * PP + k, bins[i * PP + k]);
+        }
+      }
     } else if (BINS == kBinsCache) {
       for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) {
         const int slot = i / PP;
@@ -537,9 +572,11 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
 // stages last to first inside the kernel: stage k reads its input points from
 // `points` (k = 0) or stage_points[k-1], its seed from grad_out (k = K-1) or
 // the lam buffer the stage above wrote for the same points, and writes the
-// adjoint of its input to lam (k > 0) or grad_points (k = 0).  Moments of
-// stage k go to partials / moments row (k * n_batch + b); the adjoint
-// increment table G holds the same rows (AdjStride<D>::S floats per cell).
+// adjoint of its input to lam (k > 0) or grad_points (k = 0).  The per-cell
+// sums of stage k go to row (k * n_batch + b): added to that moments row (zero
+// on entry), or, from a dense full-bin workgroup, to its partial table with
+// its dense-part bit set; the adjoint increment table G holds the same rows
+// (AdjStride<D>::S floats per cell).
 // Launch bound: 768 threads (3 waves per SIMD, up to 168 VGPRs), or 512 (2 waves
 // per SIMD, 256 VGPRs) for the 3D register variant whose trajectory alone takes
 // 150 VGPRs.
@@ -550,9 +587,11 @@ template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 __global__ __launch_bounds__((kBwdThreads<D, TS>)) void backward_kernel(
     int nP, int batched, int T, Cells g, int nC, int K, const float* __restrict__ points,
     const float* __restrict__ stage_points, const float* __restrict__ As,
-    const float* __restrict__ Gs, const float* __restrict__ grad_out, float* __restrict__ moments, float* __restrict__ partials,
-    float* __restrict__ lam, float* __restrict__ grad_points) {
+    const float* __restrict__ Gs, const float* __restrict__ grad_out, float* __restrict__ moments,
+    float* __restrict__ partials, uint64_t* __restrict__ dense_parts, float* __restrict__ lam,
+    float* __restrict__ grad_points) {
   extern __shared__ float lds[];
+  __shared__ int touched_cnt;
   const int b = blockIdx.y;
   const int n_batch = gridDim.y;
   const int R = nC * Dim<D>::P;
@@ -569,11 +608,13 @@ __global__ __launch_bounds__((kBwdThreads<D, TS>)) void backward_kernel(
     io.gout = k == K - 1 ? grad_out + (size_t)b * plane : lam + (size_t)b * plane;
     io.lam_out = k == 0 ? (grad_points ? grad_points + (size_t)b * plane : nullptr)
                         : lam + (size_t)b * plane;
-    L.begin(Ag, R);
+    L.begin(Ag, R, &touched_cnt);
     run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, nP, T, g, io, moments + row * R);
     // Every lane is done with this stage's tables before they are written out
     // (and, for the next stage, overwritten).
-    L.end(partials + (row * gridDim.x + blockIdx.x) * R, moments + row * R, R);
+    const size_t part = row * gridDim.x + blockIdx.x;
+    L.end(partials + part * R, dense_parts + row * ((gridDim.x + 63) / 64), (int)blockIdx.x,
+          moments + row * R, nC, &touched_cnt);
     if (k > 0 && (LDS_A || BINS != kBinsGlobal)) __syncthreads();
   }
 }
@@ -585,8 +626,10 @@ __global__ __launch_bounds__((kBwdThreads<D, TS>)) void image_backward_kernel(
     ImageShape s, int T, Cells g, int nC, const float* __restrict__ grid,
     const float* __restrict__ final_points, const float* __restrict__ As,
     const float* __restrict__ Gs, const float* __restrict__ data, const float* __restrict__ grad_out,
-    float* __restrict__ moments, float* __restrict__ partials, float* __restrict__ grad_data) {
+    float* __restrict__ moments, float* __restrict__ partials, uint64_t* __restrict__ dense_parts,
+    float* __restrict__ grad_data) {
   extern __shared__ float lds[];
+  __shared__ int touched_cnt;
   const int b = blockIdx.y;
   const int R = nC * Dim<D>::P;
   const StageLds<D, LDS_A, BINS> L(lds, R);
@@ -599,9 +642,11 @@ __global__ __launch_bounds__((kBwdThreads<D, TS>)) void image_backward_kernel(
   io.gout = grad_out + (size_t)b * s.C * s.nP;
   io.data = data + (size_t)b * s.C * s.plane_in;
   io.gdata = grad_data ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
-  L.begin(Ag, R);
+  L.begin(Ag, R, &touched_cnt);
   run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, s.nP, T, g, io, moments + (size_t)b * R);
-  L.end(partials + ((size_t)b * gridDim.x + blockIdx.x) * R, moments + (size_t)b * R, R);
+  const size_t part = (size_t)b * gridDim.x + blockIdx.x;
+  L.end(partials + part * R, dense_parts + (size_t)b * ((gridDim.x + 63) / 64), (int)blockIdx.x,
+        moments + (size_t)b * R, nC, &touched_cnt);
 }
 
 template <int D, bool LDS_A, int BINS>
@@ -628,6 +673,7 @@ struct BackwardJob {
   int batched, T, K;
   const float *points, *stage_points, *As, *G, *grad_out;
   float *moments, *partials, *lam, *grad_points;
+  uint64_t* dense_parts;
   const ImageShape* image;
   const float *grid, *final_points, *data;
   float* grad_data;
@@ -644,14 +690,14 @@ hipError_t go(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, grid, block, lds, s, *j.image, j.T, g, j.geo.nC, j.grid,
                        j.final_points, j.As, j.G, j.data, j.grad_out, j.moments, j.partials,
-                       j.grad_data);
+                       j.dense_parts, j.grad_data);
   } else {
     auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
     hipError_t e = allow_lds(kernel, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, grid, block, lds, s, (int)j.nP, j.batched, j.T, g, j.geo.nC, j.K,
                        j.points, j.stage_points, j.As, j.G, j.grad_out, j.moments, j.partials,
-                       j.lam, j.grad_points);
+                       j.dense_parts, j.lam, j.grad_points);
   }
   return hipGetLastError();
 }
@@ -710,8 +756,8 @@ hipError_t dispatch_any(const BackwardJob& j, int adaptive, const LaunchCfg& cfg
 hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
                            int K, int adaptive, const float* points, const float* stage_points,
                            const float* As, const float* G, const float* grad_out, float* moments,
-                           float* partials, float* lam, float* grad_points, const LaunchCfg& cfg,
-                           hipStream_t s) {
+                           float* partials, uint64_t* dense_parts, float* lam, float* grad_points,
+                           const LaunchCfg& cfg, hipStream_t s) {
   BackwardJob j{};
   j.geo = g;
   j.nP = nP;
@@ -726,6 +772,7 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
   j.grad_out = grad_out;
   j.moments = moments;
   j.partials = partials;
+  j.dense_parts = dense_parts;
   j.lam = lam;
   j.grad_points = grad_points;
   return dispatch_any(j, adaptive, cfg, s);
@@ -735,7 +782,8 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
                                  int adaptive, const float* grid, const float* final_points,
                                  const float* As, const float* G, const float* data,
                                  const float* grad_out, float* moments, float* partials,
-                                 float* grad_data, const LaunchCfg& cfg, hipStream_t s) {
+                                 uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
+                                 hipStream_t s) {
   BackwardJob j{};
   j.geo = g;
   j.nP = img.nP;
@@ -747,6 +795,7 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
   j.grad_out = grad_out;
   j.moments = moments;
   j.partials = partials;
+  j.dense_parts = dense_parts;
   j.image = &img;
   j.grid = grid;
   j.final_points = final_points;

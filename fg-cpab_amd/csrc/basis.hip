@@ -2,14 +2,16 @@
 //   affine   A = B theta          (replaces torch.sparse.mm, cpab/pytorch/transformer.py:84)
 //   expm     Trels = expm(dT A)   (cpab_ops_1d.cu:404-429, 2d.cu:537-653, 3d.cu:538-674)
 //   project  dtheta = B^T vec(M)  (replaces torch.sparse.mm, transformer.py:165-166)
-//   adjoint table   G = h A + (h^2/2) A^2 per cell (the factored reverse step)
-//   finish   moments from the per-cell sums S of the reverse sweep, after
-//            summing the per-workgroup partial tables
+//   adjoint table   G = h A + (h^2/2) A^2 per cell (the factored reverse step);
+//            also clears the HBM sums and dense-part masks the backward fills
+//   finish   moments from the per-cell sums S of the reverse sweep: the HBM
+//            sums plus the dense per-workgroup partial tables
 //   sum      grad_points.sum(0)   (transformer.py:151-152)
 // These are latency-sized (µs) next to the integrator; they exist so the
 // whole path stays on HIP with fixed, reproducible summation orders.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <algorithm>
 #include "cpab_device.hpp"
 #include "cpab_launch.hpp"
 
@@ -56,13 +58,16 @@ __global__ void project_kernel(int64_t n_theta, int D, int d, const float* __res
 }
 
 // One thread per cell row of the table: G[i] = h A_lin + (h^2/2) A_lin^2 of
-// cell i (cpab_device.hpp, adjoint_increment).
+// cell i (cpab_device.hpp, adjoint_increment), the cell's sums zeroed; the
+// first n_words threads also clear the dense-part masks.
 template <int D>
 __global__ void adjoint_table_kernel(int64_t n_cells, float h, const float* __restrict__ As,
-                                     float* __restrict__ G) {
+                                     float* __restrict__ G, float* __restrict__ moments,
+                                     uint64_t* __restrict__ dense_parts, int64_t n_words) {
   constexpr int P = D * (D + 1);
   constexpr int S = AdjStride<D>::S;
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n_words) dense_parts[i] = 0;
   if (i >= n_cells) return;
   float a[P], g[S];
 #pragma unroll
@@ -70,32 +75,39 @@ __global__ void adjoint_table_kernel(int64_t n_cells, float h, const float* __re
   adjoint_increment<D>(a, h, (h * 0.5f) * h, g);
 #pragma unroll
   for (int k = 0; k < S; ++k) G[i * S + k] = g[k];
+#pragma unroll
+  for (int k = 0; k < P; ++k) moments[i * P + k] = 0.0f;
 }
 
-// One thread per (row, cell): S = sum_w partials[row, w, cell] (w ascending,
-// deterministic), or S read in place from `moments` when nparts == 0; then the
-// cell's moments from S and its A (cpab_device.hpp, moments_from_s).
+// One thread per (row, cell): S = the HBM sum in `moments` plus
+// partials[row, w, cell] for every part w set in the row's dense-part mask
+// (ascending, a fixed order); then the cell's moments from S and its A
+// (cpab_device.hpp, moments_from_s), in place.
 template <int D>
 __global__ void finish_moments_kernel(int64_t n_cells, int nC, int nparts, float h,
                                       const float* __restrict__ partials,
+                                      const uint64_t* __restrict__ dense_parts,
                                       const float* __restrict__ As, float* __restrict__ moments) {
   constexpr int P = D * (D + 1);
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= n_cells) return;
   float s[P];
+#pragma unroll
+  for (int k = 0; k < P; ++k) s[k] = moments[i * P + k];
   if (nparts > 0) {
     const int64_t R = (int64_t)nC * P;
+    const int NW = (nparts + 63) / 64;
     const int64_t row = i / nC;
     const float* src = partials + row * nparts * R + (i - row * nC) * P;
+    for (int q = 0; q < NW; ++q) {
+      uint64_t bits = dense_parts[row * NW + q];
+      while (bits) {
+        const int w = q * 64 + __builtin_ctzll(bits);
+        bits &= bits - 1;
 #pragma unroll
-    for (int k = 0; k < P; ++k) s[k] = 0.0f;
-    for (int w = 0; w < nparts; ++w) {
-#pragma unroll
-      for (int k = 0; k < P; ++k) s[k] += src[w * R + k];
+        for (int k = 0; k < P; ++k) s[k] += src[w * R + k];
+      }
     }
-  } else {
-#pragma unroll
-    for (int k = 0; k < P; ++k) s[k] = moments[i * P + k];
   }
   float a[P], m[P];
 #pragma unroll
@@ -334,29 +346,36 @@ hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
 }
 
 hipError_t launch_adjoint_table(int ndim, int64_t n_cells, int T, const float* As, float* G,
+                                float* moments, uint64_t* dense_parts, int64_t n_words,
                                 hipStream_t s) {
   if (n_cells <= 0) return hipSuccess;
   const float h = 1.0f / (float)T;
-  const dim3 g(grid_for(n_cells, 256)), b(256);
-  if (ndim == 1) hipLaunchKernelGGL(adjoint_table_kernel<1>, g, b, 0, s, n_cells, h, As, G);
-  else if (ndim == 2) hipLaunchKernelGGL(adjoint_table_kernel<2>, g, b, 0, s, n_cells, h, As, G);
-  else hipLaunchKernelGGL(adjoint_table_kernel<3>, g, b, 0, s, n_cells, h, As, G);
+  const dim3 g(grid_for(std::max(n_cells, n_words), 256)), b(256);
+  if (ndim == 1)
+    hipLaunchKernelGGL(adjoint_table_kernel<1>, g, b, 0, s, n_cells, h, As, G, moments, dense_parts, n_words);
+  else if (ndim == 2)
+    hipLaunchKernelGGL(adjoint_table_kernel<2>, g, b, 0, s, n_cells, h, As, G, moments, dense_parts, n_words);
+  else
+    hipLaunchKernelGGL(adjoint_table_kernel<3>, g, b, 0, s, n_cells, h, As, G, moments, dense_parts, n_words);
   return hipGetLastError();
 }
 
 hipError_t launch_finish_moments(int ndim, int64_t rows, int nC, int nparts, int T,
-                                 const float* partials, const float* As, float* moments,
-                                 hipStream_t s) {
+                                 const float* partials, const uint64_t* dense_parts,
+                                 const float* As, float* moments, hipStream_t s) {
   const int64_t n = rows * nC;
   if (n <= 0) return hipSuccess;
   const float h = 1.0f / (float)T;
   const dim3 g(grid_for(n, 256)), b(256);
   if (ndim == 1)
-    hipLaunchKernelGGL(finish_moments_kernel<1>, g, b, 0, s, n, nC, nparts, h, partials, As, moments);
+    hipLaunchKernelGGL(finish_moments_kernel<1>, g, b, 0, s, n, nC, nparts, h, partials, dense_parts,
+                       As, moments);
   else if (ndim == 2)
-    hipLaunchKernelGGL(finish_moments_kernel<2>, g, b, 0, s, n, nC, nparts, h, partials, As, moments);
+    hipLaunchKernelGGL(finish_moments_kernel<2>, g, b, 0, s, n, nC, nparts, h, partials, dense_parts,
+                       As, moments);
   else
-    hipLaunchKernelGGL(finish_moments_kernel<3>, g, b, 0, s, n, nC, nparts, h, partials, As, moments);
+    hipLaunchKernelGGL(finish_moments_kernel<3>, g, b, 0, s, n, nC, nparts, h, partials, dense_parts,
+                       As, moments);
   return hipGetLastError();
 }
 

@@ -250,11 +250,12 @@ constexpr int64_t kAlign = 256;
 
 int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
-// Workspace of a K-stage backward: per-workgroup partial tables (full LDS bins
-// only), the inter-stage adjoint [n_batch, ndim, nP] (K > 1), then the adjoint
-// increment table G [K * n_batch, nC, 1|4|12].
+// Workspace of a K-stage backward (rows = K * n_batch): with full LDS bins the
+// dense-part masks [rows, ceil(chunks/64)] and the partial tables
+// [rows, chunks, nC, ppc]; then the inter-stage adjoint [n_batch, ndim, nP]
+// (K > 1) and the adjoint increment table G [rows, nC, 1|4|12].
 struct BackwardWorkspace {
-  int64_t partials_bytes, lam_offset, g_offset, total;
+  int64_t dense_words, partials_offset, lam_offset, g_offset, total;
 };
 
 int adj_stride(int ndim) { return ndim == 1 ? 1 : (ndim == 2 ? 4 : 12); }
@@ -262,8 +263,10 @@ int adj_stride(int ndim) { return ndim == 1 ? 1 : (ndim == 2 ? 4 : 12); }
 BackwardWorkspace backward_workspace(const cpab::Geometry& g, int64_t nP, int64_t n_batch, int K,
                                      const cpab::LaunchCfg& cfg) {
   BackwardWorkspace w{};
-  w.partials_bytes = cfg.lds_bins ? (int64_t)K * n_batch * cfg.chunks * g.nC * g.ppc() * 4 : 0;
-  w.lam_offset = align_up(w.partials_bytes);
+  const int64_t parts = cfg.lds_bins ? (int64_t)K * n_batch * cfg.chunks : 0;
+  w.dense_words = cfg.lds_bins ? (int64_t)K * n_batch * ((cfg.chunks + 63) / 64) : 0;
+  w.partials_offset = align_up(w.dense_words * 8);
+  w.lam_offset = align_up(w.partials_offset + parts * g.nC * g.ppc() * 4);
   w.g_offset = K > 1 ? align_up(w.lam_offset + n_batch * g.ndim * nP * 4) : w.lam_offset;
   w.total = w.g_offset + (int64_t)K * n_batch * g.nC * adj_stride(g.ndim) * 4;
   return w;
@@ -305,29 +308,30 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   if (K > 1) CPAB_REQUIRE(stage_points);
   const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_batch, nstepsolver, adaptive);
   const BackwardWorkspace w = backward_workspace(g, nP, n_batch, K, cfg);
-  if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
+  if (workspace == nullptr || workspace_bytes < w.total)
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
                 (long long)w.total, (long long)workspace_bytes);
   char* ws = static_cast<char*>(workspace);
-  float* partials = reinterpret_cast<float*>(ws);
+  uint64_t* dense = reinterpret_cast<uint64_t*>(ws);
+  float* partials = reinterpret_cast<float*>(ws + w.partials_offset);
   float* lam = K > 1 ? reinterpret_cast<float*>(ws + w.lam_offset) : nullptr;
   float* G = reinterpret_cast<float*>(ws + w.g_offset);
-  if (!cfg.lds_bins) {
-    rc = check_hip(cpab::launch_fill(moments, rows * R, 0.0f, s), who);
-    if (rc) return rc;
-  }
-  rc = check_hip(cpab::launch_adjoint_table(ndim, rows * g.nC, nstepsolver, As, G, s), who);
+  // G table; the HBM sums and dense-part masks cleared.
+  rc = check_hip(cpab::launch_adjoint_table(ndim, rows * g.nC, nstepsolver, As, G, moments, dense,
+                                            w.dense_words, s),
+                 who);
   if (rc) return rc;
   hipEvent_t ev;
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_backward(g, nP, n_batch, batched ? 1 : 0, nstepsolver, K, adaptive,
                                        points, stage_points, As, G, grad_out, moments, partials,
-                                       lam, grad_points, cfg, s),
+                                       dense, lam, grad_points, cfg, s),
                  who);
   prof_end(timed, ev, "backward", s);
   if (rc) return rc;
   return check_hip(cpab::launch_finish_moments(ndim, rows, g.nC, cfg.lds_bins ? cfg.chunks : 0,
-                                               nstepsolver, partials, As, moments, s),
+                                               nstepsolver, partials, dense, As, moments,
+                                               s),
                    who);
 }
 
@@ -511,19 +515,17 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(workspace, 16);
   CPAB_REQUIRE(grad_out); CPAB_REQUIRE(moments);
   hipStream_t s = as_stream(stream);
-  const int R = g.nC * g.ppc();
   const cpab::LaunchCfg cfg = backward_cfg(g, img.nP, n_batch, nstepsolver, adaptive);
   const BackwardWorkspace w = backward_workspace(g, img.nP, n_batch, 1, cfg);
-  if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
+  if (workspace == nullptr || workspace_bytes < w.total)
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
                 (long long)w.total, (long long)workspace_bytes);
-  float* partials = static_cast<float*>(workspace);
-  float* G = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.g_offset);
-  if (!cfg.lds_bins) {
-    rc = check_hip(cpab::launch_fill(moments, n_batch * R, 0.0f, s), "cpab_transform_data_backward");
-    if (rc) return rc;
-  }
-  rc = check_hip(cpab::launch_adjoint_table(ndim, n_batch * g.nC, nstepsolver, As, G, s),
+  char* ws = static_cast<char*>(workspace);
+  uint64_t* dense = reinterpret_cast<uint64_t*>(ws);
+  float* partials = reinterpret_cast<float*>(ws + w.partials_offset);
+  float* G = reinterpret_cast<float*>(ws + w.g_offset);
+  rc = check_hip(cpab::launch_adjoint_table(ndim, n_batch * g.nC, nstepsolver, As, G, moments,
+                                            dense, w.dense_words, s),
                  "cpab_transform_data_backward");
   if (rc) return rc;
   if (grad_data) {
@@ -535,12 +537,13 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, grid,
                                              final_points, As, G, data, grad_out, moments,
-                                             partials, grad_data, cfg, s),
+                                             partials, dense, grad_data, cfg, s),
                  "cpab_transform_data_backward");
   prof_end(timed, ev, "image_backward", s);
   if (rc) return rc;
   return check_hip(cpab::launch_finish_moments(ndim, n_batch, g.nC, cfg.lds_bins ? cfg.chunks : 0,
-                                               nstepsolver, partials, As, moments, s),
+                                               nstepsolver, partials, dense, As, moments,
+                                               s),
                    "cpab_transform_data_backward");
 }
 

@@ -37,15 +37,17 @@ hipError_t launch_expm(int ndim, int64_t n, float dT, const float* As, float* Tr
 hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
                           const int32_t* col_ptr, const int32_t* row_idx, const float* vals,
                           float* grad_theta, hipStream_t s);
-// G [n_cells, AdjStride] = h A + (h^2/2) A^2 per cell, h = 1/T.
+// G [n_cells, AdjStride] = h A + (h^2/2) A^2 per cell, h = 1/T; zeroes
+// moments [n_cells, ppc] (the HBM sums) and dense_parts [n_words].
 hipError_t launch_adjoint_table(int ndim, int64_t n_cells, int T, const float* As, float* G,
+                                float* moments, uint64_t* dense_parts, int64_t n_words,
                                 hipStream_t s);
-// moments [rows, nC, ppc] from the reverse sweep's per-cell sums S: summed over
-// `nparts` per-workgroup partial tables [rows, nparts, nC, ppc], or (nparts = 0)
-// read in place from `moments`.
+// moments [rows, nC, ppc] from the reverse sweep's per-cell sums S, in place:
+// the HBM sums in `moments` plus the partial tables [rows, nparts, nC, ppc] of
+// the parts set in dense_parts [rows, ceil(nparts/64)], in ascending order.
 hipError_t launch_finish_moments(int ndim, int64_t rows, int nC, int nparts, int T,
-                                 const float* partials, const float* As, float* moments,
-                                 hipStream_t s);
+                                 const float* partials, const uint64_t* dense_parts,
+                                 const float* As, float* moments, hipStream_t s);
 hipError_t launch_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, hipStream_t s);
 
 hipError_t launch_forward_1d(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int K,
@@ -62,12 +64,15 @@ hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, in
                               const float* As, int32_t* cells, hipStream_t s);
 // lam: [n_batch, ndim, nP] scratch carrying the adjoint between stages (K > 1).
 // G: the adjoint increment table of launch_adjoint_table, same rows as As.
-// moments / partials receive the per-cell sums S (launch_finish_moments).
+// The per-cell sums S go to moments (HBM sums, zero on entry) or, for a
+// full-bin workgroup that touched a quarter of the cells or more, to its
+// partial table [rows, chunks, nC, ppc] with its bit set in dense_parts
+// [rows, ceil(chunks/64)] (zero on entry).  launch_finish_moments follows.
 hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
                            int K, int adaptive, const float* points, const float* stage_points,
                            const float* As, const float* G, const float* grad_out, float* moments,
-                           float* partials, float* lam, float* grad_points, const LaunchCfg& cfg,
-                           hipStream_t s);
+                           float* partials, uint64_t* dense_parts, float* lam, float* grad_points,
+                           const LaunchCfg& cfg, hipStream_t s);
 
 // Fused transform_data (image-ordered outputs; see cpab_sample.hpp ImageShape).
 hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
@@ -78,7 +83,8 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
                                  int adaptive, const float* grid, const float* final_points,
                                  const float* As, const float* G, const float* data,
                                  const float* grad_out, float* moments, float* partials,
-                                 float* grad_data, const LaunchCfg& cfg, hipStream_t s);
+                                 uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
+                                 hipStream_t s);
 
 hipError_t launch_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
                                  const int64_t* out_size, const float* data, const float* grid,

@@ -79,7 +79,8 @@ int cpab_trace_cells(int ndim, int64_t nP, int64_t n_theta, int batched, int nst
 
 /* Bytes of device workspace cpab_backward needs for this problem: per-cell
  * adjoint increments h*A + (h^2/2)*A^2 (1, 4 or 12 floats per cell and theta)
- * and, where the moments are privatised per workgroup, the partial tables. */
+ * and, where the sums are privatised per workgroup, the partial tables with
+ * their touched-cell masks. */
 int64_t cpab_backward_workspace_size(int ndim, int64_t nP, int64_t n_theta, int nC);
 
 /* Fused backward: cell moments [n_theta, nC, ndim*(ndim+1)] (overwritten, no
