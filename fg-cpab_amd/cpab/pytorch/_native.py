@@ -25,6 +25,8 @@ _SIGNATURES = {
     "cpab_abi_version": (_c_int, []),
     "cpab_affine": (_c_int, [_c_int, _c_i64, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "cpab_expm": (_c_int, [_c_int, _c_i64, _c_f32, _c_vp, _c_vp, _c_vp]),
+    "cpab_affine_expm": (_c_int, [_c_int, _c_i64, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
+                                  _c_f32, _c_vp, _c_vp, _c_vp]),
     "cpab_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int,
                               _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "cpab_forward_1d_closed_form": (_c_int, [_c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
@@ -120,6 +122,12 @@ class Native:
         _check(self.lib.cpab_affine(ndim, theta.shape[0], nC, theta.shape[1], _ptr(theta),
                                     _ptr(row_ptr), _ptr(col_idx), _ptr(vals), _ptr(As),
                                     _stream(theta.device)), "cpab_affine")
+
+    def affine_expm(self, ndim, theta, nC, row_ptr, col_idx, vals, dT, As, Trels):
+        _check(self.lib.cpab_affine_expm(ndim, theta.shape[0], nC, theta.shape[1], _ptr(theta),
+                                         _ptr(row_ptr), _ptr(col_idx), _ptr(vals), float(dT),
+                                         _ptr(As), _ptr(Trels), _stream(theta.device)),
+               "cpab_affine_expm")
 
     def expm(self, ndim, As, dT, Trels):
         n = As.numel() // (ndim * (ndim + 1))

@@ -6,8 +6,9 @@ the integrated points ``[n_theta, ndim, nP]`` and differentiates w.r.t. theta
 (and the points when asked).  Every numeric step runs in the HIP library
 (``libcpab_hip.so``) through its C ABI:
 
-  forward   A = B theta (cpab_affine) -> expm(A/T) (cpab_expm) -> integrate
-            (cpab_forward), or the 1D closed form      (transformer.py:72-126)
+  forward   A = B theta and expm(A/T) in one launch (cpab_affine_expm) ->
+            integrate (cpab_forward), or A = B theta (cpab_affine) and the 1D
+            closed form                                 (transformer.py:72-126)
   backward  fused replay + adjoint + moments (cpab_backward) -> dtheta = B^T M
             (cpab_project) [-> sum over theta for shared points]
                                                         (transformer.py:128-168)
@@ -114,17 +115,17 @@ class _CPABFunction(torch.autograd.Function):
         points_c = points.detach().contiguous()
 
         As = torch.empty((n_theta, nC, ndim, ndim + 1), device=dev, dtype=torch.float32)
-        lib.affine(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"], As)
-
         nstepsolver = int(params.nstepsolver)
         adaptive = int(getattr(params, "adaptive_substeps", False))
         nc = [int(v) for v in params.nc]
         out = torch.empty((n_theta, ndim, nP), device=dev, dtype=torch.float32)
         if ndim == 1:
+            lib.affine(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"], As)
             lib.forward_1d_closed_form(points_c, batched, n_theta, nP, nc[0], As, out)
         else:
             Trels = torch.empty_like(As)
-            lib.expm(ndim, As, 1.0 / nstepsolver, Trels)
+            lib.affine_expm(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"],
+                            1.0 / nstepsolver, As, Trels)
             lib.forward(ndim, points_c, batched, n_theta, nP, nstepsolver, nc, adaptive, Trels,
                         As, out)
 
@@ -203,14 +204,16 @@ class _CPABChainFunction(torch.autograd.Function):
         points_c = points.detach().contiguous()
 
         As = torch.empty((K * n_batch, nC, ndim, ndim + 1), device=dev, dtype=torch.float32)
-        lib.affine(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"], As)
         nstepsolver = int(params.nstepsolver)
         adaptive = int(getattr(params, "adaptive_substeps", False))
         nc = [int(v) for v in params.nc]
         Trels = None
         if ndim > 1:
             Trels = torch.empty_like(As)
-            lib.expm(ndim, As, 1.0 / nstepsolver, Trels)
+            lib.affine_expm(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"],
+                            1.0 / nstepsolver, As, Trels)
+        else:
+            lib.affine(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"], As)
         grad_wanted = any(ctx.needs_input_grad[:2])
         stage_points = (torch.empty((K - 1, n_batch, ndim, nP), device=dev, dtype=torch.float32)
                         if grad_wanted and K > 1 else None)
@@ -300,15 +303,17 @@ class _CPABImageFunction(torch.autograd.Function):
         data_c = data.detach().contiguous()
         grid_c = grid.detach().contiguous()
         As = torch.empty((n, nC, ndim, ndim + 1), device=dev, dtype=torch.float32)
-        lib.affine(ndim, theta.detach().contiguous(), nC, tab["row_ptr"], tab["col_idx"],
-                   tab["vals"], As)
+        theta_c = theta.detach().contiguous()
         T = int(params.nstepsolver)
         adaptive = int(getattr(params, "adaptive_substeps", False))
         nc = [int(v) for v in params.nc]
         Trels = None
         if ndim > 1:
             Trels = torch.empty_like(As)
-            lib.expm(ndim, As, 1.0 / T, Trels)
+            lib.affine_expm(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"],
+                            1.0 / T, As, Trels)
+        else:
+            lib.affine(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"], As)
         grad_wanted = ctx.needs_input_grad[0] or ctx.needs_input_grad[1]
         final = (torch.empty((n, ndim, nP), device=dev, dtype=torch.float32)
                  if grad_wanted else None)

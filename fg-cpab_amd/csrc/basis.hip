@@ -1,6 +1,7 @@
 // Small per-theta kernels around the integrator:
 //   affine   A = B theta          (replaces torch.sparse.mm, cpab/pytorch/transformer.py:84)
 //   expm     Trels = expm(dT A)   (cpab_ops_1d.cu:404-429, 2d.cu:537-653, 3d.cu:538-674)
+//   affine + expm in one pass (the forward's table setup)
 //   project  dtheta = B^T vec(M)  (replaces torch.sparse.mm, transformer.py:165-166)
 //   adjoint table   G = h A + (h^2/2) A^2 per cell (the factored reverse step);
 //            also clears the HBM sums and dense-part masks the backward fills
@@ -42,18 +43,36 @@ __global__ void affine_kernel(int64_t n_theta, int rows, int d, const float* __r
 }
 
 // One thread per (theta, column j of B): grad[b, j] = sum_k B[row_k, j] * M[b, row_k],
-// in ascending row order.
+// in ascending row order.  The column is read eight entries at a time (indices
+// and values, then the eight gathers) so the loads overlap; the products are
+// still added one by one in order.
 __global__ void project_kernel(int64_t n_theta, int D, int d, const float* __restrict__ M,
                                const int32_t* __restrict__ col_ptr,
                                const int32_t* __restrict__ row_idx,
                                const float* __restrict__ vals, float* __restrict__ grad) {
+  constexpr int U = 8;
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= n_theta * d) return;
   const int64_t b = i / d;
   const int j = (int)(i - b * d);
   const float* m = M + b * D;
   float acc = 0.0f;
-  for (int k = col_ptr[j]; k < col_ptr[j + 1]; ++k) acc = fmaf(vals[k], m[row_idx[k]], acc);
+  const int e = col_ptr[j + 1];
+  for (int k = col_ptr[j]; k < e; k += U) {
+    int r[U];
+    float v[U], x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool ok = k + u < e;
+      r[u] = ok ? row_idx[k + u] : 0;
+      v[u] = ok ? vals[k + u] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) x[u] = m[r[u]];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (k + u < e) acc = fmaf(v[u], x[u], acc);
+  }
   grad[i] = acc;
 }
 
@@ -99,13 +118,27 @@ __global__ void finish_moments_kernel(int64_t n_cells, int nC, int nparts, float
     const int NW = (nparts + 63) / 64;
     const int64_t row = i / nC;
     const float* src = partials + row * nparts * R + (i - row * nC) * P;
+    constexpr int U = 4;  // parts loaded together, then added in order
     for (int q = 0; q < NW; ++q) {
       uint64_t bits = dense_parts[row * NW + q];
       while (bits) {
-        const int w = q * 64 + __builtin_ctzll(bits);
-        bits &= bits - 1;
+        int w[U];
 #pragma unroll
-        for (int k = 0; k < P; ++k) s[k] += src[w * R + k];
+        for (int u = 0; u < U; ++u) {
+          w[u] = bits ? q * 64 + __builtin_ctzll(bits) : -1;
+          bits &= bits - 1;
+        }
+        float x[U][P];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int k = 0; k < P; ++k) x[u][k] = w[u] >= 0 ? src[w[u] * R + k] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (w[u] >= 0) {
+#pragma unroll
+            for (int k = 0; k < P; ++k) s[k] += x[u][k];
+          }
       }
     }
   }
@@ -130,11 +163,10 @@ __global__ void sum_batch_kernel(int64_t n_theta, int64_t n, const float* __rest
 
 // ---- matrix exponentials of dT*[A; 0] (affine, last row zero) -------------
 
-__global__ void expm2_kernel(int64_t n, float dT, const float* __restrict__ As,
-                             float* __restrict__ out) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float m00 = dT * As[2 * i], m01 = dT * As[2 * i + 1];
+// One cell's exponential: A is the row-major [D, D+1] block, out the same
+// shape.  1D: [exp(m), m01 * (exp(m) - 1) / m].
+__device__ __forceinline__ void expm_cell2(const float* A, float dT, float* out) {
+  const float m00 = dT * A[0], m01 = dT * A[1];
   float exprel;
   if (fabsf(m00) > 1e-6f) {
     exprel = expm1_cr(m00) / m00;
@@ -142,8 +174,8 @@ __global__ void expm2_kernel(int64_t n, float dT, const float* __restrict__ As,
     const float m2 = m00 * m00;
     exprel = fmaf((1.0f / 24.0f) * m2, m00, fmaf(1.0f / 6.0f, m2, fmaf(0.5f, m00, 1.0f)));
   }
-  out[2 * i] = exp_cr(m00);
-  out[2 * i + 1] = m01 * exprel;
+  out[0] = exp_cr(m00);
+  out[1] = m01 * exprel;
 }
 
 __device__ __forceinline__ int n_squarings(float norm) {
@@ -151,11 +183,7 @@ __device__ __forceinline__ int n_squarings(float norm) {
 }
 
 // Pade(3,3) with scaling and squaring: R = Q^{-1} P, P/Q = I +- M/2 + M^2/12.
-__global__ void expm3_kernel(int64_t n, float dT, const float* __restrict__ As,
-                             float* __restrict__ out) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float* A = As + 6 * i;
+__device__ __forceinline__ void expm_cell3(const float* A, float dT, float* o) {
   const float a00 = dT * A[0], a01 = dT * A[1], a02 = dT * A[2];
   const float a10 = dT * A[3], a11 = dT * A[4], a12 = dT * A[5];
   float nsq = fmaf(a00, a00, a01 * a01);
@@ -194,7 +222,6 @@ __global__ void expm3_kernel(int64_t n, float dT, const float* __restrict__ As,
     const float n12 = fmaf(r10, r02, r11 * r12) + r12;
     r00 = n00; r01 = n01; r02 = n02; r10 = n10; r11 = n11; r12 = n12;
   }
-  float* o = out + 6 * i;
   o[0] = r00; o[1] = r01; o[2] = r02; o[3] = r10; o[4] = r11; o[5] = r12;
 }
 
@@ -207,11 +234,7 @@ __device__ __forceinline__ float cross2(float x1, float y1, float x2, float y2) 
   return fmaf(x1, y1, -(x2 * y2));
 }
 
-__global__ void expm4_kernel(int64_t n, float dT, const float* __restrict__ As,
-                             float* __restrict__ out) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float* A = As + 12 * i;
+__device__ __forceinline__ void expm_cell4(const float* A, float dT, float* o) {
   float a[12];
 #pragma unroll
   for (int k = 0; k < 12; ++k) a[k] = dT * A[k];
@@ -293,11 +316,62 @@ __global__ void expm4_kernel(int64_t n, float dT, const float* __restrict__ As,
 #pragma unroll
       for (int c = 0; c < 4; ++c) R[r][c] = N[r][c];
   }
-  float* o = out + 12 * i;
 #pragma unroll
   for (int r = 0; r < 3; ++r)
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[4 * r + c] = R[r][c];
+}
+
+template <int D> __device__ __forceinline__ void expm_cell(const float* A, float dT, float* o);
+template <> __device__ __forceinline__ void expm_cell<1>(const float* A, float dT, float* o) { expm_cell2(A, dT, o); }
+template <> __device__ __forceinline__ void expm_cell<2>(const float* A, float dT, float* o) { expm_cell3(A, dT, o); }
+template <> __device__ __forceinline__ void expm_cell<3>(const float* A, float dT, float* o) { expm_cell4(A, dT, o); }
+
+// One thread per cell matrix: Trels[i] = expm(dT * As[i]).
+template <int D>
+__global__ void expm_kernel(int64_t n, float dT, const float* __restrict__ As,
+                            float* __restrict__ out) {
+  constexpr int P = D * (D + 1);
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float a[P], r[P];
+#pragma unroll
+  for (int k = 0; k < P; ++k) a[k] = As[i * P + k];
+  expm_cell<D>(a, dT, r);
+#pragma unroll
+  for (int k = 0; k < P; ++k) out[i * P + k] = r[k];
+}
+
+// A = B theta and Trels = expm(dT A) in one pass: one thread per (theta, cell)
+// forms the cell's P rows of A exactly as affine_kernel does (each row summed
+// in ascending column order), stores them, and exponentiates them in registers
+// as expm_kernel does, so both outputs equal the two-kernel sequence bit for
+// bit.
+template <int D>
+__global__ void affine_expm_kernel(int64_t n_theta, int nC, int d, const float* __restrict__ theta,
+                                   const int32_t* __restrict__ row_ptr,
+                                   const int32_t* __restrict__ col_idx,
+                                   const float* __restrict__ vals, float dT,
+                                   float* __restrict__ As, float* __restrict__ Trels) {
+  constexpr int P = D * (D + 1);
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n_theta * nC) return;
+  const int64_t b = i / nC;
+  const int c = (int)(i - b * nC);
+  const float* th = theta + b * d;
+  float a[P], r[P];
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const int row = c * P + j;
+    float acc = 0.0f;
+    for (int k = row_ptr[row]; k < row_ptr[row + 1]; ++k) acc = fmaf(vals[k], th[col_idx[k]], acc);
+    a[j] = acc;
+  }
+#pragma unroll
+  for (int k = 0; k < P; ++k) As[i * P + k] = a[k];
+  expm_cell<D>(a, dT, r);
+#pragma unroll
+  for (int k = 0; k < P; ++k) Trels[i * P + k] = r[k];
 }
 
 inline unsigned grid_for(int64_t n, int block) {
@@ -329,9 +403,27 @@ hipError_t launch_expm(int ndim, int64_t n, float dT, const float* As, float* Tr
                        hipStream_t s) {
   if (n <= 0) return hipSuccess;
   const dim3 g(grid_for(n, 256)), b(256);
-  if (ndim == 1) hipLaunchKernelGGL(expm2_kernel, g, b, 0, s, n, dT, As, Trels);
-  else if (ndim == 2) hipLaunchKernelGGL(expm3_kernel, g, b, 0, s, n, dT, As, Trels);
-  else hipLaunchKernelGGL(expm4_kernel, g, b, 0, s, n, dT, As, Trels);
+  if (ndim == 1) hipLaunchKernelGGL(expm_kernel<1>, g, b, 0, s, n, dT, As, Trels);
+  else if (ndim == 2) hipLaunchKernelGGL(expm_kernel<2>, g, b, 0, s, n, dT, As, Trels);
+  else hipLaunchKernelGGL(expm_kernel<3>, g, b, 0, s, n, dT, As, Trels);
+  return hipGetLastError();
+}
+
+hipError_t launch_affine_expm(int ndim, int64_t n_theta, int nC, int d, const float* theta,
+                              const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
+                              float dT, float* As, float* Trels, hipStream_t s) {
+  const int64_t n = n_theta * nC;
+  if (n <= 0) return hipSuccess;
+  const dim3 g(grid_for(n, 256)), b(256);
+  if (ndim == 1)
+    hipLaunchKernelGGL(affine_expm_kernel<1>, g, b, 0, s, n_theta, nC, d, theta, row_ptr, col_idx,
+                       vals, dT, As, Trels);
+  else if (ndim == 2)
+    hipLaunchKernelGGL(affine_expm_kernel<2>, g, b, 0, s, n_theta, nC, d, theta, row_ptr, col_idx,
+                       vals, dT, As, Trels);
+  else
+    hipLaunchKernelGGL(affine_expm_kernel<3>, g, b, 0, s, n_theta, nC, d, theta, row_ptr, col_idx,
+                       vals, dT, As, Trels);
   return hipGetLastError();
 }
 

@@ -395,6 +395,20 @@ int cpab_expm(int ndim, int64_t n_matrices, float dT, const float* As, float* Tr
                    "cpab_expm");
 }
 
+int cpab_affine_expm(int ndim, int64_t n_theta, int nC, int d, const float* theta,
+                     const int32_t* row_ptr, const int32_t* col_idx, const float* vals, float dT,
+                     float* As, float* Trels, void* stream) {
+  if (ndim < 1 || ndim > 3) return fail(CPAB_ERR_INVALID, "ndim must be 1, 2 or 3, got %d", ndim);
+  if (n_theta < 0 || nC < 0 || d < 0) return fail(CPAB_ERR_INVALID, "negative size");
+  if (n_theta == 0 || nC == 0) return CPAB_OK;
+  CPAB_REQUIRE(row_ptr); CPAB_REQUIRE(As); CPAB_REQUIRE(Trels);
+  if (d > 0) { CPAB_REQUIRE(theta); CPAB_REQUIRE(col_idx); CPAB_REQUIRE(vals); }
+  CPAB_ALIGNED(As, 16); CPAB_ALIGNED(Trels, 16);
+  return check_hip(cpab::launch_affine_expm(ndim, n_theta, nC, d, theta, row_ptr, col_idx, vals,
+                                            dT, As, Trels, as_stream(stream)),
+                   "cpab_affine_expm");
+}
+
 int cpab_forward_1d_closed_form(int64_t nP, int64_t n_theta, int batched, int ncx,
                                 const float* points, const float* As, float* out, void* stream) {
   return forward_impl("cpab_forward_1d_closed_form", 1, nP, n_theta, batched, 1, 1, ncx, 1, 1, 0,

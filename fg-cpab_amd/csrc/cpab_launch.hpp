@@ -34,6 +34,10 @@ hipError_t launch_affine(int64_t n_theta, int rows, int d, const float* theta,
                          const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
                          float* As, hipStream_t s);
 hipError_t launch_expm(int ndim, int64_t n, float dT, const float* As, float* Trels, hipStream_t s);
+// launch_affine then launch_expm as one kernel (one thread per theta and cell).
+hipError_t launch_affine_expm(int ndim, int64_t n_theta, int nC, int d, const float* theta,
+                              const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
+                              float dT, float* As, float* Trels, hipStream_t s);
 hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
                           const int32_t* col_ptr, const int32_t* row_idx, const float* vals,
                           float* grad_theta, hipStream_t s);

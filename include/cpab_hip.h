@@ -55,6 +55,14 @@ int cpab_affine(int ndim, int64_t n_theta, int nC, int d, const float* theta,
 int cpab_expm(int ndim, int64_t n_matrices, float dT, const float* As, float* Trels,
               void* stream);
 
+/* cpab_affine followed by cpab_expm(ndim, n_theta * nC, dT, As, Trels) in one
+ * launch; both outputs equal the two-call sequence bit for bit.  Replaces the
+ * reference forward's first two steps, sparse.mm(B, theta^T)
+ * (cpab/pytorch/transformer.py:84) and cpab_gpu.expm (transformer_cuda.cpp:159-170). */
+int cpab_affine_expm(int ndim, int64_t n_theta, int nC, int d, const float* theta,
+                     const int32_t* row_ptr, const int32_t* col_idx, const float* vals, float dT,
+                     float* As, float* Trels, void* stream);
+
 /* Forward integration: out[b] = phi(points[b or shared]; theta_b), [n_theta, ndim, nP].
  * ndim 2/3: nstepsolver steps of Trels (+ Heun on crossings if adaptive);
  * ndim 1: the closed form (Trels unused), as the reference does.

@@ -40,6 +40,13 @@ def test_affine_and_expm_bitexact(cuda, tess):
     Tr = torch.empty_like(As)
     native().expm(nd, As, 1.0 / 50, Tr)
     np.testing.assert_array_equal(Tr.cpu().numpy(), orc.expm(nd, ref, 1.0 / 50))
+    # The fused launch the forward uses: the same two tables, bit for bit.
+    tab = basis_tables(T.params, cuda)
+    As2, Tr2 = torch.empty_like(As), torch.empty_like(As)
+    native().affine_expm(nd, _dev(theta, cuda), T.params.nC, tab["row_ptr"], tab["col_idx"],
+                         tab["vals"], 1.0 / 50, As2, Tr2)
+    np.testing.assert_array_equal(As2.cpu().numpy(), ref)
+    np.testing.assert_array_equal(Tr2.cpu().numpy(), Tr.cpu().numpy())
 
 
 def test_expm_squaring_branch_bitexact(cuda):
