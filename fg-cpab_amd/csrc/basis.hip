@@ -342,36 +342,46 @@ __global__ void expm_kernel(int64_t n, float dT, const float* __restrict__ As,
   for (int k = 0; k < P; ++k) out[i * P + k] = r[k];
 }
 
-// A = B theta and Trels = expm(dT A) in one pass: one thread per (theta, cell)
-// forms the cell's P rows of A exactly as affine_kernel does (each row summed
-// in ascending column order), stores them, and exponentiates them in registers
-// as expm_kernel does, so both outputs equal the two-kernel sequence bit for
-// bit.
+// A = B theta and Trels = expm(dT A) in one launch.  A workgroup covers
+// kAffCells<D> consecutive (theta, cell) matrices: first one thread per row of
+// A forms it exactly as affine_kernel does (summed in ascending column order)
+// and stores it (coalesced) and into LDS; then one thread per cell
+// exponentiates its block as expm_kernel does and the results leave through
+// LDS, coalesced.  Both outputs equal the two-kernel sequence bit for bit.
+template <int D> constexpr int kAffCells = D == 1 ? 128 : (D == 2 ? 64 : 32);
+
 template <int D>
-__global__ void affine_expm_kernel(int64_t n_theta, int nC, int d, const float* __restrict__ theta,
-                                   const int32_t* __restrict__ row_ptr,
-                                   const int32_t* __restrict__ col_idx,
-                                   const float* __restrict__ vals, float dT,
-                                   float* __restrict__ As, float* __restrict__ Trels) {
+__global__ __launch_bounds__(kAffCells<D> * D * (D + 1)) void affine_expm_kernel(
+    int64_t n_theta, int nC, int d, const float* __restrict__ theta,
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_idx,
+    const float* __restrict__ vals, float dT, float* __restrict__ As, float* __restrict__ Trels) {
   constexpr int P = D * (D + 1);
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= n_theta * nC) return;
-  const int64_t b = i / nC;
-  const int c = (int)(i - b * nC);
-  const float* th = theta + b * d;
-  float a[P], r[P];
-#pragma unroll
-  for (int j = 0; j < P; ++j) {
-    const int row = c * P + j;
+  constexpr int CB = kAffCells<D>;
+  __shared__ float tile[CB * P];
+  const int64_t n = n_theta * nC * P;                  // rows of A in all
+  const int64_t base = (int64_t)blockIdx.x * CB * P;   // first row of this block
+  const int t = threadIdx.x;
+  const int64_t g = base + t;
+  if (g < n) {
+    const int64_t b = g / ((int64_t)nC * P);
+    const int row = (int)(g - b * nC * P);
+    const float* th = theta + b * d;
     float acc = 0.0f;
     for (int k = row_ptr[row]; k < row_ptr[row + 1]; ++k) acc = fmaf(vals[k], th[col_idx[k]], acc);
-    a[j] = acc;
+    As[g] = acc;
+    tile[t] = acc;
   }
+  __syncthreads();
+  if (t < CB && base + (int64_t)t * P < n) {
+    float a[P], r[P];
 #pragma unroll
-  for (int k = 0; k < P; ++k) As[i * P + k] = a[k];
-  expm_cell<D>(a, dT, r);
+    for (int k = 0; k < P; ++k) a[k] = tile[t * P + k];
+    expm_cell<D>(a, dT, r);
 #pragma unroll
-  for (int k = 0; k < P; ++k) Trels[i * P + k] = r[k];
+    for (int k = 0; k < P; ++k) tile[t * P + k] = r[k];  // only this thread uses these slots
+  }
+  __syncthreads();
+  if (g < n) Trels[g] = tile[t];
 }
 
 inline unsigned grid_for(int64_t n, int block) {
@@ -414,16 +424,14 @@ hipError_t launch_affine_expm(int ndim, int64_t n_theta, int nC, int d, const fl
                               float dT, float* As, float* Trels, hipStream_t s) {
   const int64_t n = n_theta * nC;
   if (n <= 0) return hipSuccess;
-  const dim3 g(grid_for(n, 256)), b(256);
-  if (ndim == 1)
-    hipLaunchKernelGGL(affine_expm_kernel<1>, g, b, 0, s, n_theta, nC, d, theta, row_ptr, col_idx,
-                       vals, dT, As, Trels);
-  else if (ndim == 2)
-    hipLaunchKernelGGL(affine_expm_kernel<2>, g, b, 0, s, n_theta, nC, d, theta, row_ptr, col_idx,
-                       vals, dT, As, Trels);
-  else
-    hipLaunchKernelGGL(affine_expm_kernel<3>, g, b, 0, s, n_theta, nC, d, theta, row_ptr, col_idx,
-                       vals, dT, As, Trels);
+  auto go = [&](auto kernel, int cells, int P) {
+    const dim3 g((unsigned)((n + cells - 1) / cells)), b((unsigned)(cells * P));
+    hipLaunchKernelGGL(kernel, g, b, 0, s, n_theta, nC, d, theta, row_ptr, col_idx, vals, dT, As,
+                       Trels);
+  };
+  if (ndim == 1) go(affine_expm_kernel<1>, kAffCells<1>, 2);
+  else if (ndim == 2) go(affine_expm_kernel<2>, kAffCells<2>, 6);
+  else go(affine_expm_kernel<3>, kAffCells<3>, 12);
   return hipGetLastError();
 }
 

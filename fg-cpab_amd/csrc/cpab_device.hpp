@@ -115,9 +115,20 @@ __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
                            __builtin_amdgcn_ballot_w64(!(px < 1.0f)) |
                            __builtin_amdgcn_ballot_w64(!(py > 0.0f)) |
                            __builtin_amdgcn_ballot_w64(!(py < 1.0f));
-  // The boundary rules fall through to the inside rule, so lanes that are
-  // inside get the same cell back from them.
-  if (outside) c = cell_2d_outside(px, py, fx, fy, base, lx, ly);
+  if (outside) {
+    // Away from the domain's corners the boundary rules return a fixed
+    // triangle per side (left 3, right 1, bottom 0, top 2) and fall through to
+    // the inside rule otherwise (inside lanes, NaN).  Points on a domain edge
+    // (every meshgrid row has two) mostly get that same triangle from the
+    // inside rule already, so the full rules run only when some lane is at a
+    // corner or the inside rule disagrees with its side's triangle.
+    const int t = c - base;
+    const bool xl = px <= 0.0f, xh = px >= 1.0f, yl = py <= 0.0f, yh = py >= 1.0f;
+    const int side = xl ? 3 : (xh ? 1 : (yl ? 0 : (yh ? 2 : t)));
+    const bool corner = (xl | xh) & (yl | yh);
+    if (__builtin_amdgcn_ballot_w64(corner | (side != t)))
+      c = cell_2d_outside(px, py, fx, fy, base, lx, ly);
+  }
   return c;
 }
 
