@@ -26,9 +26,6 @@ struct LaunchCfg {
   int lds_chain;    // forward: LDS bytes available for the per-stage table of a 2D chain (0 = off)
 };
 
-int device_cu_count();
-int device_max_lds();
-
 hipError_t launch_fill(float* dst, int64_t n, float value, hipStream_t s);
 hipError_t launch_affine(int64_t n_theta, int rows, int d, const float* theta,
                          const int32_t* row_ptr, const int32_t* col_idx, const float* vals,
