@@ -253,6 +253,51 @@ def test_backward_3d_moment_paths(cuda, monkeypatch, mode, kind, n):
     assert_grad_close(mom, ref_m, rtol=2e-5)
 
 
+@pytest.mark.parametrize("chain", [False, True])
+def test_backward_mixed_dense_sparse(cuda, chain):
+    # One launch where some workgroups touch most cells (uniform points: they
+    # store partial tables) and others touch few (a small cluster: they add
+    # their sums to HBM with atomics), into the same moments rows.
+    T = cpab_for([20, 20])
+    p = T.params
+    rng = np.random.default_rng(77)
+    spread = rng.random((2, 60000)).astype(np.float32)
+    cluster = (0.4 + 0.05 * rng.random((2, 60000))).astype(np.float32)
+    pts = np.concatenate([spread, cluster], axis=1)
+    nP = pts.shape[1]
+    if not chain:
+        theta = seeded_theta(T, 2, 0.5, 78)
+        g = rng.standard_normal((2, 2, nP)).astype(np.float32)
+        As, mom, gp = _backward_case(T, theta, pts, g, cuda)
+        ref_m, ref_gp = orc.backward(pts, As, g, [20, 20], 50)
+        assert_adjoint_close(gp, ref_gp)
+        assert_grad_close(mom, ref_m, rtol=2e-5)
+        return
+    K = 2
+    theta = seeded_theta(T, K, 0.3, 79)
+    As = _As_gpu(T, theta, cuda)
+    Tr = torch.empty_like(As)
+    native().expm(2, As, 1.0 / 50, Tr)
+    out = torch.empty((1, 2, nP), device=cuda)
+    sp = torch.empty((K - 1, 1, 2, nP), device=cuda)
+    native().chain_forward(2, _dev(pts, cuda), False, 1, K, nP, 50, p.nc, 0, Tr, As, out, sp)
+    g = rng.standard_normal((1, 2, nP)).astype(np.float32)
+    mom = torch.empty((K, p.nC, 6), device=cuda)
+    gp = torch.empty((1, 2, nP), device=cuda)
+    ws = torch.empty(native().chain_backward_workspace_size(2, nP, 1, K, p.nC), dtype=torch.uint8,
+                     device=cuda)
+    native().chain_backward(2, _dev(pts, cuda), False, 1, K, nP, 50, p.nc, 0, sp, As, _dev(g, cuda),
+                            mom, gp, ws)
+    A = As.cpu().numpy().reshape(K, 1, p.nC, 2, 3)
+    x1 = sp[0].cpu().numpy()
+    m1, lam = orc.backward(x1, A[1], g, [20, 20], 50)
+    m0, lam = orc.backward(pts, A[0], lam, [20, 20], 50)
+    M = mom.cpu().numpy()
+    assert_grad_close(M[1], m1[0], rtol=2e-5)
+    assert_grad_close(M[0], m0[0], rtol=2e-5)
+    assert_adjoint_close(gp.cpu().numpy(), lam)
+
+
 def test_backward_no_points_grad(cuda):
     T = cpab_for([20, 20])
     theta = seeded_theta(T, 2, 0.5, 3)
