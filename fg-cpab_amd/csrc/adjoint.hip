@@ -86,6 +86,10 @@ template <int D> __device__ __forceinline__ Adj<D> fetch_adj(const float* tab, i
 template <> __device__ __forceinline__ Adj<1> fetch_adj<1>(const float* tab, int c) { return load_adj1(tab, c); }
 template <> __device__ __forceinline__ Adj<2> fetch_adj<2>(const float* tab, int c) { return load_adj2(tab, c); }
 template <> __device__ __forceinline__ Adj<3> fetch_adj<3>(const float* tab, int c) { return load_adj3(tab, c); }
+template <int D> __device__ __forceinline__ Inv<D> fetch_inv(const float* tab, int c);
+template <> __device__ __forceinline__ Inv<1> fetch_inv<1>(const float* tab, int c) { return load_inv1(tab, c); }
+template <> __device__ __forceinline__ Inv<2> fetch_inv<2>(const float* tab, int c) { return load_inv2(tab, c); }
+template <> __device__ __forceinline__ Inv<3> fetch_inv<3>(const float* tab, int c) { return load_inv3(tab, c); }
 
 __device__ __forceinline__ void velocity(const Aff<1>& A, const float (&p)[1], float (&v)[1]) {
   v[0] = fmaf(A.a, p[0], A.b);
@@ -409,7 +413,12 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
 }
 
 // Register variant: T == TS known at compile time, moments in full LDS bins
-// or (3D) in the LDS cell cache.
+// or (3D) in the LDS cell cache.  Without adaptive substeps every replay step
+// is p' = E_c [p; 1] with the cell's fixed midpoint map, so phase 1 keeps only
+// the cells and phase 2 recovers each position from the next through the
+// cell's inverse map (a few ulp per step; the positions only feed the sums
+// S, the cells stay exact).  With adaptive substeps (Heun on crossings) the
+// positions are kept in registers instead.
 template <int D, bool ADAPTIVE, int BINS, int TS, typename P, typename IO>
 __device__ __forceinline__ void register_body(P tab, const float* __restrict__ gtab, int nP,
                                               const Cells& g, const IO& io, float* bins,
@@ -443,8 +452,10 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
       cur = c;
       if (t & 1) cells[t >> 1] |= (uint32_t)c << 16;
       else cells[t >> 1] = (uint32_t)c;
+      if (ADAPTIVE) {
 #pragma unroll
-      for (int k = 0; k < D; ++k) traj[t][k] = p[k];
+        for (int k = 0; k < D; ++k) traj[t][k] = p[k];
+      }
       replay_step_with<D, ADAPTIVE>(tab, A, c, p, h, hh, g);
     }
 
@@ -454,6 +465,7 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
     for (int k = 0; k < PP; ++k) m[k] = 0.0f;
     int prev = -1;
     Adj<D> G;
+    Inv<D> E;
 #pragma unroll
     for (int t = TS - 1; t >= 0; --t) {
       const int c = (int)((t & 1) ? (cells[t >> 1] >> 16) : (cells[t >> 1] & 0xffffu));
@@ -467,9 +479,15 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
 #pragma unroll
         for (int k = 0; k < PP; ++k) m[k] = 0.0f;
         G = fetch_adj<D>(gtab, c);
+        if (!ADAPTIVE) E = fetch_inv<D>(gtab, c);
       }
       prev = c;
-      adjoint(G, traj[t], m, lam);
+      if constexpr (ADAPTIVE) {
+        adjoint(G, traj[t], m, lam);
+      } else {
+        step_back<D>(E, p);  // p = position at step t
+        adjoint(G, p, m, lam);
+      }
     }
     if (valid) {
       if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, prev, m);
@@ -575,16 +593,17 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
 // adjoint of its input to lam (k > 0) or grad_points (k = 0).  The per-cell
 // sums of stage k go to row (k * n_batch + b): added to that moments row (zero
 // on entry), or, from a dense full-bin workgroup, to its partial table with
-// its dense-part bit set; the adjoint increment table G holds the same rows
-// (AdjStride<D>::S floats per cell).
-// Launch bound: 768 threads (3 waves per SIMD, up to 168 VGPRs), or 512 (2 waves
-// per SIMD, 256 VGPRs) for the 3D register variant whose trajectory alone takes
-// 150 VGPRs.
-template <int D, int TS>
-constexpr int kBwdThreads = (D == 3 && TS > 0) ? 512 : 768;
+// its dense-part bit set; the reverse-sweep table G holds the same rows
+// (RevStride<D>::S floats per cell).
+// Launch bound: 1024 threads (4 waves per SIMD, up to 128 VGPRs) for the 1D/2D
+// register variant without adaptive substeps (cells only in registers, ~90
+// VGPRs); 768 (3 waves per SIMD, up to 168 VGPRs) for 3D, the segmented variant
+// and the 1D/2D adaptive register variant, whose trajectory takes 2 x 50 VGPRs.
+template <int D, bool ADAPTIVE, int TS>
+constexpr int kBwdThreads = (TS > 0 && !ADAPTIVE && D <= 2) ? 1024 : 768;
 
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
-__global__ __launch_bounds__((kBwdThreads<D, TS>)) void backward_kernel(
+__global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kernel(
     int nP, int batched, int T, Cells g, int nC, int K, const float* __restrict__ points,
     const float* __restrict__ stage_points, const float* __restrict__ As,
     const float* __restrict__ Gs, const float* __restrict__ grad_out, float* __restrict__ moments,
@@ -600,7 +619,7 @@ __global__ __launch_bounds__((kBwdThreads<D, TS>)) void backward_kernel(
   for (int k = K - 1; k >= 0; --k) {
     const size_t row = (size_t)k * n_batch + b;
     const float* __restrict__ Ag = As + row * R;
-    const float* __restrict__ Gg = Gs + row * nC * AdjStride<D>::S;
+    const float* __restrict__ Gg = Gs + row * nC * RevStride<D>::S;
     PlainIO<D> io;
     io.nP = nP;
     io.pts = k == 0 ? points + (batched ? (size_t)b * plane : 0)
@@ -622,7 +641,7 @@ __global__ __launch_bounds__((kBwdThreads<D, TS>)) void backward_kernel(
 // Fused transform_data backward: one workgroup = one theta x one contiguous
 // range of output positions.
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
-__global__ __launch_bounds__((kBwdThreads<D, TS>)) void image_backward_kernel(
+__global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward_kernel(
     ImageShape s, int T, Cells g, int nC, const float* __restrict__ grid,
     const float* __restrict__ final_points, const float* __restrict__ As,
     const float* __restrict__ Gs, const float* __restrict__ data, const float* __restrict__ grad_out,
@@ -634,7 +653,7 @@ __global__ __launch_bounds__((kBwdThreads<D, TS>)) void image_backward_kernel(
   const int R = nC * Dim<D>::P;
   const StageLds<D, LDS_A, BINS> L(lds, R);
   const float* __restrict__ Ag = As + (size_t)b * R;
-  const float* __restrict__ Gg = Gs + (size_t)b * nC * AdjStride<D>::S;
+  const float* __restrict__ Gg = Gs + (size_t)b * nC * RevStride<D>::S;
   ImageIO<D> io;
   io.s = s;
   io.grid = grid;

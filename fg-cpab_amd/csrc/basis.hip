@@ -76,24 +76,35 @@ __global__ void project_kernel(int64_t n_theta, int D, int d, const float* __res
   grad[i] = acc;
 }
 
-// One thread per cell row of the table: G[i] = h A_lin + (h^2/2) A_lin^2 of
-// cell i (cpab_device.hpp, adjoint_increment), the cell's sums zeroed; the
-// first n_words threads also clear the dense-part masks.
+// One thread per cell row of the table: the reverse-sweep entry of cell i
+// (cpab_device.hpp, RevStride): G = h A_lin + (h^2/2) A_lin^2
+// (adjoint_increment) and the inverse one-step map (inverse_step_map); the
+// cell's sums zeroed; the first n_words threads also clear the dense-part
+// masks.
 template <int D>
 __global__ void adjoint_table_kernel(int64_t n_cells, float h, const float* __restrict__ As,
                                      float* __restrict__ G, float* __restrict__ moments,
                                      uint64_t* __restrict__ dense_parts, int64_t n_words) {
   constexpr int P = D * (D + 1);
-  constexpr int S = AdjStride<D>::S;
+  constexpr int S = RevStride<D>::S;
+  constexpr int GS = D == 1 ? 1 : (D == 2 ? 4 : 12);   // floats of the G part
+  constexpr int IW = D == 1 ? 2 : 4;                   // row stride of the inverse map
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i < n_words) dense_parts[i] = 0;
   if (i >= n_cells) return;
-  float a[P], g[S];
+  float a[P], e[S], inv[P];
+#pragma unroll
+  for (int k = 0; k < S; ++k) e[k] = 0.0f;
 #pragma unroll
   for (int k = 0; k < P; ++k) a[k] = As[i * P + k];
-  adjoint_increment<D>(a, h, (h * 0.5f) * h, g);
+  adjoint_increment<D>(a, h, (h * 0.5f) * h, e);
+  inverse_step_map<D>(a, h, inv);
 #pragma unroll
-  for (int k = 0; k < S; ++k) G[i * S + k] = g[k];
+  for (int r = 0; r < D; ++r)
+#pragma unroll
+    for (int j = 0; j <= D; ++j) e[GS + r * IW + j] = inv[r * (D + 1) + j];
+#pragma unroll
+  for (int k = 0; k < S; ++k) G[i * S + k] = e[k];
 #pragma unroll
   for (int k = 0; k < P; ++k) moments[i * P + k] = 0.0f;
 }

@@ -151,17 +151,18 @@ cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_thet
   // Table too large for LDS: hashed cell cache in LDS, flushed to HBM at the end.
   const int64_t cache = (int64_t)cpab::kCacheSlots * (g.ppc() + 1) * 4;
   c.lds_cache = (!c.lds_bins && cache <= dev.lds) ? env_int("CPAB_BWD_CACHE", 1) : 0;
-  // Register variant: whole trajectory in VGPRs, one workgroup per CU; the
-  // per-cell table is read through L1/L2 (re-read only when a lane changes
-  // cell).  1D/2D: ~168 VGPRs per lane -> 3 waves per SIMD, 768 threads.  3D
-  // (not adaptive): ~254 VGPRs -> 2 waves per SIMD, 512 threads.
+  // Register variant: the trajectory's cells (and, with adaptive substeps, its
+  // positions) in VGPRs, one workgroup per CU; the per-cell tables are read
+  // through L1/L2 (re-read only when a lane changes cell).  Without adaptive
+  // substeps in 1D/2D: 1024 threads (4 waves per SIMD); 3D and 1D/2D adaptive:
+  // 768 threads (3 waves per SIMD).
   const bool reg = T == cpab::kRegSteps && g.nC <= 65535 && env_int("CPAB_BWD_REG", 1) &&
                    (g.ndim <= 2 ? c.lds_bins != 0 : (!adaptive && (c.lds_bins || c.lds_cache)));
   c.reg_steps = reg ? cpab::kRegSteps : 0;
   const int64_t used = c.lds_bins ? table : (c.lds_cache ? cache : 0);
   c.lds_table = (used + table <= dev.lds) ? env_int("CPAB_BWD_LDS_TABLE", reg ? 0 : 1) : 0;
   const int64_t lds = used + (c.lds_table ? table : 0);
-  const int limit = (reg && g.ndim == 3) ? 512 : 768;  // kernel launch bound
+  const int limit = (reg && !adaptive && g.ndim <= 2) ? 1024 : 768;  // kernel launch bound
   int wg_per_cu;
   if (reg) {
     c.block = env_int("CPAB_BWD_BLOCK", limit);
@@ -253,12 +254,13 @@ int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 // Workspace of a K-stage backward (rows = K * n_batch): with full LDS bins the
 // dense-part masks [rows, ceil(chunks/64)] and the partial tables
 // [rows, chunks, nC, ppc]; then the inter-stage adjoint [n_batch, ndim, nP]
-// (K > 1) and the adjoint increment table G [rows, nC, 1|4|12].
+// (K > 1) and the reverse-sweep table [rows, nC, 4|12|24] (G and the inverse
+// one-step map per cell, cpab_device.hpp RevStride).
 struct BackwardWorkspace {
   int64_t dense_words, partials_offset, lam_offset, g_offset, total;
 };
 
-int adj_stride(int ndim) { return ndim == 1 ? 1 : (ndim == 2 ? 4 : 12); }
+int adj_stride(int ndim) { return ndim == 1 ? 4 : (ndim == 2 ? 12 : 24); }
 
 BackwardWorkspace backward_workspace(const cpab::Geometry& g, int64_t nP, int64_t n_batch, int K,
                                      const cpab::LaunchCfg& cfg) {

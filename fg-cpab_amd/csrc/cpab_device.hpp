@@ -371,26 +371,64 @@ __device__ __forceinline__ void adjoint3(const Aff<3>& A, float px, float py, fl
 // reference's op order by a few ulp.
 // ---------------------------------------------------------------------------
 
-// Row stride (floats) of the G table: 1x1, 2x2, 3x3 padded to 3 rows of 4.
-template <int D> struct AdjStride;
-template <> struct AdjStride<1> { static constexpr int S = 1; };
-template <> struct AdjStride<2> { static constexpr int S = 4; };
-template <> struct AdjStride<3> { static constexpr int S = 12; };
+// Per-cell table of the reverse sweep (16-byte aligned entries of
+// RevStride<D>::S floats): G first, then the inverse of the cell's one-step
+// midpoint map p' = E [p; 1], as rows [M | m] with p = M p' + m.
+//   1D  [g, M, m, 0]                                              4 floats
+//   2D  [g00 g01 g10 g11] [M00 M01 m0 0] [M10 M11 m1 0]             12 floats
+//   3D  3 rows of G (4th column 0), then 3 rows [M_r0 M_r1 M_r2 m_r] 24 floats
+template <int D> struct RevStride;
+template <> struct RevStride<1> { static constexpr int S = 4; };
+template <> struct RevStride<2> { static constexpr int S = 12; };
+template <> struct RevStride<3> { static constexpr int S = 24; };
 
 template <int D> struct Adj;
 template <> struct Adj<1> { float g; };
 template <> struct Adj<2> { float g[4]; };   // row-major g00 g01 g10 g11
-template <> struct Adj<3> { float g[9]; };   // row-major, stored with a zero 4th column
+template <> struct Adj<3> { float g[9]; };   // row-major
 
-__device__ __forceinline__ Adj<1> load_adj1(const float* tab, int c) { return {tab[c]}; }
+__device__ __forceinline__ Adj<1> load_adj1(const float* tab, int c) { return {tab[4 * (int64_t)c]}; }
 __device__ __forceinline__ Adj<2> load_adj2(const float* tab, int c) {
-  const v4f v = reinterpret_cast<const v4f*>(tab)[c];
+  const v4f v = reinterpret_cast<const v4f*>(tab)[3 * (int64_t)c];
   return {{v.x, v.y, v.z, v.w}};
 }
 __device__ __forceinline__ Adj<3> load_adj3(const float* tab, int c) {
-  const v4f* q = reinterpret_cast<const v4f*>(tab) + 3 * (int64_t)c;
+  const v4f* q = reinterpret_cast<const v4f*>(tab) + 6 * (int64_t)c;
   const v4f a = q[0], b = q[1], d = q[2];
   return {{a.x, a.y, a.z, b.x, b.y, b.z, d.x, d.y, d.z}};
+}
+
+// Inverse one-step map of a cell, row-major [D, D+1].
+template <int D> struct Inv { float m[D * (D + 1)]; };
+
+__device__ __forceinline__ Inv<1> load_inv1(const float* tab, int c) {
+  const v2f v = *reinterpret_cast<const v2f*>(tab + 4 * (int64_t)c + 1);
+  return {{v.x, v.y}};
+}
+__device__ __forceinline__ Inv<2> load_inv2(const float* tab, int c) {
+  const v4f* q = reinterpret_cast<const v4f*>(tab) + 3 * (int64_t)c;
+  const v4f a = q[1], b = q[2];
+  return {{a.x, a.y, a.z, b.x, b.y, b.z}};
+}
+__device__ __forceinline__ Inv<3> load_inv3(const float* tab, int c) {
+  const v4f* q = reinterpret_cast<const v4f*>(tab) + 6 * (int64_t)c;
+  const v4f a = q[3], b = q[4], d = q[5];
+  return {{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w}};
+}
+
+// p <- M p + m: the position one replay step earlier.
+template <int D>
+__device__ __forceinline__ void step_back(const Inv<D>& E, float (&p)[D]) {
+  float q[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    float acc = E.m[i * (D + 1) + D];
+#pragma unroll
+    for (int j = D - 1; j >= 0; --j) acc = fmaf(E.m[i * (D + 1) + j], p[j], acc);
+    q[i] = acc;
+  }
+#pragma unroll
+  for (int i = 0; i < D; ++i) p[i] = q[i];
 }
 
 // One reverse step: S += lam (x) [p; 1], then lam += G^T lam.
@@ -429,7 +467,7 @@ __device__ __forceinline__ void adjoint_s3(const Adj<3>& G, float px, float py, 
 }
 
 // G = h A_lin + (h^2/2) A_lin^2 of one cell; `a` is the row-major [D, D+1]
-// block of A, `hhh` = (h/2)*h.  Writes AdjStride<D>::S floats.
+// block of A, `hhh` = (h/2)*h.  Writes the G part of a RevStride<D> entry.
 template <int D>
 __device__ __forceinline__ void adjoint_increment(const float* a, float h, float hhh, float* g) {
   constexpr int W = D + 1;
@@ -444,6 +482,66 @@ __device__ __forceinline__ void adjoint_increment(const float* a, float h, float
       g[i * RS + j] = fmaf(h, a[i * W + j], hhh * sq);
     }
     if (RS > D) g[i * RS + D] = 0.0f;
+  }
+}
+
+// Inverse of a cell's one-step midpoint map.  With the replay's fp32 step h
+// (and h/2, exact), one explicit-midpoint step is, in exact arithmetic,
+//   p' = E_lin p + e,  E_lin = I + h A + h (h/2) A^2,  e = h b + h (h/2) A b.
+// Its inverse M = E_lin^-1, m = -M e is formed in double and rounded once.
+// Writes [M | m] row-major, D rows of D+1.
+template <int D>
+__device__ __forceinline__ void inverse_step_map(const float* a, float h, float* out) {
+  constexpr int W = D + 1;
+  const double hd = h, h2 = (double)h * (double)(h * 0.5f);
+  double E[3][3] = {}, e[3] = {};
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    double ab = 0.0;
+#pragma unroll
+    for (int r = 0; r < D; ++r) ab += (double)a[i * W + r] * a[r * W + D];
+    e[i] = hd * a[i * W + D] + h2 * ab;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      double sq = 0.0;
+#pragma unroll
+      for (int r = 0; r < D; ++r) sq += (double)a[i * W + r] * a[r * W + j];
+      E[i][j] = (i == j ? 1.0 : 0.0) + hd * a[i * W + j] + h2 * sq;
+    }
+  }
+  double M[3][3] = {};
+  if (D == 1) {
+    M[0][0] = 1.0 / E[0][0];
+  } else if (D == 2) {
+    const double id = 1.0 / (E[0][0] * E[1][1] - E[0][1] * E[1][0]);
+    M[0][0] = E[1][1] * id;
+    M[0][1] = -E[0][1] * id;
+    M[1][0] = -E[1][0] * id;
+    M[1][1] = E[0][0] * id;
+  } else {
+    const double c00 = E[1][1] * E[2][2] - E[1][2] * E[2][1];
+    const double c01 = E[0][2] * E[2][1] - E[0][1] * E[2][2];
+    const double c02 = E[0][1] * E[1][2] - E[0][2] * E[1][1];
+    const double id = 1.0 / (E[0][0] * c00 + E[1][0] * c01 + E[2][0] * c02);
+    M[0][0] = c00 * id;
+    M[0][1] = c01 * id;
+    M[0][2] = c02 * id;
+    M[1][0] = (E[1][2] * E[2][0] - E[1][0] * E[2][2]) * id;
+    M[1][1] = (E[0][0] * E[2][2] - E[0][2] * E[2][0]) * id;
+    M[1][2] = (E[0][2] * E[1][0] - E[0][0] * E[1][2]) * id;
+    M[2][0] = (E[1][0] * E[2][1] - E[1][1] * E[2][0]) * id;
+    M[2][1] = (E[0][1] * E[2][0] - E[0][0] * E[2][1]) * id;
+    M[2][2] = (E[0][0] * E[1][1] - E[0][1] * E[1][0]) * id;
+  }
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    double m = 0.0;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      out[i * W + j] = (float)M[i][j];
+      m -= M[i][j] * e[j];
+    }
+    out[i * W + D] = (float)m;
   }
 }
 

@@ -38,7 +38,8 @@ hipError_t launch_affine_expm(int ndim, int64_t n_theta, int nC, int d, const fl
 hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
                           const int32_t* col_ptr, const int32_t* row_idx, const float* vals,
                           float* grad_theta, hipStream_t s);
-// G [n_cells, AdjStride] = h A + (h^2/2) A^2 per cell, h = 1/T; zeroes
+// G [n_cells, RevStride]: per cell h A + (h^2/2) A^2 and the inverse one-step
+// map (cpab_device.hpp), h = 1/T; zeroes
 // moments [n_cells, ppc] (the HBM sums) and dense_parts [n_words].
 hipError_t launch_adjoint_table(int ndim, int64_t n_cells, int T, const float* As, float* G,
                                 float* moments, uint64_t* dense_parts, int64_t n_words,
@@ -64,7 +65,7 @@ hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, in
                               int adaptive, const float* points, const float* Trels,
                               const float* As, int32_t* cells, hipStream_t s);
 // lam: [n_batch, ndim, nP] scratch carrying the adjoint between stages (K > 1).
-// G: the adjoint increment table of launch_adjoint_table, same rows as As.
+// G: the reverse-sweep table of launch_adjoint_table, same rows as As.
 // The per-cell sums S go to moments (HBM sums, zero on entry) or, for a
 // full-bin workgroup that touched a quarter of the cells or more, to its
 // partial table [rows, chunks, nC, ppc] with its bit set in dense_parts

@@ -86,7 +86,8 @@ int cpab_trace_cells(int ndim, int64_t nP, int64_t n_theta, int batched, int nst
                      const float* Trels, const float* As, int32_t* cells, void* stream);
 
 /* Bytes of device workspace cpab_backward needs for this problem: per-cell
- * adjoint increments h*A + (h^2/2)*A^2 (1, 4 or 12 floats per cell and theta)
+ * reverse-sweep tables (per cell and theta: the adjoint increment h*A + (h^2/2)*A^2 and the
+ * inverse of the one-step map; 4, 12 or 24 floats)
  * and, where the sums are privatised per workgroup, the partial tables with
  * their touched-cell masks. */
 int64_t cpab_backward_workspace_size(int ndim, int64_t nP, int64_t n_theta, int nC);

@@ -210,6 +210,28 @@ def test_backward_parity(cuda, tess, kind, n, adaptive):
     assert_grad_close(mom, ref_m, rtol=2e-5)
 
 
+@pytest.mark.parametrize("tess,kind,scale", [([20, 20], "uniform", 2.0), ([30, 30], "mesh", 2.0),
+                                             ([4, 4, 4], "mesh", 1.5), ([50], "line", 3.0)])
+def test_backward_parity_strong_field(cuda, tess, kind, scale):
+    # Large theta: strong, fast-changing fields, where the backward's positions
+    # (recovered step by step through each cell's inverse one-step map) and the
+    # factored adjoint see the largest h*|A|.
+    T = cpab_for(tess)
+    nd = len(tess)
+    theta = seeded_theta(T, 2, scale, 110 + nd)
+    if kind == "line":
+        pts = np.linspace(0, 1, 5000, dtype=np.float32)[None]
+    elif kind == "uniform":
+        pts = uniform_points(nd, 20000, 111)
+    else:
+        pts = meshgrid([64, 48] if nd == 2 else [17, 13, 11])
+    g = np.random.default_rng(112).standard_normal((2, nd, pts.shape[-1])).astype(np.float32)
+    As, mom, gp = _backward_case(T, theta, pts, g, cuda)
+    ref_m, ref_gp = orc.backward(pts, As, g, tess, 50)
+    assert_adjoint_close(gp, ref_gp)
+    assert_grad_close(mom, ref_m, rtol=2e-5)
+
+
 @pytest.mark.parametrize("tess,kind,nstep", [([50], "line", 20), ([20, 20], "uniform", 37),
                                              ([30, 30], "mesh", 100), ([4, 4, 4], "uniform", 20),
                                              ([10, 10, 10], "mesh", 37)])
