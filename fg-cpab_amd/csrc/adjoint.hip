@@ -459,39 +459,49 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
       replay_step_with<D, ADAPTIVE>(tab, A, c, p, h, hh, g);
     }
 
-    // Phase 2: reverse sweep.
+    // Phase 2: reverse sweep.  A cell change is handled at the end of the
+    // step before it (flush the finished cell, load the next cell's entry),
+    // so each load writes the registers the next step reads.
+    auto cell_at = [&](int t) {
+      return (int)((t & 1) ? (cells[t >> 1] >> 16) : (cells[t >> 1] & 0xffffu));
+    };
     float m[PP];
 #pragma unroll
     for (int k = 0; k < PP; ++k) m[k] = 0.0f;
-    int prev = -1;
-    Adj<D> G;
+    int c = cell_at(TS - 1);
+    Adj<D> G = fetch_adj<D>(gtab, c);
     Inv<D> E;
+    if (!ADAPTIVE) E = fetch_inv<D>(gtab, c);
 #pragma unroll
     for (int t = TS - 1; t >= 0; --t) {
-      const int c = (int)((t & 1) ? (cells[t >> 1] >> 16) : (cells[t >> 1] & 0xffffu));
-      // Divergent branch: skipped by the hardware (exec = 0) at steps where no
-      // lane of the wave changes cell.
-      if (c != prev) {
-        if (prev >= 0 && valid) {
-          if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, prev, m);
-          else flush_lds<PP>(bins, prev, m);
-        }
-#pragma unroll
-        for (int k = 0; k < PP; ++k) m[k] = 0.0f;
-        G = fetch_adj<D>(gtab, c);
-        if (!ADAPTIVE) E = fetch_inv<D>(gtab, c);
-      }
-      prev = c;
       if constexpr (ADAPTIVE) {
         adjoint(G, traj[t], m, lam);
       } else {
         step_back<D>(E, p);  // p = position at step t
         adjoint(G, p, m, lam);
       }
+      // The lambda update reads G: finish it before the branch that reloads G.
+      pin(lam);
+      if (t > 0) {
+        const int cn = cell_at(t - 1);
+        // Divergent branch: skipped by the hardware (exec = 0) at steps where
+        // no lane of the wave changes cell.
+        if (cn != c) {
+          if (valid) {
+            if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, c, m);
+            else flush_lds<PP>(bins, c, m);
+          }
+#pragma unroll
+          for (int k = 0; k < PP; ++k) m[k] = 0.0f;
+          G = fetch_adj<D>(gtab, cn);
+          if (!ADAPTIVE) E = fetch_inv<D>(gtab, cn);
+        }
+        c = cn;
+      }
     }
     if (valid) {
-      if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, prev, m);
-      else flush_lds<PP>(bins, prev, m);
+      if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, c, m);
+      else flush_lds<PP>(bins, c, m);
     }
     io.finish(pi, valid, lam);
   }

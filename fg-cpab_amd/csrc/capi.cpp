@@ -83,7 +83,11 @@ int check_geometry(int ndim, int ncx, int ncy, int ncz, cpab::Geometry* g) {
   const int64_t nC = ndim == 1 ? (int64_t)ncx
                      : ndim == 2 ? 4LL * ncx * ncy
                                  : 5LL * ncx * ncy * ncz;
-  if (nC * g->ppc() >= (1LL << 30)) return fail(CPAB_ERR_INVALID, "tessellation too large (nC=%lld)", (long long)nC);
+  // Cell ids are formed with 24-bit arithmetic, and a row's per-cell tables
+  // (the affine maps, ppc floats per cell, and the reverse-sweep table,
+  // 2 * ppc) are addressed with 32-bit byte offsets.
+  if (nC >= (1LL << 24) || 2 * nC * g->ppc() >= (1LL << 30))
+    return fail(CPAB_ERR_INVALID, "tessellation too large (nC=%lld, at most 2^24 - 1 cells)", (long long)nC);
   g->nC = (int)nC;
   return CPAB_OK;
 }

@@ -106,7 +106,7 @@ __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   const float xc = clamp_lookup(px), yc = clamp_lookup(py);
   const float sx = __builtin_floorf(xc * fx), sy = __builtin_floorf(yc * fy);
   const float lx = fmaf(xc, fx, -sx), ly = fmaf(yc, fy, -sy);
-  const int base = (int)fmaf(sy, fx, sx) << 2;  // exact: cx + cy*nx < 2^24
+  const int base = (int)fmaf(sy, fx, sx) << 2;  // exact: cx + cy*nx < 2^22
   int c = base + tri_2d(lx, ly);
   // Wave-wide "any lane outside (0,1)^2": one ballot per compare keeps the
   // masks in SGPRs (a ballot of a combined bool would first be materialised
@@ -188,9 +188,13 @@ template <> struct Aff<1> { float a, b; };
 template <> struct Aff<2> { float m[6]; };
 template <> struct Aff<3> { float m[12]; };
 
-// Per-cell table loads.  Global tables use 64-bit addressing; LDS tables are
-// passed as address-space-3 pointers so the offsets stay 32-bit (one
-// v_mul_u32_u24 per fetch) and the loads become ds_read2_b64 / ds_read_b128.
+// Per-cell table loads.  The C ABI limits a tessellation to fewer than 2^24
+// cells and a row's table to fewer than 2^30 floats, so the byte offset of an
+// entry fits in 32 bits: global loads take it as a VGPR offset from the scalar
+// row base (no 64-bit address arithmetic per fetch).  LDS
+// tables are passed as address-space-3 pointers so the offsets stay 32-bit
+// (one v_mul_u32_u24 per fetch) and the loads become ds_read2_b64 /
+// ds_read_b128.
 #define CPAB_LDS __attribute__((address_space(3)))
 template <typename T> using lds_ptr = const T CPAB_LDS*;
 typedef float v2f __attribute__((ext_vector_type(2)));
@@ -198,8 +202,16 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ lds_ptr<float> as_lds(const float* p) { return (lds_ptr<float>)p; }
 
+// Entry c of a global table of B-byte entries.  Cell ids are below 2^24, so
+// the offset is one full-rate v_mul_u32_u24.
+template <typename V, uint32_t B>
+__device__ __forceinline__ const V* entry(const float* tab, int c) {
+  const uint32_t off = __umul24((uint32_t)c, B);
+  return reinterpret_cast<const V*>(reinterpret_cast<const char*>(tab) + off);
+}
+
 __device__ __forceinline__ Aff<1> load_aff1(const float* tab, int c) {
-  const v2f v = reinterpret_cast<const v2f*>(tab)[c];
+  const v2f v = *entry<v2f, 8>(tab, c);
   return {v.x, v.y};
 }
 __device__ __forceinline__ Aff<1> load_aff1(lds_ptr<float> tab, int c) {
@@ -207,7 +219,7 @@ __device__ __forceinline__ Aff<1> load_aff1(lds_ptr<float> tab, int c) {
   return {v.x, v.y};
 }
 __device__ __forceinline__ Aff<2> load_aff2(const float* tab, int c) {
-  const v2f* q = reinterpret_cast<const v2f*>(tab) + 3 * (int64_t)c;
+  const v2f* q = entry<v2f, 24>(tab, c);
   const v2f a = q[0], b = q[1], d = q[2];
   return {{a.x, a.y, b.x, b.y, d.x, d.y}};
 }
@@ -217,7 +229,7 @@ __device__ __forceinline__ Aff<2> load_aff2(lds_ptr<float> tab, int c) {
   return {{a.x, a.y, b.x, b.y, d.x, d.y}};
 }
 __device__ __forceinline__ Aff<3> load_aff3(const float* tab, int c) {
-  const v4f* q = reinterpret_cast<const v4f*>(tab) + 3 * (int64_t)c;
+  const v4f* q = entry<v4f, 48>(tab, c);
   const v4f a = q[0], b = q[1], d = q[2];
   return {{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w}};
 }
@@ -387,13 +399,13 @@ template <> struct Adj<1> { float g; };
 template <> struct Adj<2> { float g[4]; };   // row-major g00 g01 g10 g11
 template <> struct Adj<3> { float g[9]; };   // row-major
 
-__device__ __forceinline__ Adj<1> load_adj1(const float* tab, int c) { return {tab[4 * (int64_t)c]}; }
+__device__ __forceinline__ Adj<1> load_adj1(const float* tab, int c) { return {*entry<float, 16>(tab, c)}; }
 __device__ __forceinline__ Adj<2> load_adj2(const float* tab, int c) {
-  const v4f v = reinterpret_cast<const v4f*>(tab)[3 * (int64_t)c];
+  const v4f v = *entry<v4f, 48>(tab, c);
   return {{v.x, v.y, v.z, v.w}};
 }
 __device__ __forceinline__ Adj<3> load_adj3(const float* tab, int c) {
-  const v4f* q = reinterpret_cast<const v4f*>(tab) + 6 * (int64_t)c;
+  const v4f* q = entry<v4f, 96>(tab, c);
   const v4f a = q[0], b = q[1], d = q[2];
   return {{a.x, a.y, a.z, b.x, b.y, b.z, d.x, d.y, d.z}};
 }
@@ -402,16 +414,16 @@ __device__ __forceinline__ Adj<3> load_adj3(const float* tab, int c) {
 template <int D> struct Inv { float m[D * (D + 1)]; };
 
 __device__ __forceinline__ Inv<1> load_inv1(const float* tab, int c) {
-  const v2f v = *reinterpret_cast<const v2f*>(tab + 4 * (int64_t)c + 1);
+  const v2f v = *reinterpret_cast<const v2f*>(entry<float, 16>(tab, c) + 1);
   return {{v.x, v.y}};
 }
 __device__ __forceinline__ Inv<2> load_inv2(const float* tab, int c) {
-  const v4f* q = reinterpret_cast<const v4f*>(tab) + 3 * (int64_t)c;
+  const v4f* q = entry<v4f, 48>(tab, c);
   const v4f a = q[1], b = q[2];
   return {{a.x, a.y, a.z, b.x, b.y, b.z}};
 }
 __device__ __forceinline__ Inv<3> load_inv3(const float* tab, int c) {
-  const v4f* q = reinterpret_cast<const v4f*>(tab) + 6 * (int64_t)c;
+  const v4f* q = entry<v4f, 96>(tab, c);
   const v4f a = q[3], b = q[4], d = q[5];
   return {{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w}};
 }
@@ -429,6 +441,15 @@ __device__ __forceinline__ void step_back(const Inv<D>& E, float (&p)[D]) {
   }
 #pragma unroll
   for (int i = 0; i < D; ++i) p[i] = q[i];
+}
+
+// Keeps the values in VGPRs at this point of the program (an empty asm
+// statement, no instruction): code that computes them cannot be sunk past it,
+// e.g. into the join block of a following divergent branch.
+template <int N>
+__device__ __forceinline__ void pin(float (&v)[N]) {
+#pragma unroll
+  for (int k = 0; k < N; ++k) __asm__ volatile("" : "+v"(v[k]));
 }
 
 // One reverse step: S += lam (x) [p; 1], then lam += G^T lam.

@@ -48,6 +48,11 @@ def test_forward_rejects_bad_steps_and_ndim():
     assert rc == 1 and "adaptive_substeps" in _err(lib)
     rc = lib.cpab_forward(2, 10, 1, 0, 50, 0, 4, 1, 0, p, p, p, p, None)
     assert rc == 1 and "tessellation" in _err(lib)
+    # cell ids are 24-bit: 2D 2048 x 2048 squares (2^24 triangles) is one too many
+    rc = lib.cpab_forward(2, 10, 1, 0, 50, 2048, 2048, 1, 0, p, p, p, p, None)
+    assert rc == 1 and "2^24" in _err(lib)
+    rc = lib.cpab_forward(3, 10, 1, 0, 50, 256, 256, 52, 0, p, p, p, p, None)
+    assert rc == 1 and "2^24" in _err(lib)
 
 
 def test_backward_rejects_null_and_small_workspace():
