@@ -98,37 +98,49 @@ __device__ __forceinline__ int cell_2d_outside(float px, float py, float fx, flo
   return base + (xl ? tl : (xh ? th : tm));
 }
 
+// Inside rule from the clamped coordinates: square base id (4 * square) in
+// `base`, local coordinates in (lx, ly), and the triangle within the square.
+__device__ __forceinline__ int tri_2d_inside(float xc, float yc, float fx, float fy, int& base,
+                                             float& lx, float& ly) {
+  const float sx = __builtin_floorf(xc * fx), sy = __builtin_floorf(yc * fy);
+  lx = fmaf(xc, fx, -sx);
+  ly = fmaf(yc, fy, -sy);
+  base = (int)fmaf(sy, fx, sx) << 2;  // exact: cx + cy*nx < 2^22
+  return tri_2d(lx, ly);
+}
+
 // Square (cx, cy) holds triangles 4*(cx + cy*nx) + {0 top, 1 right, 2 bottom, 3 left}.
-// Lanes strictly inside (0,1)^2 use the inside rule; if any lane of the wave is
-// outside, a wave-uniform branch applies the boundary rules to all its lanes.
+// A wave whose lanes all lie in (0, kClampHi]^2, where the lookup clamp is the
+// identity, takes the inside rule on the raw coordinates.  Otherwise a
+// wave-uniform branch clamps, and applies the boundary rules to lanes outside
+// (0,1)^2.
 __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   const float fx = (float)nx, fy = (float)ny;
-  const float xc = clamp_lookup(px), yc = clamp_lookup(py);
-  const float sx = __builtin_floorf(xc * fx), sy = __builtin_floorf(yc * fy);
-  const float lx = fmaf(xc, fx, -sx), ly = fmaf(yc, fy, -sy);
-  const int base = (int)fmaf(sy, fx, sx) << 2;  // exact: cx + cy*nx < 2^22
-  int c = base + tri_2d(lx, ly);
-  // Wave-wide "any lane outside (0,1)^2": one ballot per compare keeps the
-  // masks in SGPRs (a ballot of a combined bool would first be materialised
-  // in a VGPR and compared back).
-  const uint64_t outside = __builtin_amdgcn_ballot_w64(!(px > 0.0f)) |
-                           __builtin_amdgcn_ballot_w64(!(px < 1.0f)) |
-                           __builtin_amdgcn_ballot_w64(!(py > 0.0f)) |
-                           __builtin_amdgcn_ballot_w64(!(py < 1.0f));
-  if (outside) {
-    // Away from the domain's corners the boundary rules return a fixed
-    // triangle per side (left 3, right 1, bottom 0, top 2) and fall through to
-    // the inside rule otherwise (inside lanes, NaN).  Points on a domain edge
-    // (every meshgrid row has two) mostly get that same triangle from the
-    // inside rule already, so the full rules run only when some lane is at a
-    // corner or the inside rule disagrees with its side's triangle.
-    const int t = c - base;
-    const bool xl = px <= 0.0f, xh = px >= 1.0f, yl = py <= 0.0f, yh = py >= 1.0f;
-    const int side = xl ? 3 : (xh ? 1 : (yl ? 0 : (yh ? 2 : t)));
-    const bool corner = (xl | xh) & (yl | yh);
-    if (__builtin_amdgcn_ballot_w64(corner | (side != t)))
-      c = cell_2d_outside(px, py, fx, fy, base, lx, ly);
+  // One ballot per compare keeps the masks in SGPRs (a ballot of a combined
+  // bool would first be materialised in a VGPR and compared back).
+  const uint64_t edge = __builtin_amdgcn_ballot_w64(!(px > 0.0f)) |
+                        __builtin_amdgcn_ballot_w64(!(px <= kClampHi)) |
+                        __builtin_amdgcn_ballot_w64(!(py > 0.0f)) |
+                        __builtin_amdgcn_ballot_w64(!(py <= kClampHi));
+  int base;
+  float lx, ly;
+  if (!edge) {
+    const int t = tri_2d_inside(px, py, fx, fy, base, lx, ly);
+    return base + t;
   }
+  const int t = tri_2d_inside(clamp_lookup(px), clamp_lookup(py), fx, fy, base, lx, ly);
+  int c = base + t;
+  // Away from the domain's corners the boundary rules return a fixed triangle
+  // per side (left 3, right 1, bottom 0, top 2) and fall through to the inside
+  // rule otherwise (inside lanes, NaN).  Points on a domain edge (every
+  // meshgrid row has two) mostly get that same triangle from the inside rule
+  // already, so the full rules run only when some lane is at a corner or the
+  // inside rule disagrees with its side's triangle.
+  const bool xl = px <= 0.0f, xh = px >= 1.0f, yl = py <= 0.0f, yh = py >= 1.0f;
+  const int side = xl ? 3 : (xh ? 1 : (yl ? 0 : (yh ? 2 : t)));
+  const bool corner = (xl | xh) & (yl | yh);
+  if (__builtin_amdgcn_ballot_w64(corner | (side != t)))
+    c = cell_2d_outside(px, py, fx, fy, base, lx, ly);
   return c;
 }
 
