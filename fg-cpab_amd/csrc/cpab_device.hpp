@@ -43,11 +43,6 @@ __device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x);
 __device__ __forceinline__ float log_cr(float x) { return (float)log((double)x); }
 __device__ __forceinline__ float expm1_cr(float x) { return (float)expm1((double)x); }
 
-__device__ __forceinline__ int floor_to_int(float x) {
-  // __float2int_rd: round toward -inf, then convert.
-  return (int)__builtin_floorf(x);
-}
-
 // ---------------------------------------------------------------------------
 // Cell lookup.  Indexing and tie-breaking follow
 //   1D: cpab_ops_1d.cu:52-59   2D: cpab_ops_2d.cu:71-128   3D: cpab_ops_3d.cu:67-131
@@ -144,10 +139,46 @@ __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   return c;
 }
 
+// Tetrahedron of the clamped point (xc, yc, zc) in [0,1]^3.  The cube
+// coordinates are kept as floats (integers below 2^24, so every sum and
+// product here is exact): floor(xc * n) capped at n - 1 as the reference's
+// min(floor, n - 1), then the cube id and its parity.
+__device__ __forceinline__ int tet_3d(float xc, float yc, float zc, float fx, float fy, float fz,
+                                      float fxy) {
+  const float si = fminf(__builtin_floorf(xc * fx), fx - 1.0f);
+  const float sj = fminf(__builtin_floorf(yc * fy), fy - 1.0f);
+  const float sk = fminf(__builtin_floorf(zc * fz), fz - 1.0f);
+  float x = fmaf(xc, fx, -si);
+  float y = fmaf(yc, fy, -sj);
+  const float z = fmaf(zc, fz, -sk);
+  const uint32_t cube = (uint32_t)fmaf(sk, fxy, fmaf(sj, fx, si));
+  if ((int)(si + sj + sk) & 1) {  // parity of i + j + k == parity of i ^ j ^ k
+    const float t = x;
+    x = y;
+    y = 1.0f - t;
+  }
+  // First matching test wins, as in the reference's if-chain; evaluated as
+  // selects (every lane needs all four tests anyway).  (-x) + y == -(x - y)
+  // and ((-x) - y) + z == z - (x + y) in IEEE arithmetic.
+  const float d = x - y, s = x + y;
+  int t = (d - z >= 0.0f) ? 4 : 0;
+  t = ((-d) - z >= 0.0f) ? 3 : t;
+  t = ((s + z) - 2.0f >= 0.0f) ? 2 : t;
+  t = (z - s >= 0.0f) ? 1 : t;
+  return (int)__umul24(cube, 5u) + t;
+}
+
 // Cube (i, j, k) holds tetrahedra 5*(i + j*nx + k*nx*ny) + {0 central, 1..4 corners};
 // odd-parity cubes are mirrored by the local remap (x, y) -> (y, 1 - x).
+// A wave whose lanes all lie in [0,1]^3 (the meshgrid and most trajectories)
+// needs neither the corner rule nor the clamps: as unsigned integers the bit
+// patterns of +0 ... 1.0 are exactly 0 ... 0x3f800000, and negative values,
+// -0, NaN and infinities compare above.
 __device__ __forceinline__ int cell_3d(float px, float py, float pz, int nx, int ny, int nz) {
   const float fx = (float)nx, fy = (float)ny, fz = (float)nz;
+  const float fxy = (float)(nx * ny);
+  const uint32_t bmax = max(max(__float_as_uint(px), __float_as_uint(py)), __float_as_uint(pz));
+  if (!__builtin_amdgcn_ballot_w64(bmax > 0x3f800000u)) return tet_3d(px, py, pz, fx, fy, fz, fxy);
   const float ox = (fabsf(px - 0.5f) - 0.5f) * fx;
   const float oy = (fabsf(py - 0.5f) - 0.5f) * fy;
   const float oz = (fabsf(pz - 0.5f) - 0.5f) * fz;
@@ -165,29 +196,8 @@ __device__ __forceinline__ int cell_3d(float px, float py, float pz, int nx, int
       }
     }
   }
-  const float xc = fminf(fmaxf(px, 0.0f), 1.0f);
-  const float yc = fminf(fmaxf(py, 0.0f), 1.0f);
-  const float zc = fminf(fmaxf(pz, 0.0f), 1.0f);
-  const int i = min(floor_to_int(xc * fx), nx - 1);
-  const int j = min(floor_to_int(yc * fy), ny - 1);
-  const int k = min(floor_to_int(zc * fz), nz - 1);
-  float x = fmaf(xc, fx, -(float)i);
-  float y = fmaf(yc, fy, -(float)j);
-  const float z = fmaf(zc, fz, -(float)k);
-  int c = 5 * (i + j * nx + k * nx * ny);
-  if ((i ^ j ^ k) & 1) {
-    const float t = x;
-    x = y;
-    y = 1.0f - t;
-  }
-  // First matching test wins, as in the reference's if-chain; evaluated as
-  // selects (every lane needs all four tests anyway).
-  const float s = x + y;
-  int t = ((x - y) - z >= 0.0f) ? 4 : 0;
-  t = ((y - x) - z >= 0.0f) ? 3 : t;         // ((-x) + y) - z
-  t = ((s + z) - 2.0f >= 0.0f) ? 2 : t;
-  t = (z - s >= 0.0f) ? 1 : t;               // ((-x) - y) + z, rounded identically
-  return c + t;
+  return tet_3d(fminf(fmaxf(px, 0.0f), 1.0f), fminf(fmaxf(py, 0.0f), 1.0f),
+                fminf(fmaxf(pz, 0.0f), 1.0f), fx, fy, fz, fxy);
 }
 
 // ---------------------------------------------------------------------------
