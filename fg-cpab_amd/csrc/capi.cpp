@@ -638,10 +638,12 @@ static int check_interp(int ndim, int64_t B, int64_t C, const int64_t* in_size,
   for (int k = 0; k < ndim; ++k) plane *= in_size[k];
   if (plane >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "one data channel must hold < 2^31 values");
   if (ndim >= 2) {
-    // one 256-thread workgroup per 32 x 64 tile, 1D grid (< 2^32 threads)
-    const int64_t tiles = div_up(out_size[0], 32) * div_up(out_size[ndim - 1], 64) * B *
+    // one workgroup per tile, 1D grid (fewer than 2^31 threads)
+    const int64_t tiles = div_up(out_size[0], cpab::kInterpTile0) *
+                          div_up(out_size[ndim - 1], cpab::kInterpTileLast) * B *
                           (ndim == 3 ? out_size[1] : 1);
-    if (tiles >= (1LL << 23)) return fail(CPAB_ERR_INVALID, "output too large for one launch");
+    if (tiles * cpab::kInterpThreads >= (1LL << 31))
+      return fail(CPAB_ERR_INVALID, "output too large for one launch");
   }
   return CPAB_OK;
 }

@@ -7,9 +7,10 @@
 // with coordinate 0 fastest, p = i0 + o0*(i1 + o1*i2); the output is
 // [B, C, o0, o1(, o2)] with the LAST axis fastest.  So the point order and the
 // output order are transposes of each other.  HBM-bound, so each workgroup
-// takes a 32 x 64 tile over (i0, i_last) at fixed i_mid, reads the grid rows
+// takes a kT0 x kTL tile over (i0, i_last) at fixed i_mid, reads the grid rows
 // coalesced along i0 into LDS, and computes/writes with i_last across the
-// lanes (coalesced output and, for smooth warps, near-contiguous data rows).
+// lanes (whole 128-byte output lines and, for smooth warps, near-contiguous
+// data rows).
 // The backward does the same transpose in the other direction for grad_grid.
 // The per-sample arithmetic lives in cpab_sample.hpp.
 #include <hip/hip_runtime.h>
@@ -20,9 +21,10 @@
 namespace cpab {
 namespace {
 
-constexpr int kT0 = 32;      // tile extent along i0 (grid rows are contiguous in i0)
-constexpr int kTL = 64;      // tile extent along i_last (output rows are contiguous in i_last)
-constexpr int kThreads = 256;
+constexpr int kT0 = kInterpTile0;      // tile extent along i0 (grid rows are contiguous in i0)
+constexpr int kTL = kInterpTileLast;   // tile extent along i_last (output rows are contiguous in i_last)
+constexpr int kThreads = kInterpThreads;
+static_assert(kThreads % kTL == 0 && kT0 % 4 == 0 && 64 % kTL == 0, "tile shape");
 constexpr int kUnroll = 4;   // outputs in flight per lane in the compute loop
 constexpr int kXcds = 8;     // MI355X: accelerator complex dies, each with its own L2
 
