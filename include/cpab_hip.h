@@ -17,7 +17,10 @@
  *     TORCH_CHECK, or exit()ed on a launch error, transformer_cuda.cu:12-18);
  *   - `batched` = 1 when points are [n_theta, ndim, nP], 0 when one [ndim, nP]
  *     set is shared by all thetas (the reference's `broadcast` flag,
- *     transformer_cuda.cpp:43).
+ *     transformer_cuda.cpp:43);
+ *   - size limits (CPAB_ERR_INVALID beyond them): fewer than 2^24 cells
+ *     (cell ids and table offsets are 24/32-bit in the kernels), nP below
+ *     2^31 / 3, and n_theta (n_batch, n_stages * n_batch) below 65536.
  *
  * Layouts: theta [n_theta, d]; As/Trels [n_theta, nC, ndim, ndim+1] row-major;
  * moments [n_theta, nC, ndim*(ndim+1)]; points/outputs SoA rows [.., ndim, nP].
