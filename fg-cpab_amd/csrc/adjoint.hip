@@ -424,8 +424,20 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
                                               const Cells& g, const IO& io, float* bins,
                                               int* keys, float* __restrict__ mom_b) {
   constexpr int PP = Dim<D>::P;
+  // A trajectory's last flush has all 64 lanes of every wave adding to
+  // scattered bins at the same moment, a burst the LDS atomic pipe drains at
+  // about one lane per clock.  With full bins (1D/2D, no adaptive substeps:
+  // registers to spare) it is kept pending instead and issued one component
+  // every TS / PP steps during the next range's phase 1, alongside its VALU
+  // work; the last range's flush follows the loop.
+  constexpr bool kSpread = D <= 2 && !ADAPTIVE && BINS == kBinsFull;
   const float h = 1.0f / (float)TS;
   const float hh = h * 0.5f;
+  float pend[PP];
+#pragma unroll
+  for (int k = 0; k < PP; ++k) pend[k] = 0.0f;
+  int pend_c = 0;
+  bool pend_on = false;
   int lo, hi;
   wg_range(nP, lo, hi);
   for (int base = lo; base < hi; base += blockDim.x) {
@@ -446,6 +458,14 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
     Aff<D> A = fetch<D>(tab, cur);
 #pragma unroll
     for (int t = 0; t < TS; ++t) {
+      if constexpr (kSpread) {
+#pragma unroll
+        for (int k = 0; k < PP; ++k) {
+          if (t == (k * TS) / PP && pend_on)
+            __hip_atomic_fetch_add(bins + PP * pend_c + k, pend[k], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+      }
       const int c = (t == 0) ? cur : lookup<D>(p, g);
       // Divergent branch, skipped (exec = 0) when no lane changed cell.
       if (c != cur) A = fetch<D>(tab, c);
@@ -499,12 +519,18 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
         c = cn;
       }
     }
-    if (valid) {
+    if constexpr (kSpread) {
+#pragma unroll
+      for (int k = 0; k < PP; ++k) pend[k] = m[k];
+      pend_c = c;
+      pend_on = valid;
+    } else if (valid) {
       if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, c, m);
       else flush_lds<PP>(bins, c, m);
     }
     io.finish(pi, valid, lam);
   }
+  if (kSpread && pend_on) flush_lds<PP>(bins, pend_c, pend);
 }
 
 // LDS layout of a backward workgroup: [A table (LDS_A)] then either the full
@@ -605,12 +631,13 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
 // on entry), or, from a dense full-bin workgroup, to its partial table with
 // its dense-part bit set; the reverse-sweep table G holds the same rows
 // (RevStride<D>::S floats per cell).
-// Launch bound: 1024 threads (4 waves per SIMD, up to 128 VGPRs) for the 1D/2D
-// register variant without adaptive substeps (cells only in registers, ~90
-// VGPRs); 768 (3 waves per SIMD, up to 168 VGPRs) for 3D, the segmented variant
-// and the 1D/2D adaptive register variant, whose trajectory takes 2 x 50 VGPRs.
+// Launch bound: 1024 threads (4 waves per SIMD, up to 128 VGPRs) for the
+// register variant without adaptive substeps (cells only in registers: ~90
+// VGPRs in 2D, ~120 in 3D); 768 (3 waves per SIMD, up to 168 VGPRs) for the
+// segmented variant and the adaptive register variant, whose trajectory takes
+// D x 50 VGPRs.
 template <int D, bool ADAPTIVE, int TS>
-constexpr int kBwdThreads = (TS > 0 && !ADAPTIVE && D <= 2) ? 1024 : 768;
+constexpr int kBwdThreads = (TS > 0 && !ADAPTIVE) ? 1024 : 768;
 
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kernel(

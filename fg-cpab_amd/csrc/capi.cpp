@@ -158,15 +158,15 @@ cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_thet
   // Register variant: the trajectory's cells (and, with adaptive substeps, its
   // positions) in VGPRs, one workgroup per CU; the per-cell tables are read
   // through L1/L2 (re-read only when a lane changes cell).  Without adaptive
-  // substeps in 1D/2D: 1024 threads (4 waves per SIMD); 3D and 1D/2D adaptive:
-  // 768 threads (3 waves per SIMD).
+  // substeps: 1024 threads (4 waves per SIMD); with them: 768 threads (3 waves
+  // per SIMD, the positions take D x 50 VGPRs).
   const bool reg = T == cpab::kRegSteps && g.nC <= 65535 && env_int("CPAB_BWD_REG", 1) &&
                    (g.ndim <= 2 ? c.lds_bins != 0 : (!adaptive && (c.lds_bins || c.lds_cache)));
   c.reg_steps = reg ? cpab::kRegSteps : 0;
   const int64_t used = c.lds_bins ? table : (c.lds_cache ? cache : 0);
   c.lds_table = (used + table <= dev.lds) ? env_int("CPAB_BWD_LDS_TABLE", reg ? 0 : 1) : 0;
   const int64_t lds = used + (c.lds_table ? table : 0);
-  const int limit = (reg && !adaptive && g.ndim <= 2) ? 1024 : 768;  // kernel launch bound
+  const int limit = (reg && !adaptive) ? 1024 : 768;  // kernel launch bound
   int wg_per_cu;
   if (reg) {
     c.block = env_int("CPAB_BWD_BLOCK", limit);
