@@ -248,7 +248,10 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
 // across the workgroup and the table can be swapped between stages; a chain
 // over few points has only a handful of waves per SIMD, and LDS latency
 // instead of L1/L2 latency on the frequent per-wave table re-reads is what
-// keeps them busy.
+// keeps them busy.  One point per lane: with so few trajectories, twice the
+// waves (each one stream of dependent steps) hide the per-step branch and
+// scalar work better than two interleaved points per wave (C5, 262,144
+// points x 8 stages: 126 against 176 us).
 template <bool ADAPTIVE, int PPT>
 __global__ __launch_bounds__(1024) void chain2d_lds_kernel(int nP, int batched, int T, int nx,
                                                           int ny, int K,
@@ -492,14 +495,13 @@ hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_batch, int ba
   const bool lds_table = cfg.lds_table && K == 1;
   const size_t lds = lds_table ? tab : 0;
   if (g.ndim == 2 && K > 1 && cfg.lds_chain && tab <= (size_t)cfg.lds_chain) {
-    // one pass over the points: grid.x * block * PPT >= nP
-    const int ppt = adaptive ? 1 : 2;
-    const int64_t need = (nP + (int64_t)ppt * cfg.block - 1) / ((int64_t)ppt * cfg.block);
+    // one pass over the points, one point per lane
+    const int64_t need = (nP + (int64_t)cfg.block - 1) / (int64_t)cfg.block;
     const dim3 gridc((unsigned)need, (unsigned)n_batch);
     return adaptive ? launch_with_lds(chain2d_lds_kernel<true, 1>, gridc, block, tab, s, (int)nP,
                                       batched, T, g.nx, g.ny, K, points, Trels, As, out,
                                       stage_points)
-                    : launch_with_lds(chain2d_lds_kernel<false, 2>, gridc, block, tab, s, (int)nP,
+                    : launch_with_lds(chain2d_lds_kernel<false, 1>, gridc, block, tab, s, (int)nP,
                                       batched, T, g.nx, g.ny, K, points, Trels, As, out,
                                       stage_points);
   }
