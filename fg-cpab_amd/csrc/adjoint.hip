@@ -186,6 +186,54 @@ __device__ __forceinline__ void flush_lds(float* bins, int c, const float (&m)[P
     __hip_atomic_fetch_add(q + k, m[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// Sums of a converged wave's last flush, pre-added per run of lanes with the
+// same cell.  Meshgrid inputs start neighbouring trajectories in the same
+// cell, so without this up to 64 lanes add into the same few LDS words,
+// which serialises on the atomic unit.  When the lanes' cells form at most 16
+// runs (counted per row of 16 lanes), each row runs a segmented inclusive scan
+// over its runs (DPP row shifts by 1, 2, 4, 8, guarded by the run id) and only
+// the last lane of each run keeps a flush (`on`), holding the run's sums in
+// `out`; otherwise (scattered cells, e.g. random points) `out` = m and
+// `on` = need.  Lanes with need == false take part in no run.
+// One step of the segmented scan: add the value CTRL's row shift brings in
+// when it comes from the same run (lanes shifted in from outside the row read
+// 0, which matches no run id).
+template <int CTRL, int P>
+__device__ __forceinline__ void run_scan_step(int run, float (&v)[P]) {
+  const int rd = __builtin_amdgcn_update_dpp(0, run, CTRL, 0xf, 0xf, true);
+  const float f = rd == run ? 1.0f : 0.0f;
+#pragma unroll
+  for (int k = 0; k < P; ++k) {
+    const float t = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[k]), CTRL, 0xf, 0xf, true));
+    v[k] = fmaf(t, f, v[k]);
+  }
+}
+
+template <int P>
+__device__ __forceinline__ void wave_run_sums(bool need, int c, const float (&m)[P],
+                                              float (&out)[P], bool& on) {
+  const int lane = __lane_id();
+  const int key = need ? c : -1;
+  const int before = __shfl_up(key, 1);
+  const bool head = (lane & 15) == 0 || key != before;
+  const uint64_t heads = __ballot(head);
+#pragma unroll
+  for (int k = 0; k < P; ++k) out[k] = need ? m[k] : 0.0f;
+  on = need;
+  if (__popcll(heads) > 16) return;  // wave-uniform
+  // run id: heads at or below this lane (>= 1, since every row starts a run)
+  const int run = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(heads >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)heads, 0u)) +
+                  (head ? 1 : 0);
+  run_scan_step<0x111, P>(run, out);  // row_shr:1
+  run_scan_step<0x112, P>(run, out);  // row_shr:2
+  run_scan_step<0x114, P>(run, out);  // row_shr:4
+  run_scan_step<0x118, P>(run, out);  // row_shr:8
+  const bool last = (lane & 15) == 15 || ((heads >> (lane < 63 ? lane + 1 : 63)) & 1);
+  on = need && last;
+}
+
 // LDS cache flush (divergent lanes allowed).  The slot of cell c is claimed
 // with a compare-and-swap on its key; a lane whose probe sequence meets only
 // other cells adds to HBM instead.
@@ -520,13 +568,15 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
       }
     }
     if constexpr (kSpread) {
-#pragma unroll
-      for (int k = 0; k < PP; ++k) pend[k] = m[k];
+      wave_run_sums<PP>(valid, c, m, pend, pend_on);
       pend_c = c;
-      pend_on = valid;
+    } else if (BINS == kBinsFull) {
+      float r[PP];
+      bool on;
+      wave_run_sums<PP>(valid, c, m, r, on);
+      if (on) flush_lds<PP>(bins, c, r);
     } else if (valid) {
-      if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, c, m);
-      else flush_lds<PP>(bins, c, m);
+      flush_cache<PP>(keys, bins, mom_b, c, m);
     }
     io.finish(pi, valid, lam);
   }
