@@ -570,13 +570,14 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
     if constexpr (kSpread) {
       wave_run_sums<PP>(valid, c, m, pend, pend_on);
       pend_c = c;
-    } else if (BINS == kBinsFull) {
+    } else {
       float r[PP];
       bool on;
       wave_run_sums<PP>(valid, c, m, r, on);
-      if (on) flush_lds<PP>(bins, c, r);
-    } else if (valid) {
-      flush_cache<PP>(keys, bins, mom_b, c, m);
+      if (on) {
+        if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, c, r);
+        else flush_lds<PP>(bins, c, r);
+      }
     }
     io.finish(pi, valid, lam);
   }
