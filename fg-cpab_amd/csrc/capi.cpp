@@ -189,30 +189,56 @@ cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_thet
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // ---- optional kernel timing (HIP events recorded on the launch stream) -----
+// Events are created once per device and recycled through a pool: a timed
+// launch then costs two hipEventRecord calls, which matters for small,
+// host-bound problems where the timing runs inside the measured region.
 struct Timed {
   const char* name;
+  int device;
   hipEvent_t start, stop;
 };
 std::mutex g_prof_mu;
 std::atomic<bool> g_prof_on{false};
 std::vector<Timed> g_prof_pending;
+std::vector<std::pair<int, hipEvent_t>> g_prof_pool;  // (device, free event)
+
+// Caller holds g_prof_mu.
+bool pool_take(int device, hipEvent_t* e) {
+  for (size_t i = g_prof_pool.size(); i-- > 0;) {
+    if (g_prof_pool[i].first == device) {
+      *e = g_prof_pool[i].second;
+      g_prof_pool[i] = g_prof_pool.back();
+      g_prof_pool.pop_back();
+      return true;
+    }
+  }
+  return hipEventCreate(e) == hipSuccess;
+}
 
 bool prof_begin(hipStream_t s, hipEvent_t* a) {
   if (!g_prof_on.load(std::memory_order_relaxed)) return false;
-  if (hipEventCreate(a) != hipSuccess) return false;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  if (!pool_take(device, a)) return false;
   if (hipEventRecord(*a, s) != hipSuccess) {
-    (void)hipEventDestroy(*a);
+    g_prof_pool.push_back({device, *a});
     return false;
   }
   return true;
 }
 void prof_end(bool on, hipEvent_t a, const char* name, hipStream_t s) {
   if (!on) return;
-  hipEvent_t b;
-  if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return; }
-  (void)hipEventRecord(b, s);
+  int device = 0;
+  (void)hipGetDevice(&device);
   std::lock_guard<std::mutex> lock(g_prof_mu);
-  g_prof_pending.push_back({name, a, b});
+  hipEvent_t b;
+  if (!pool_take(device, &b)) {
+    g_prof_pool.push_back({device, a});
+    return;
+  }
+  (void)hipEventRecord(b, s);
+  g_prof_pending.push_back({name, device, a, b});
 }
 
 // Forward of a chain of K stages (K = 1: one transform).  ndim 1 uses the
@@ -601,13 +627,13 @@ int cpab_profile_read(const char* kernel, double* total_ms, int64_t* launches) {
   std::vector<Timed> keep;
   for (const Timed& t : g_prof_pending) {
     if (std::strcmp(t.name, kernel) != 0) { keep.push_back(t); continue; }
-    // Every matching record is consumed (and its events released) even if one
-    // of them fails, so nothing is left pointing at destroyed events.
+    // Every matching record is consumed (and its events returned to the
+    // pool) even if one of them fails.
     float ms = 0.0f;
     hipError_t e = hipEventSynchronize(t.stop);
     if (e == hipSuccess) e = hipEventElapsedTime(&ms, t.start, t.stop);
-    (void)hipEventDestroy(t.start);
-    (void)hipEventDestroy(t.stop);
+    g_prof_pool.push_back({t.device, t.start});
+    g_prof_pool.push_back({t.device, t.stop});
     if (e != hipSuccess) {
       if (first == hipSuccess) first = e;
       continue;
