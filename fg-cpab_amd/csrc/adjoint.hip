@@ -1,15 +1,20 @@
 // Fused backward: midpoint-trajectory replay + discrete adjoint + cell moments
 // (cpab_ops_1d.cu:331-422, cpab_ops_2d.cu:384-513, cpab_ops_3d.cu:405-532).
 //
-// Per trajectory (one lane), two variants with identical results:
-//   register  (T == kRegSteps, 1D/2D) phase 1 runs the T explicit-midpoint
-//             steps fully unrolled and keeps every position and cell in VGPRs
-//             (cells packed two per register); phase 2 walks them backwards.
-//             One midpoint pass per trajectory.
-//   segmented (any T <= 100, 3D) phase 1 keeps a checkpoint every kSeg steps
-//             in a VGPR shift register; phase 2 replays each segment from its
+// Per trajectory (one lane), two variants:
+//   register  (T == kRegSteps) phase 1 runs the T explicit-midpoint steps
+//             fully unrolled and keeps every cell in VGPRs (two per
+//             register); phase 2 walks them backwards, recovering each
+//             position from the next through the cell's inverse one-step map
+//             (with adaptive substeps, whose steps are not fixed affine maps,
+//             the positions are kept in VGPRs too).  One midpoint pass per
+//             trajectory.
+//   segmented (any T <= 100) phase 1 keeps a checkpoint every kSeg steps in a
+//             VGPR shift register; phase 2 replays each segment from its
 //             checkpoint into registers and walks it backwards (the
 //             reference's scheme, cpab_ops_2d.cu:236-263).
+// Both visit the reference's cells; the positions fed to the sums may differ
+// from the replayed ones by a few ulps in the register variant.
 // In both, phase 2 propagates lambda and accumulates the 2x3 (1x2, 3x4) sum
 // S = sum lam (x) [p; 1] of the current cell, flushing it whenever the cell
 // changes, as the reference groups its moment flushes.  The reverse step is the
@@ -671,7 +676,8 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
   }
 }
 
-// TS == 0: segmented variant; TS > 0: register variant (requires full bins).
+// TS == 0: segmented variant; TS > 0: register variant (full LDS bins or the
+// LDS cell cache, no global-atomic flushes).
 // One workgroup = one theta (blockIdx.y) x one contiguous point range
 // (blockIdx.x).  A chain of K stages (Cpab.transform_grid_chain) runs its
 // stages last to first inside the kernel: stage k reads its input points from
