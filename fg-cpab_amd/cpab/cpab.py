@@ -205,17 +205,12 @@ class Cpab(object):
         """Warp ``data`` [n_batch, C, *in_size] by theta onto an ``outsize`` grid.
 
         Same result as ``interpolate(data, transform_grid(uniform_meshgrid(outsize),
-        theta), outsize)`` (cpab/cpab.py:295-309).  In 1D and 2D it is computed
-        by one fused forward and one fused backward launch.  In 3D the separate
-        kernels are faster (the fused kernels' image-order pixel walk scatters
-        the cells a workgroup touches), so the three steps run as in the
-        reference.
+        theta), outsize)`` (cpab/cpab.py:295-309), computed by one fused
+        forward and one fused backward launch: the warped grid never goes
+        through HBM.
         """
         grid = self._meshgrid(outsize)
-        if self.params.ndim <= 2:
-            return transform_data_fused(data, theta, grid, outsize, self.params)
-        grid_t = self.transform_grid(grid, theta)
-        return self.interpolate(data, grid_t, outsize)
+        return transform_data_fused(data, theta, grid, outsize, self.params)
 
     def _meshgrid(self, outsize):
         # uniform_meshgrid is deterministic: keep one per output size (internal
