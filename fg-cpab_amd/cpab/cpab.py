@@ -122,8 +122,7 @@ class Cpab(object):
 
     def uniform_meshgrid(self, n_points):
         """[ndim, prod(n_points)] grid over the domain, coordinate 0 varying fastest."""
-        lin = [torch.linspace(self.params.domain_min[i], self.params.domain_max[i],
-                              n_points[i], device=_DEVICE) for i in range(self.params.ndim)]
+        lin = self._linspaces(n_points)
         mesh = torch.meshgrid(lin[::-1], indexing='ij')
         return torch.cat([g.reshape(1, -1) for g in mesh[::-1]], dim=0)
 
@@ -209,17 +208,22 @@ class Cpab(object):
         forward and one fused backward launch: the warped grid never goes
         through HBM.
         """
-        grid = self._meshgrid(outsize)
-        return transform_data_fused(data, theta, grid, outsize, self.params)
+        return transform_data_fused(data, theta, self._uniform_axes(outsize), outsize,
+                                    self.params)
 
-    def _meshgrid(self, outsize):
-        # uniform_meshgrid is deterministic: keep one per output size (internal
-        # use only, never handed to callers, so it cannot be modified).
+    def _uniform_axes(self, outsize):
+        # The per-axis coordinates uniform_meshgrid takes the Cartesian product
+        # of, concatenated; deterministic, so one per output size is kept
+        # (internal use only, never handed to callers).
         key = tuple(int(v) for v in outsize)
-        cache = self.__dict__.setdefault("_meshgrids", {})
+        cache = self.__dict__.setdefault("_uniform_axes_cache", {})
         if key not in cache:
-            cache[key] = self.uniform_meshgrid(list(key))
+            cache[key] = torch.cat(self._linspaces(list(key)))
         return cache[key]
+
+    def _linspaces(self, n_points):
+        return [torch.linspace(self.params.domain_min[i], self.params.domain_max[i],
+                               n_points[i], device=_DEVICE) for i in range(self.params.ndim)]
 
     def _check_input(self, tess_size, zero_boundary, volume_perservation, override):
         assert type(tess_size) in [list, tuple], 'tess_size must be a list or tuple'

@@ -185,25 +185,25 @@ class Native:
                                             wbytes, _stream(points.device)),
                "cpab_chain_backward")
 
-    def transform_data_forward(self, ndim, data, grid, outsize, T, nc, adaptive, Trels, As, out,
+    def transform_data_forward(self, ndim, data, axes, outsize, T, nc, adaptive, Trels, As, out,
                                final_points):
         ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
         _check(self.lib.cpab_transform_data_forward(
             ndim, data.shape[0], data.shape[1], _lengths(data.shape[2:]), _lengths(outsize),
-            int(T), ncx, ncy, ncz, int(adaptive), _ptr(grid), _ptr(Trels), _ptr(As), _ptr(data),
+            int(T), ncx, ncy, ncz, int(adaptive), _ptr(axes), _ptr(Trels), _ptr(As), _ptr(data),
             _ptr(out), _ptr(final_points), _stream(data.device)), "cpab_transform_data_forward")
 
     def transform_data_backward_workspace_size(self, ndim, n_batch, outsize, nC):
         return int(self.lib.cpab_transform_data_backward_workspace_size(
             ndim, n_batch, _lengths(outsize), nC))
 
-    def transform_data_backward(self, ndim, data, grid, outsize, T, nc, adaptive, final_points,
+    def transform_data_backward(self, ndim, data, axes, outsize, T, nc, adaptive, final_points,
                                 As, grad_out, moments, grad_data, workspace):
         ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
         wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
         _check(self.lib.cpab_transform_data_backward(
             ndim, data.shape[0], data.shape[1], _lengths(data.shape[2:]), _lengths(outsize),
-            int(T), ncx, ncy, ncz, int(adaptive), _ptr(grid), _ptr(final_points), _ptr(As),
+            int(T), ncx, ncy, ncz, int(adaptive), _ptr(axes), _ptr(final_points), _ptr(As),
             _ptr(data), _ptr(grad_out), _ptr(moments), _ptr(grad_data), _ptr(workspace), wbytes,
             _stream(data.device)), "cpab_transform_data_backward")
 

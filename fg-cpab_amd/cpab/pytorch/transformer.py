@@ -262,28 +262,31 @@ class _CPABChainFunction(torch.autograd.Function):
         return gp, grad_theta.view(K, n_batch, tab["d"]), None
 
 
-def CPAB_transform_data(data, theta, grid, outsize, params):
-    """``interpolate(data, CPAB_transformer(grid, theta, params), outsize)`` in
-    one fused forward and one fused backward launch.
+def CPAB_transform_data(data, theta, axes, outsize, params):
+    """``interpolate(data, CPAB_transformer(meshgrid, theta, params), outsize)``
+    in one fused forward and one fused backward launch.
 
     Arguments:
         data: [n_batch, n_channels, *in_size]
         theta: [n_batch, d]
-        grid: [ndim, prod(outsize)] meshgrid of ``outsize`` (``Cpab.uniform_meshgrid``)
+        axes: [sum(outsize)] the per-axis coordinates of the uniform grid, axis 0
+            first (the ``torch.linspace`` vectors ``Cpab.uniform_meshgrid`` takes the
+            Cartesian product of): the kernels look a pixel's start point up
+            there instead of reading a meshgrid
         outsize: list of ndim output sizes
     Returns:
         [n_batch, n_channels, *outsize]
     """
-    assert data.is_cuda and theta.is_cuda and grid.is_cuda, "Only GPU tensors supported"
+    assert data.is_cuda and theta.is_cuda and axes.is_cuda, "Only GPU tensors supported"
     assert params.ndim in (1, 2, 3), "GPU transformer supports 1D, 2D, and 3D"
-    return _CPABImageFunction.apply(data, theta, grid, [int(v) for v in outsize], params)
+    return _CPABImageFunction.apply(data, theta, axes, [int(v) for v in outsize], params)
 
 
 class _CPABImageFunction(torch.autograd.Function):
     """Fused transform_data: integrate the meshgrid and resample in one pass."""
 
     @staticmethod
-    def forward(ctx, data, theta, grid, outsize, params):
+    def forward(ctx, data, theta, axes, outsize, params):
         ndim, nC = params.ndim, int(params.nC)
         if data.dtype != torch.float32 or theta.dtype != torch.float32:
             raise RuntimeError("expected float32 data and theta")
@@ -294,14 +297,14 @@ class _CPABImageFunction(torch.autograd.Function):
         nP = 1
         for v in outsize:
             nP *= v
-        if len(outsize) != ndim or tuple(grid.shape) != (ndim, nP):
-            raise RuntimeError("grid must be the [ndim, prod(outsize)] meshgrid of outsize")
+        if len(outsize) != ndim or tuple(axes.shape) != (sum(outsize),):
+            raise RuntimeError("axes must be the [sum(outsize)] per-axis coordinates of the grid")
         lib = native()
         dev = theta.device
         n = theta.shape[0]
         tab = basis_tables(params, dev)
         data_c = data.detach().contiguous()
-        grid_c = grid.detach().contiguous()
+        axes_c = axes.detach().contiguous()
         As = torch.empty((n, nC, ndim, ndim + 1), device=dev, dtype=torch.float32)
         theta_c = theta.detach().contiguous()
         T = int(params.nstepsolver)
@@ -318,20 +321,20 @@ class _CPABImageFunction(torch.autograd.Function):
         final = (torch.empty((n, ndim, nP), device=dev, dtype=torch.float32)
                  if grad_wanted else None)
         out = torch.empty((n, data.shape[1], *outsize), device=dev, dtype=torch.float32)
-        lib.transform_data_forward(ndim, data_c, grid_c, outsize, T, nc, adaptive, Trels, As, out,
+        lib.transform_data_forward(ndim, data_c, axes_c, outsize, T, nc, adaptive, Trels, As, out,
                                    final)
         ctx.outsize = list(outsize)
         ctx.T = T
         ctx.nc = nc
         ctx.adaptive = adaptive
         ctx.params = params
-        ctx.save_for_backward(data_c, grid_c, final, As)
+        ctx.save_for_backward(data_c, axes_c, final, As)
         return out
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, grad):
-        data, grid, final, As = ctx.saved_tensors
+        data, axes, final, As = ctx.saved_tensors
         params = ctx.params
         lib = native()
         dev = As.device
@@ -341,7 +344,7 @@ class _CPABImageFunction(torch.autograd.Function):
         ws_bytes = lib.transform_data_backward_workspace_size(ndim, n, ctx.outsize, nC)
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
         grad_data = torch.empty_like(data) if ctx.needs_input_grad[0] else None
-        lib.transform_data_backward(ndim, data, grid, ctx.outsize, ctx.T, ctx.nc, ctx.adaptive,
+        lib.transform_data_backward(ndim, data, axes, ctx.outsize, ctx.T, ctx.nc, ctx.adaptive,
                                     final, As, grad, moments, grad_data, ws)
         grad_theta = None
         if ctx.needs_input_grad[1]:

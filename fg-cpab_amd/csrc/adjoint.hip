@@ -338,28 +338,37 @@ struct PlainIO {
 };
 
 //
-// Trajectory order: 1D/2D walk the points in image order (the seed reads are
-// coalesced, the meshgrid reads strided but L2-resident).  3D walks them in
-// meshgrid order instead: a workgroup's contiguous range is then a slab of
-// whole x-y planes, whose cells have nearly consecutive ids, which is what the
-// direct-mapped LDS cell cache needs (in image order a range spans every z
-// layer and the cache would thrash); the seed reads become the strided ones.
+// Trajectory order: 1D/2D walk the points in image order (the seed and
+// gradient reads are coalesced).  3D walks them in meshgrid order instead:
+// lanes then run along coordinate 0, which keeps a wave's cells few and
+// measured twice as fast as image order (lanes along the last axis) in the
+// 3D backward; the seed reads become strided.  Start points come from the
+// per-axis coordinate vectors either way.
 template <int D>
 struct ImageIO {
   static constexpr bool kMeshOrder = D == 3;
   ImageShape s;
-  const float* __restrict__ grid;   // [D, nP] meshgrid (shared by all thetas)
+  const float* __restrict__ axes;   // per-axis coordinates of the uniform grid (shared by all thetas)
   const float* __restrict__ fin;    // [D, nP] integrated points of this theta, image order
   const float* __restrict__ gout;   // [C, nP] image gradient of this theta
   const float* __restrict__ data;   // [C, plane_in]
   float* __restrict__ gdata;        // [C, plane_in] or null
   __device__ __forceinline__ void start(int i, float (&p)[D]) const {
-    const int m = kMeshOrder ? i : mesh_point<D>(s, i);
+    int ix[3];
+    if (kMeshOrder) mesh_index<D>(s, i, ix);
+    else image_index<D>(s, i, ix);
+    float x[3];
+    grid_point<D>(s, axes, ix, x);
 #pragma unroll
-    for (int k = 0; k < D; ++k) p[k] = grid[m + (size_t)k * s.nP];
+    for (int k = 0; k < D; ++k) p[k] = x[k];
   }
   __device__ __forceinline__ void seed(int i, bool valid, float (&lam)[D]) const {
-    const int q = kMeshOrder ? image_point<D>(s, i) : i;
+    int q = i;
+    if (kMeshOrder) {
+      int ix[3];
+      mesh_index<D>(s, i, ix);
+      q = image_pos<D>(s, ix);
+    }
     const Axis ax = axis_of(fin[q], s.in[0]);
     const Axis ay = D >= 2 ? axis_of(fin[q + (size_t)s.nP], s.in[1]) : Axis{0, 0, 0.0f};
     const Axis az = D == 3 ? axis_of(fin[q + 2 * (size_t)s.nP], s.in[2]) : Axis{0, 0, 0.0f};
@@ -736,7 +745,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kerne
 // range of output positions.
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward_kernel(
-    ImageShape s, int T, Cells g, int nC, const float* __restrict__ grid,
+    ImageShape s, int T, Cells g, int nC, const float* __restrict__ axes,
     const float* __restrict__ final_points, const float* __restrict__ As,
     const float* __restrict__ Gs, const float* __restrict__ data, const float* __restrict__ grad_out,
     float* __restrict__ moments, float* __restrict__ partials, uint64_t* __restrict__ dense_parts,
@@ -750,7 +759,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
   const float* __restrict__ Gg = Gs + (size_t)b * nC * RevStride<D>::S;
   ImageIO<D> io;
   io.s = s;
-  io.grid = grid;
+  io.axes = axes;
   io.fin = final_points + (size_t)b * D * s.nP;
   io.gout = grad_out + (size_t)b * s.C * s.nP;
   io.data = data + (size_t)b * s.C * s.plane_in;
@@ -788,7 +797,7 @@ struct BackwardJob {
   float *moments, *partials, *lam, *grad_points;
   uint64_t* dense_parts;
   const ImageShape* image;
-  const float *grid, *final_points, *data;
+  const float *axes, *final_points, *data;
   float* grad_data;
 };
 
@@ -801,7 +810,7 @@ hipError_t go(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
     auto kernel = image_backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
     hipError_t e = allow_lds(kernel, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kernel, grid, block, lds, s, *j.image, j.T, g, j.geo.nC, j.grid,
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, *j.image, j.T, g, j.geo.nC, j.axes,
                        j.final_points, j.As, j.G, j.data, j.grad_out, j.moments, j.partials,
                        j.dense_parts, j.grad_data);
   } else {
@@ -892,7 +901,7 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
 }
 
 hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
-                                 int adaptive, const float* grid, const float* final_points,
+                                 int adaptive, const float* axes, const float* final_points,
                                  const float* As, const float* G, const float* data,
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
@@ -910,7 +919,7 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
   j.partials = partials;
   j.dense_parts = dense_parts;
   j.image = &img;
-  j.grid = grid;
+  j.axes = axes;
   j.final_points = final_points;
   j.data = data;
   j.grad_data = grad_data;

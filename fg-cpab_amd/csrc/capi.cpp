@@ -387,6 +387,7 @@ int image_shape(int ndim, int64_t n_batch, int64_t C, const int64_t* in_size,
   for (int k = 0; k < 3; ++k) {
     img->o[k] = k < ndim ? (int)out_size[k] : 1;
     img->in[k] = k < ndim ? (int)in_size[k] : 1;
+    img->inv_o[k] = 1.0 / (double)img->o[k];
   }
   img->C = (int)C;
   img->nP = (int)nP;
@@ -400,7 +401,9 @@ extern "C" {
 
 const char* cpab_last_error_string(void) { return g_last_error.c_str(); }
 
-int cpab_abi_version(void) { return 100; }
+// 200: the fused transform_data entry points take the uniform grid's per-axis
+// coordinates instead of the meshgrid.
+int cpab_abi_version(void) { return 200; }
 
 int cpab_affine(int ndim, int64_t n_theta, int nC, int d, const float* theta,
                 const int32_t* row_ptr, const int32_t* col_idx, const float* vals, float* As,
@@ -510,7 +513,7 @@ int cpab_chain_backward(int ndim, int64_t nP, int64_t n_batch, int batched, int 
 
 int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
                                 const int64_t* in_size, const int64_t* out_size, int nstepsolver,
-                                int ncx, int ncy, int ncz, int adaptive, const float* grid,
+                                int ncx, int ncy, int ncz, int adaptive, const float* axes,
                                 const float* Trels, const float* As, const float* data,
                                 float* out, float* final_points, void* stream) {
   cpab::Geometry g{};
@@ -521,14 +524,14 @@ int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
   cpab::ImageShape img;
   if ((rc = image_shape(ndim, n_batch, n_channels, in_size, out_size, &img))) return rc;
   if (n_batch == 0) return CPAB_OK;
-  CPAB_REQUIRE(grid); CPAB_REQUIRE(As); CPAB_REQUIRE(data); CPAB_REQUIRE(out);
+  CPAB_REQUIRE(axes); CPAB_REQUIRE(As); CPAB_REQUIRE(data); CPAB_REQUIRE(out);
   if (ndim > 1) CPAB_REQUIRE(Trels);
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(Trels, 16);
   hipStream_t s = as_stream(stream);
   const cpab::LaunchCfg cfg = forward_cfg(g, img.nP, n_batch);
   hipEvent_t ev;
   const bool timed = prof_begin(s, &ev);
-  rc = check_hip(cpab::launch_image_forward(g, img, n_batch, nstepsolver, adaptive, grid, Trels,
+  rc = check_hip(cpab::launch_image_forward(g, img, n_batch, nstepsolver, adaptive, axes, Trels,
                                             As, data, out, final_points, cfg, s),
                  "cpab_transform_data_forward");
   prof_end(timed, ev, "image_forward", s);
@@ -545,7 +548,7 @@ int64_t cpab_transform_data_backward_workspace_size(int ndim, int64_t n_batch,
 
 int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
                                  const int64_t* in_size, const int64_t* out_size, int nstepsolver,
-                                 int ncx, int ncy, int ncz, int adaptive, const float* grid,
+                                 int ncx, int ncy, int ncz, int adaptive, const float* axes,
                                  const float* final_points, const float* As, const float* data,
                                  const float* grad_out, float* moments, float* grad_data,
                                  void* workspace, int64_t workspace_bytes, void* stream) {
@@ -557,7 +560,7 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   cpab::ImageShape img;
   if ((rc = image_shape(ndim, n_batch, n_channels, in_size, out_size, &img))) return rc;
   if (n_batch == 0) return CPAB_OK;
-  CPAB_REQUIRE(grid); CPAB_REQUIRE(final_points); CPAB_REQUIRE(As); CPAB_REQUIRE(data);
+  CPAB_REQUIRE(axes); CPAB_REQUIRE(final_points); CPAB_REQUIRE(As); CPAB_REQUIRE(data);
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(workspace, 16);
   CPAB_REQUIRE(grad_out); CPAB_REQUIRE(moments);
   hipStream_t s = as_stream(stream);
@@ -581,7 +584,7 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   }
   hipEvent_t ev;
   const bool timed = prof_begin(s, &ev);
-  rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, grid,
+  rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, axes,
                                              final_points, As, G, data, grad_out, moments,
                                              partials, dense, grad_data, cfg, s),
                  "cpab_transform_data_backward");

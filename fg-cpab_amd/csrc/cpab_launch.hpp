@@ -85,11 +85,11 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
 
 // Fused transform_data (image-ordered outputs; see cpab_sample.hpp ImageShape).
 hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
-                                int adaptive, const float* grid, const float* Trels,
+                                int adaptive, const float* axes, const float* Trels,
                                 const float* As, const float* data, float* out,
                                 float* final_points, const LaunchCfg& cfg, hipStream_t s);
 hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
-                                 int adaptive, const float* grid, const float* final_points,
+                                 int adaptive, const float* axes, const float* final_points,
                                  const float* As, const float* G, const float* data,
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,

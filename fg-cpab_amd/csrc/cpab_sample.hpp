@@ -151,44 +151,68 @@ __device__ __forceinline__ void sample_grad(const int* in, const float* __restri
 namespace cpab {
 
 // Output-ordered image geometry of the fused transform_data kernels.  Output
-// position q runs over [o0, o1(, o2)] with the LAST axis fastest (the image
-// layout); the meshgrid point it samples is p = i0 + o0*(i1 + o1*i2), the
-// coordinate-0-fastest order of Cpab.uniform_meshgrid (cpab/cpab.py:131-144).
+// position q = (i0*o1 + i1)*o2 + i2 runs over [o0, o1(, o2)] with the LAST axis
+// fastest (the image layout); it integrates the uniform-grid point
+// (axes_0[i0], axes_1[i1], axes_2[i2]).  Cpab.uniform_meshgrid
+// (cpab/cpab.py:131-144) is the Cartesian product of those per-axis
+// coordinates, listed with coordinate 0 fastest (m = i0 + o0*(i1 + o1*i2));
+// the kernels read the per-axis vectors, a few KB that stay in cache, instead
+// of the meshgrid.
 struct ImageShape {
   int o[3];          // output (= meshgrid) sizes, unused axes 1
   int in[3];         // data spatial sizes, unused axes 1
   int C;             // channels
   int nP;            // prod(o)
   int64_t plane_in;  // prod(in)
+  double inv_o[3];   // 1.0 / o[k]
 };
 
-// Image position of meshgrid point p (inverse of mesh_point).
-template <int ND>
-__device__ __forceinline__ int image_point(const ImageShape& s, int p) {
-  if (ND == 1) return p;
-  if (ND == 2) {
-    const int i1 = p / s.o[0];
-    return (p - i1 * s.o[0]) * s.o[1] + i1;
-  }
-  const int r = p / s.o[0];
-  const int i0 = p - r * s.o[0];
-  const int i2 = r / s.o[1];
-  const int i1 = r - i2 * s.o[1];
-  return (i0 * s.o[1] + i1) * s.o[2] + i2;
+// q / d for 0 <= q < 2^31 and 1 <= d < 2^31 without the ~40-instruction
+// integer division: the double product q * (1/d) is within one of the
+// quotient (relative error ~2^-52 on a value below 2^31), and the remainder
+// fixes the last unit.  Sets r = q - (q / d) * d.
+__device__ __forceinline__ int div_index(int q, int d, double inv_d, int& r) {
+  int e = (int)((double)q * inv_d);
+  r = q - e * d;
+  if (r < 0) { e -= 1; r += d; }
+  else if (r >= d) { e += 1; r -= d; }
+  return e;
 }
 
+// Grid indices of image position q.
 template <int ND>
-__device__ __forceinline__ int mesh_point(const ImageShape& s, int q) {
-  if (ND == 1) return q;
-  if (ND == 2) {
-    const int i0 = q / s.o[1];
-    return i0 + s.o[0] * (q - i0 * s.o[1]);
-  }
-  const int r = q / s.o[2];
-  const int i2 = q - r * s.o[2];
-  const int i0 = r / s.o[1];
-  const int i1 = r - i0 * s.o[1];
-  return i0 + s.o[0] * (i1 + s.o[1] * i2);
+__device__ __forceinline__ void image_index(const ImageShape& s, int q, int (&i)[3]) {
+  if (ND == 1) { i[0] = q; i[1] = i[2] = 0; return; }
+  if (ND == 2) { i[0] = div_index(q, s.o[1], s.inv_o[1], i[1]); i[2] = 0; return; }
+  const int r = div_index(q, s.o[2], s.inv_o[2], i[2]);
+  i[0] = div_index(r, s.o[1], s.inv_o[1], i[1]);
+}
+
+// Grid indices of meshgrid position m (coordinate 0 fastest).
+template <int ND>
+__device__ __forceinline__ void mesh_index(const ImageShape& s, int m, int (&i)[3]) {
+  if (ND == 1) { i[0] = m; i[1] = i[2] = 0; return; }
+  const int r = div_index(m, s.o[0], s.inv_o[0], i[0]);
+  if (ND == 2) { i[1] = r; i[2] = 0; return; }
+  i[2] = div_index(r, s.o[1], s.inv_o[1], i[1]);
+}
+
+// Image position of grid indices i.
+template <int ND>
+__device__ __forceinline__ int image_pos(const ImageShape& s, const int (&i)[3]) {
+  if (ND == 1) return i[0];
+  if (ND == 2) return i[0] * s.o[1] + i[1];
+  return (i[0] * s.o[1] + i[1]) * s.o[2] + i[2];
+}
+
+// The uniform-grid point with indices i: coordinate k from the k-th per-axis
+// vector of `axes` (the vectors concatenated, axis 0 first).
+template <int ND>
+__device__ __forceinline__ void grid_point(const ImageShape& s, const float* __restrict__ axes,
+                                           const int (&i)[3], float (&x)[3]) {
+  x[0] = axes[i[0]];
+  x[1] = ND >= 2 ? axes[s.o[0] + i[1]] : 0.0f;
+  x[2] = ND == 3 ? axes[s.o[0] + s.o[1] + i[2]] : 0.0f;
 }
 
 }  // namespace cpab

@@ -349,12 +349,12 @@ __global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T,
 // (image order, last axis fastest) integrates its meshgrid point under theta b
 // exactly as cpab_forward / the 1D closed form does, then samples every
 // channel of data there exactly as cpab_interp_forward does.  Lanes run along
-// the image's fast axis, so the image stores (and final_points, kept in the
-// same order for the backward) are coalesced; the meshgrid reads are strided
-// but hit L2 (the grid is shared by all thetas).
+// the image's fast axis, so the image stores and final_points (kept in the
+// same order for the backward) are coalesced; the start points come from the
+// grid's per-axis coordinate vectors.
 template <int ND, bool ADAPTIVE>
 __global__ __launch_bounds__(1024) void image_forward_kernel(
-    ImageShape s, int T, int nx, int ny, int nz, const float* __restrict__ grid,
+    ImageShape s, int T, int nx, int ny, int nz, const float* __restrict__ axes,
     const float* __restrict__ Trels, const float* __restrict__ As,
     const float* __restrict__ data, float* __restrict__ out, float* __restrict__ final_points) {
   const int b = blockIdx.y;
@@ -367,11 +367,10 @@ __global__ __launch_bounds__(1024) void image_forward_kernel(
   float* __restrict__ o = out + (size_t)b * s.C * s.nP;
   float* __restrict__ fin = final_points ? final_points + (size_t)b * ND * s.nP : nullptr;
   for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < s.nP; q += gridDim.x * blockDim.x) {
-    const int m = mesh_point<ND>(s, q);
+    int ix[3];
+    image_index<ND>(s, q, ix);
     float x[3];
-    x[0] = grid[m];
-    x[1] = ND >= 2 ? grid[m + (size_t)s.nP] : 0.0f;
-    x[2] = ND == 3 ? grid[m + 2 * (size_t)s.nP] : 0.0f;
+    grid_point<ND>(s, axes, ix, x);
     if (ND == 1) {
       x[0] = closed_form_1d(x[0], 1.0f, Ag, nx);
     } else if (ND == 2) {
@@ -540,7 +539,7 @@ hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_batch, int ba
 }
 
 hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
-                                int adaptive, const float* grid, const float* Trels,
+                                int adaptive, const float* axes, const float* Trels,
                                 const float* As, const float* data, float* out,
                                 float* final_points, const LaunchCfg& cfg, hipStream_t s) {
   if (img.nP <= 0 || n_batch <= 0) return hipSuccess;
@@ -549,7 +548,7 @@ hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_
                     (unsigned)n_batch);
   const dim3 threads((unsigned)cfg.block);
   auto go = [&](auto kernel) -> hipError_t {
-    hipLaunchKernelGGL(kernel, blocks, threads, 0, s, img, T, g.nx, g.ny, g.nz, grid, Trels, As,
+    hipLaunchKernelGGL(kernel, blocks, threads, 0, s, img, T, g.nx, g.ny, g.nz, axes, Trels, As,
                        data, out, final_points);
     return hipGetLastError();
   };

@@ -157,8 +157,10 @@ int cpab_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, voi
 
 /* Fused Cpab.transform_data forward (cpab/cpab.py:295-309: uniform_meshgrid ->
  * transform_grid -> interpolate, i.e. cpab_forward followed by
- * cpab_interp_forward).  grid: the meshgrid [ndim, prod(out_size)], coordinate 0
- * fastest (uniform_meshgrid's layout), shared by all n_batch thetas; Trels / As
+ * cpab_interp_forward).  axes: the uniform grid's coordinates per axis,
+ * concatenated (out_size[0] values of coordinate 0, then out_size[1] of
+ * coordinate 1, ...), whose Cartesian product is uniform_meshgrid(out_size),
+ * shared by all n_batch thetas; Trels / As
  * [n_batch, nC, ndim, ndim+1] (Trels unused in 1D, may be NULL); data
  * [n_batch, C, *in_size]; out [n_batch, C, *out_size].  Each output pixel
  * integrates its meshgrid point with cpab_forward's arithmetic and samples
@@ -169,7 +171,7 @@ int cpab_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, voi
  * the reference, whose transform_data is three separate steps. */
 int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
                                 const int64_t* in_size, const int64_t* out_size, int nstepsolver,
-                                int ncx, int ncy, int ncz, int adaptive, const float* grid,
+                                int ncx, int ncy, int ncz, int adaptive, const float* axes,
                                 const float* Trels, const float* As, const float* data,
                                 float* out, float* final_points, void* stream);
 
@@ -183,10 +185,11 @@ int64_t cpab_transform_data_backward_workspace_size(int ndim, int64_t n_batch,
  * does through interpolate's backward and cpab_gpu.backward_moments_and_points
  * (transformer_cuda.cpp:122-153).  moments [n_batch, nC, ndim*(ndim+1)]
  * (overwritten); grad_data [n_batch, C, *in_size] (may be NULL; overwritten).
- * grad_out is the image gradient [n_batch, C, *out_size]. */
+ * grad_out is the image gradient [n_batch, C, *out_size]; axes as for the
+ * forward. */
 int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
                                  const int64_t* in_size, const int64_t* out_size, int nstepsolver,
-                                 int ncx, int ncy, int ncz, int adaptive, const float* grid,
+                                 int ncx, int ncy, int ncz, int adaptive, const float* axes,
                                  const float* final_points, const float* As, const float* data,
                                  const float* grad_out, float* moments, float* grad_data,
                                  void* workspace, int64_t workspace_bytes, void* stream);

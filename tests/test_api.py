@@ -99,7 +99,7 @@ def test_fused_paths_reject_cpu_tensors():
         CPAB_chain_transformer(torch.zeros(2, 10), torch.zeros(2, 1, T.params.d), T.params)
     with pytest.raises(AssertionError, match="Only GPU tensors supported"):
         CPAB_transform_data(torch.zeros(1, 1, 4, 4), torch.zeros(1, T.params.d),
-                            torch.zeros(2, 16), [4, 4], T.params)
+                            torch.zeros(8), [4, 4], T.params)
 
 
 def test_transform_data_checks_before_device_work():
@@ -109,13 +109,13 @@ def test_transform_data_checks_before_device_work():
     T = Cpab([3, 3])
     with pytest.raises(RuntimeError, match="theta must be"):
         tr._CPABImageFunction.forward(_Ctx(), torch.zeros(2, 1, 4, 4), torch.zeros(3, T.params.d),
-                                      torch.zeros(2, 16), [4, 4], T.params)
-    with pytest.raises(RuntimeError, match="meshgrid of outsize"):
+                                      torch.zeros(8), [4, 4], T.params)
+    with pytest.raises(RuntimeError, match="per-axis coordinates"):
         tr._CPABImageFunction.forward(_Ctx(), torch.zeros(2, 1, 4, 4), torch.zeros(2, T.params.d),
-                                      torch.zeros(2, 15), [4, 4], T.params)
+                                      torch.zeros(2, 16), [4, 4], T.params)
     with pytest.raises(RuntimeError, match="float32"):
         tr._CPABImageFunction.forward(_Ctx(), torch.zeros(2, 1, 4, 4, dtype=torch.float64),
-                                      torch.zeros(2, T.params.d), torch.zeros(2, 16), [4, 4],
+                                      torch.zeros(2, T.params.d), torch.zeros(8), [4, 4],
                                       T.params)
 
 

@@ -476,13 +476,21 @@ def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive):
     data = rng.random((B, C, *ins)).astype(np.float32)
     grid = T.uniform_meshgrid(list(outs))
     grid_np = grid.cpu().numpy()
+    # the fused entry points take the grid's per-axis coordinates; their
+    # Cartesian product (coordinate 0 fastest) is the meshgrid
+    axes = T._uniform_axes(list(outs))
+    ax_np = axes.cpu().numpy()
+    offs = np.cumsum([0] + list(outs))
+    for k in range(nd):
+        ik = (np.arange(int(np.prod(outs))) // int(np.prod(outs[:k]))) % outs[k]
+        np.testing.assert_array_equal(ax_np[offs[k] + ik], grid_np[k])
     As = _As_gpu(T, theta, cuda)
     Tr = torch.empty_like(As)
     native().expm(nd, As, 1.0 / 50, Tr)
     out = torch.empty((B, C, *outs), device=cuda)
     nP = int(np.prod(outs))
     fin = torch.empty((B, nd, nP), device=cuda)
-    native().transform_data_forward(nd, _dev(data, cuda), grid, list(outs), 50, p.nc, adaptive,
+    native().transform_data_forward(nd, _dev(data, cuda), axes, list(outs), 50, p.nc, adaptive,
                                     Tr, As, out, fin)
     A = As.cpu().numpy()
     if nd == 1:
@@ -497,7 +505,7 @@ def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive):
     gd = torch.empty((B, C, *ins), device=cuda)
     nbytes = native().transform_data_backward_workspace_size(nd, B, list(outs), p.nC)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=cuda) if nbytes else None
-    native().transform_data_backward(nd, _dev(data, cuda), grid, list(outs), 50, p.nc, adaptive,
+    native().transform_data_backward(nd, _dev(data, cuda), axes, list(outs), 50, p.nc, adaptive,
                                      fin, As, _dev(gout, cuda), mom, gd, ws)
     rg, rd = orc.interp_backward(nd, data, xT, outs, gout)
     ref_m, _ = orc.backward(grid_np, A, rg, p.nc, 50, adaptive=bool(adaptive))
