@@ -3,7 +3,7 @@
 Default (the driver's line) = BASELINE.json configs[1], "C2": 2D tessellation
 [20, 20] on [0,1]^2, zero_boundary=True, fp32, batch 16, 125,000 points uniform
 in [0,1]^2 (seed 21); theta ~ N(0,1) * 0.5 in basis coordinates (seed 22);
-loss = MSE against a second seeded theta's (seed 23) warped points.  One step =
+loss = MSE (torch.nn.functional.mse_loss, mean) against a second seeded theta's (seed 23) warped points.  One step =
 Cpab.transform_grid forward + MSE + backward w.r.t. theta, inputs resident in
 HBM (A = B theta, expm, fixed-step forward kernel, fused replay/adjoint kernel,
 projection).  --config c1|c3|c4|c5|all measures the other BASELINE.json
@@ -122,7 +122,7 @@ def setup(cfg, nstep, dev):
         def step():
             th = th0.detach().requires_grad_(True)
             out = T.transform_grid(x, th)
-            torch.mean((out - target) ** 2).backward()
+            torch.nn.functional.mse_loss(out, target).backward()
             return th.grad
 
         traj = pts.shape[1] * theta.shape[0]
@@ -148,7 +148,7 @@ def setup(cfg, nstep, dev):
         def step():
             th = th0.detach().requires_grad_(True)
             out = T.transform_data(data, th, size)
-            torch.mean((out - target) ** 2).backward()
+            torch.nn.functional.mse_loss(out, target).backward()
             return th.grad
 
         # The resampling alone (Cpab.interpolate at the warped grid of this
@@ -190,7 +190,7 @@ def setup(cfg, nstep, dev):
     def step():
         ch = chain0.detach().requires_grad_(True)
         out = T.transform_grid_chain(grid, ch, scale_by_dt=True)
-        torch.mean((out - target) ** 2).backward()
+        torch.nn.functional.mse_loss(out, target).backward()
         return ch.grad
 
     nP = 512 * 512
