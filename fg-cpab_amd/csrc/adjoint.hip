@@ -353,20 +353,24 @@ struct ImageIO {
   const float* __restrict__ gout;   // [C, nP] image gradient of this theta
   const float* __restrict__ data;   // [C, plane_in]
   float* __restrict__ gdata;        // [C, plane_in] or null
+  __device__ __forceinline__ void walk_index(int i, int (&ix)[3]) const {
+    if (D >= 2 && s.walk_tiles) tile_index<D>(s, i, ix);
+    else if (kMeshOrder) mesh_index<D>(s, i, ix);
+    else image_index<D>(s, i, ix);
+  }
   __device__ __forceinline__ void start(int i, float (&p)[D]) const {
     int ix[3];
-    if (kMeshOrder) mesh_index<D>(s, i, ix);
-    else image_index<D>(s, i, ix);
+    walk_index(i, ix);
     float x[3];
     grid_point<D>(s, axes, ix, x);
 #pragma unroll
     for (int k = 0; k < D; ++k) p[k] = x[k];
   }
   __device__ __forceinline__ void seed(int i, bool valid, float (&lam)[D]) const {
-    int q = i;
-    if (kMeshOrder) {
+    int q = i;  // image position of walk position i
+    if (kMeshOrder || (D >= 2 && s.walk_tiles)) {
       int ix[3];
-      mesh_index<D>(s, i, ix);
+      walk_index(i, ix);
       q = image_pos<D>(s, ix);
     }
     const Axis ax = axis_of(fin[q], s.in[0]);

@@ -165,6 +165,7 @@ struct ImageShape {
   int nP;            // prod(o)
   int64_t plane_in;  // prod(in)
   double inv_o[3];   // 1.0 / o[k]
+  int walk_tiles;    // the fused kernels walk 16 x 4 tiles (tile_index)
 };
 
 // q / d for 0 <= q < 2^31 and 1 <= d < 2^31 without the ~40-instruction
@@ -186,6 +187,33 @@ __device__ __forceinline__ void image_index(const ImageShape& s, int q, int (&i)
   if (ND == 2) { i[0] = div_index(q, s.o[1], s.inv_o[1], i[1]); i[2] = 0; return; }
   const int r = div_index(q, s.o[2], s.inv_o[2], i[2]);
   i[0] = div_index(r, s.o[1], s.inv_o[1], i[1]);
+}
+
+// Grid indices of position m in the tiled walk of the fused kernels: each run
+// of 64 positions (one wave) is a tile of 16 along the last axis by 4 along
+// the axis before it, which keeps a wave's trajectories in few cells and its
+// image reads and writes in 64-byte runs.  Consecutive tiles step
+// 2D: the i0 block, then the i1 block (1024 positions = 64 x 16, i0 x i1);
+// 3D: i0, then the i1 block, then the i2 block (1024 = 16 x 4 x 16).
+// Needs o[ND-1] % 16 == 0 and o[ND-2] % 4 == 0 (then the tiles cover the grid
+// exactly once).  1 / (o / 4) == 4 * (1 / o) exactly: scaling by 4 commutes
+// with rounding.
+template <int ND>
+__device__ __forceinline__ void tile_index(const ImageShape& s, int m, int (&i)[3]) {
+  const int l = m & 63;
+  int r0, r1;
+  if (ND == 2) {
+    const int b1 = div_index(m >> 6, s.o[0] >> 2, 4.0 * s.inv_o[0], r0);
+    i[0] = (r0 << 2) + (l >> 4);
+    i[1] = (b1 << 4) + (l & 15);
+    i[2] = 0;
+    return;
+  }
+  const int rest = div_index(m >> 6, s.o[0], s.inv_o[0], r0);
+  const int b2 = div_index(rest, s.o[1] >> 2, 4.0 * s.inv_o[1], r1);
+  i[0] = r0;
+  i[1] = (r1 << 2) + (l >> 4);
+  i[2] = (b2 << 4) + (l & 15);
 }
 
 // Grid indices of meshgrid position m (coordinate 0 fastest).

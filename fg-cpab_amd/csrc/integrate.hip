@@ -366,9 +366,14 @@ __global__ __launch_bounds__(1024) void image_forward_kernel(
   const float* __restrict__ dat = data + (size_t)b * s.C * s.plane_in;
   float* __restrict__ o = out + (size_t)b * s.C * s.nP;
   float* __restrict__ fin = final_points ? final_points + (size_t)b * ND * s.nP : nullptr;
-  for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < s.nP; q += gridDim.x * blockDim.x) {
-    int ix[3];
-    image_index<ND>(s, q, ix);
+  for (int m = blockIdx.x * blockDim.x + threadIdx.x; m < s.nP; m += gridDim.x * blockDim.x) {
+    int ix[3], q = m;
+    if (ND >= 2 && s.walk_tiles) {
+      tile_index<ND>(s, m, ix);
+      q = image_pos<ND>(s, ix);
+    } else {
+      image_index<ND>(s, m, ix);
+    }
     float x[3];
     grid_point<ND>(s, axes, ix, x);
     if (ND == 1) {

@@ -461,7 +461,12 @@ def _image_order(x, outs):
 @pytest.mark.parametrize("tess,ins,outs,adaptive", [([10], (50,), (70,), 0),
                                                     ([6, 5], (40, 48), (36, 44), 0),
                                                     ([6, 5], (40, 48), (36, 44), 1),
-                                                    ([3, 3, 3], (10, 12, 9), (11, 9, 13), 0)])
+                                                    ([3, 3, 3], (10, 12, 9), (11, 9, 13), 0),
+                                                    # last axis % 16 == 0 and the one before % 4 == 0:
+                                                    # the tiled walk
+                                                    ([6, 5], (40, 48), (36, 48), 0),
+                                                    ([6, 5], (40, 48), (20, 32), 1),
+                                                    ([3, 3, 3], (10, 12, 9), (6, 8, 32), 0)])
 def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive):
     # cpab_transform_data_forward / _backward against the unfused composition
     # the reference runs (transform_grid of the meshgrid, interpolate, and the
