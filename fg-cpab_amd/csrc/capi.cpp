@@ -389,7 +389,7 @@ int image_shape(int ndim, int64_t n_batch, int64_t C, const int64_t* in_size,
     img->in[k] = k < ndim ? (int)in_size[k] : 1;
     img->inv_o[k] = 1.0 / (double)img->o[k];
   }
-  img->walk_tiles = ndim >= 2 && img->o[ndim - 1] % 16 == 0 && img->o[ndim - 2] % 4 == 0;
+  img->walk_tiles = ndim >= 2 && img->o[ndim - 1] % cpab::kWalkW == 0 && img->o[ndim - 2] % cpab::kWalkH == 0;
   img->C = (int)C;
   img->nP = (int)nP;
   img->plane_in = plane;

@@ -189,31 +189,35 @@ __device__ __forceinline__ void image_index(const ImageShape& s, int q, int (&i)
   i[0] = div_index(r, s.o[1], s.inv_o[1], i[1]);
 }
 
-// Grid indices of position m in the tiled walk of the fused kernels: each run
-// of 64 positions (one wave) is a tile of 16 along the last axis by 4 along
-// the axis before it, which keeps a wave's trajectories in few cells and its
-// image reads and writes in 64-byte runs.  Consecutive tiles step
+// Tiled walk of the fused kernels: each run of 64 positions (one wave) is a
+// tile of kWalkW along the last axis by kWalkH along the axis before it, which
+// keeps a wave's trajectories in few cells and its image reads and writes in
+// kWalkW-float runs.  Consecutive tiles step
 // 2D: the i0 block, then the i1 block (1024 positions = 64 x 16, i0 x i1);
 // 3D: i0, then the i1 block, then the i2 block (1024 = 16 x 4 x 16).
-// Needs o[ND-1] % 16 == 0 and o[ND-2] % 4 == 0 (then the tiles cover the grid
-// exactly once).  1 / (o / 4) == 4 * (1 / o) exactly: scaling by 4 commutes
-// with rounding.
+// Needs o[ND-1] % kWalkW == 0 and o[ND-2] % kWalkH == 0 (then the tiles cover
+// the grid exactly once).  1 / (o / kWalkH) == kWalkH * (1 / o) exactly:
+// scaling by a power of two commutes with rounding.
+constexpr int kWalkW = 16;
+constexpr int kWalkH = 64 / kWalkW;
+static_assert(kWalkW * kWalkH == 64 && (kWalkW & (kWalkW - 1)) == 0, "walk tile");
+
 template <int ND>
 __device__ __forceinline__ void tile_index(const ImageShape& s, int m, int (&i)[3]) {
   const int l = m & 63;
   int r0, r1;
   if (ND == 2) {
-    const int b1 = div_index(m >> 6, s.o[0] >> 2, 4.0 * s.inv_o[0], r0);
-    i[0] = (r0 << 2) + (l >> 4);
-    i[1] = (b1 << 4) + (l & 15);
+    const int b1 = div_index(m >> 6, s.o[0] / kWalkH, kWalkH * s.inv_o[0], r0);
+    i[0] = r0 * kWalkH + l / kWalkW;
+    i[1] = b1 * kWalkW + l % kWalkW;
     i[2] = 0;
     return;
   }
   const int rest = div_index(m >> 6, s.o[0], s.inv_o[0], r0);
-  const int b2 = div_index(rest, s.o[1] >> 2, 4.0 * s.inv_o[1], r1);
+  const int b2 = div_index(rest, s.o[1] / kWalkH, kWalkH * s.inv_o[1], r1);
   i[0] = r0;
-  i[1] = (r1 << 2) + (l >> 4);
-  i[2] = (b2 << 4) + (l & 15);
+  i[1] = r1 * kWalkH + l / kWalkW;
+  i[2] = b2 * kWalkW + l % kWalkW;
 }
 
 // Grid indices of meshgrid position m (coordinate 0 fastest).
