@@ -338,12 +338,12 @@ struct PlainIO {
 };
 
 //
-// Trajectory order: 1D/2D walk the points in image order (the seed and
-// gradient reads are coalesced).  3D walks them in meshgrid order instead:
-// lanes then run along coordinate 0, which keeps a wave's cells few and
-// measured twice as fast as image order (lanes along the last axis) in the
-// 3D backward; the seed reads become strided.  Start points come from the
-// per-axis coordinate vectors either way.
+// Trajectory order: the tiled walk (tile_index: one 16 x 4 pixel tile per
+// wave) when the output size tiles, which keeps a wave's cells few and its
+// seed reads in 64-byte runs.  Otherwise 1D/2D walk the points in image order
+// (coalesced seed reads) and 3D in meshgrid order (lanes along coordinate 0:
+// fewer cells per wave than image order, strided seed reads).  Start points
+// come from the per-axis coordinate vectors either way.
 template <int D>
 struct ImageIO {
   static constexpr bool kMeshOrder = D == 3;

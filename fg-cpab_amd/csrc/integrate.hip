@@ -348,10 +348,11 @@ __global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T,
 // Fused transform_data forward (cpab/cpab.py:295-309): output position q
 // (image order, last axis fastest) integrates its meshgrid point under theta b
 // exactly as cpab_forward / the 1D closed form does, then samples every
-// channel of data there exactly as cpab_interp_forward does.  Lanes run along
-// the image's fast axis, so the image stores and final_points (kept in the
-// same order for the backward) are coalesced; the start points come from the
-// grid's per-axis coordinate vectors.
+// channel of data there exactly as cpab_interp_forward does.  Each wave takes
+// one 16 x 4 pixel tile (tile_index) when the size tiles, else a run of 64
+// pixels in image order; the image stores and final_points (image order, for
+// the backward) go out in 64-byte runs or better.  The start points come from
+// the grid's per-axis coordinate vectors.
 template <int ND, bool ADAPTIVE>
 __global__ __launch_bounds__(1024) void image_forward_kernel(
     ImageShape s, int T, int nx, int ny, int nz, const float* __restrict__ axes,
