@@ -104,11 +104,38 @@ __device__ __forceinline__ int tri_2d_inside(float xc, float yc, float fx, float
   return tri_2d(lx, ly);
 }
 
+// Inside rule on in-range coordinates: 4 * square + tri_2d.
+__device__ __forceinline__ int base_plus_tri(float xc, float yc, float fx, float fy) {
+  int base;
+  float lx, ly;
+  const int t = tri_2d_inside(xc, yc, fx, fy, base, lx, ly);
+  return base + t;
+}
+
+// 4 * square + tri_2d(lx, ly) in two adds with a carry-in.  With
+// b3 = lx < ly and b1 = (1 - lx) < ly, tri_2d = 3*b3 ^ b1 = 2*b3 + (b3 ^ b1),
+// so the cell is 2 * (2 * square + b3) + (b3 ^ b1).  Each "x + x + bit" is one
+// v_addc_co_u32 whose carry-in is the bit's lane mask (the compare's own
+// result; the xor of two masks is a scalar op), where the select form takes a
+// shift, two selects and an or.
+__device__ __forceinline__ int cell_from_square(int square, float lx, float ly) {
+  const uint64_t m3 = __builtin_amdgcn_ballot_w64(lx < ly);
+  const uint64_t m0 = m3 ^ __builtin_amdgcn_ballot_w64((1.0f - lx) < ly);
+  int u, c;
+  uint64_t co;
+  asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(u), "=s"(co) : "v"(square), "s"(m3));
+  asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(c), "=s"(co) : "v"(u), "s"(m0));
+  return c;
+}
+
 // Square (cx, cy) holds triangles 4*(cx + cy*nx) + {0 top, 1 right, 2 bottom, 3 left}.
 // A wave whose lanes all lie in (0, kClampHi]^2, where the lookup clamp is the
 // identity, takes the inside rule on the raw coordinates.  Otherwise a
 // wave-uniform branch clamps, and applies the boundary rules to lanes outside
-// (0,1)^2.
+// (0,1)^2.  CARRY picks cell_from_square for the inside rule (fewer VALU ops,
+// for throughput-bound callers) over the select form (a shorter dependency
+// chain, without the scalar xor, for latency-bound ones).
+template <bool CARRY = true>
 __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   const float fx = (float)nx, fy = (float)ny;
   // One ballot per compare keeps the masks in SGPRs (a ballot of a combined
@@ -120,8 +147,9 @@ __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   int base;
   float lx, ly;
   if (!edge) {
-    const int t = tri_2d_inside(px, py, fx, fy, base, lx, ly);
-    return base + t;
+    if (!CARRY) return base_plus_tri(px, py, fx, fy);
+    const float sx = __builtin_floorf(px * fx), sy = __builtin_floorf(py * fy);
+    return cell_from_square((int)fmaf(sy, fx, sx), fmaf(px, fx, -sx), fmaf(py, fy, -sy));
   }
   const int t = tri_2d_inside(clamp_lookup(px), clamp_lookup(py), fx, fy, base, lx, ly);
   int c = base + t;

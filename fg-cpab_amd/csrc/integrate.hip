@@ -109,7 +109,7 @@ __device__ __forceinline__ void stage(float* __restrict__ dst, const float* __re
 // steps where some lane of the wave changed cell, which keeps table traffic and
 // LDS bank conflicts off most steps.  With adaptive_substeps a step that
 // leaves its cell is redone with Heun's rule (cpab_ops_2d.cu:202-219).
-template <bool ADAPTIVE, bool LDS, int PPT>
+template <bool ADAPTIVE, bool LDS, int PPT, bool CARRY = true>
 __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT], float* lds,
                                          const float* __restrict__ Tg,
                                          const float* __restrict__ Ag, int T, int nx, int ny,
@@ -118,20 +118,20 @@ __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT], flo
   Aff<2> M[PPT];
 #pragma unroll
   for (int k = 0; k < PPT; ++k) {
-    cur[k] = cell_2d(px[k], py[k], nx, ny);
+    cur[k] = cell_2d<CARRY>(px[k], py[k], nx, ny);
     M[k] = LDS ? load_aff2(as_lds(lds), cur[k]) : load_aff2(Tg, cur[k]);
   }
   for (int t = 0; t < T; ++t) {
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
-      const int c = (t == 0) ? cur[k] : cell_2d(px[k], py[k], nx, ny);
+      const int c = (t == 0) ? cur[k] : cell_2d<CARRY>(px[k], py[k], nx, ny);
       // Divergent branch, skipped (exec = 0) when no lane changed cell.
       if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
       cur[k] = c;
       float sx, sy;
       apply2(M[k], px[k], py[k], sx, sy);
       if (ADAPTIVE) {
-        const int ce = cell_2d(sx, sy, nx, ny);
+        const int ce = cell_2d<CARRY>(sx, sy, nx, ny);
         if (ce != c) {
           float v0x, v0y, v1x, v1y;
           apply2(load_aff2(Ag, c), px[k], py[k], v0x, v0y);
@@ -291,8 +291,10 @@ __global__ __launch_bounds__(1024) void chain2d_lds_kernel(int nP, int batched, 
         }
       }
     }
-    steps_2d<ADAPTIVE, true, PPT>(px, py, lds, Trels + row * nC * 6, As + row * nC * 6, T, nx,
-                                  ny, hh);
+    // One trajectory per lane leaves few waves: the select form of the lookup
+    // (a shorter dependency chain) measured faster here.
+    steps_2d<ADAPTIVE, true, PPT, false>(px, py, lds, Trels + row * nC * 6, As + row * nC * 6, T,
+                                         nx, ny, hh);
   }
   float* __restrict__ o = out + (size_t)b * 2 * nP;
 #pragma unroll
