@@ -186,13 +186,18 @@ __device__ __forceinline__ int tet_3d(float xc, float yc, float zc, float fx, fl
     y = 1.0f - t;
   }
   // First matching test wins, as in the reference's if-chain; evaluated as
-  // selects (every lane needs all four tests anyway).  (-x) + y == -(x - y)
-  // and ((-x) - y) + z == z - (x + y) in IEEE arithmetic.
+  // selects (every lane needs all four tests anyway).  The reference tests the
+  // signs of (x - y) - z, ((-x) + y) - z, ((x + y) + z) - 2 and
+  // ((-x) - y) + z; (-x) + y == -(x - y) and ((-x) - y) + z == z - (x + y) in
+  // IEEE arithmetic.  With finite operands and denormals kept (these kernels
+  // run with fp32 denormals on: a rounded difference is zero only when the
+  // operands are equal and otherwise has the sign of the exact one), a >= b
+  // decides "a - b >= 0" exactly, so the outer subtractions are compares.
   const float d = x - y, s = x + y;
-  int t = (d - z >= 0.0f) ? 4 : 0;
-  t = ((-d) - z >= 0.0f) ? 3 : t;
-  t = ((s + z) - 2.0f >= 0.0f) ? 2 : t;
-  t = (z - s >= 0.0f) ? 1 : t;
+  int t = (d >= z) ? 4 : 0;
+  t = (-d >= z) ? 3 : t;
+  t = (s + z >= 2.0f) ? 2 : t;
+  t = (z >= s) ? 1 : t;
   return (int)__umul24(cube, 5u) + t;
 }
 
