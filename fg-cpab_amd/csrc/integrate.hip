@@ -121,29 +121,45 @@ __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT], flo
     cur[k] = cell_2d<CARRY>(px[k], py[k], nx, ny);
     M[k] = LDS ? load_aff2(as_lds(lds), cur[k]) : load_aff2(Tg, cur[k]);
   }
-  for (int t = 0; t < T; ++t) {
+  // One step of point k from its cell c (M[k] already holds c's map).
+  auto advance = [&](int k, int c) {
+    float sx, sy;
+    apply2(M[k], px[k], py[k], sx, sy);
+    if (ADAPTIVE) {
+      const int ce = cell_2d<CARRY>(sx, sy, nx, ny);
+      if (ce != c) {
+        float v0x, v0y, v1x, v1y;
+        apply2(load_aff2(Ag, c), px[k], py[k], v0x, v0y);
+        apply2(load_aff2(Ag, ce), sx, sy, v1x, v1y);
+        sx = fmaf(hh, v0x + v1x, px[k]);
+        sy = fmaf(hh, v0y + v1y, py[k]);
+      }
+    }
+    px[k] = sx;
+    py[k] = sy;
+  };
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) advance(k, cur[k]);
+  auto step = [&]() {
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
-      const int c = (t == 0) ? cur[k] : cell_2d<CARRY>(px[k], py[k], nx, ny);
+      const int c = cell_2d<CARRY>(px[k], py[k], nx, ny);
       // Divergent branch, skipped (exec = 0) when no lane changed cell.
       if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
       cur[k] = c;
-      float sx, sy;
-      apply2(M[k], px[k], py[k], sx, sy);
-      if (ADAPTIVE) {
-        const int ce = cell_2d<CARRY>(sx, sy, nx, ny);
-        if (ce != c) {
-          float v0x, v0y, v1x, v1y;
-          apply2(load_aff2(Ag, c), px[k], py[k], v0x, v0y);
-          apply2(load_aff2(Ag, ce), sx, sy, v1x, v1y);
-          sx = fmaf(hh, v0x + v1x, px[k]);
-          sy = fmaf(hh, v0y + v1y, py[k]);
-        }
-      }
-      px[k] = sx;
-      py[k] = sy;
+      advance(k, c);
     }
+  };
+  // Steps 1 .. T-1, two per iteration (written out: the lookup's ballots keep
+  // the compiler from unrolling a loop of unknown trip count), so that the
+  // loop-carried positions and cells alternate between two register sets
+  // instead of being copied back at every step.
+  int t = 1;
+  for (; t + 1 < T; t += 2) {
+    step();
+    step();
   }
+  if (t < T) step();
 }
 
 // T fixed steps of one transform for one point (3D, cpab_ops_3d.cu:169-241),
