@@ -3,8 +3,10 @@
 Mirrors the helper surface of the reference's ``cpab/core/utility.py``
 (``params`` container, directory helpers, null space, pickle cache I/O), with
 one deliberate difference: cached basis files are read back through a
-restricted unpickler that only rebuilds numpy / scipy.sparse / builtin
-containers, so a cache file can never execute code on load.
+restricted unpickler that resolves only an exact list of globals (numpy's
+array, scalar and dtype reconstructors, scipy.sparse's csr / csc / coo classes
+and builtin containers), so a cache file cannot name any callable that runs
+code or touches files.
 """
 import os
 import pickle
@@ -90,20 +92,28 @@ def null(A, eps=1e-6, zero_tol=None):
 # Basis cache I/O
 # ---------------------------------------------------------------------------
 
-# Globals a cached tessellation dict may reference: numpy arrays / scalars and
-# scipy.sparse matrices, nothing that can run code.
-_SAFE_PREFIXES = ("numpy", "scipy.sparse")
-_SAFE_BUILTINS = {"dict", "list", "tuple", "set", "frozenset", "int", "float",
-                  "complex", "bool", "str", "bytes", "bytearray", "slice", "range"}
+# The exact globals a cached tessellation dict may reference, as the
+# reference's save_obj (pickle.dump of Tesselation.__dict__, utility.py:70-73,
+# tesselation.py:101) writes them under numpy 1.x / 2.x and scipy's old and
+# new module layouts: array and scalar reconstructors, dtype, and the sparse
+# matrix classes (rebuilt from their state, without calling __init__).  Every
+# other global, in numpy or anywhere else, is refused.
+_NUMPY_CORE = ("numpy.core", "numpy._core")
+_SAFE_GLOBALS = frozenset(
+    [("numpy", "dtype"), ("numpy", "ndarray")]
+    + [(c + ".multiarray", n) for c in _NUMPY_CORE for n in ("_reconstruct", "scalar")]
+    + [(c + ".numeric", "_frombuffer") for c in _NUMPY_CORE]
+    + [(m, k + "_" + kind)
+       for k in ("csr", "csc", "coo")
+       for m in ("scipy.sparse", "scipy.sparse." + k, "scipy.sparse._" + k)
+       for kind in ("matrix", "array")]
+    + [("builtins", n) for n in ("dict", "list", "tuple", "set", "frozenset", "int", "float",
+                                  "complex", "bool", "str", "bytes", "bytearray", "slice", "range")])
 
 
 class _RestrictedUnpickler(pickle.Unpickler):
     def find_class(self, module, name):
-        if module == "builtins" and name in _SAFE_BUILTINS:
-            return super().find_class(module, name)
-        if module.split(".")[0] == "numpy" or module.startswith("scipy.sparse"):
-            if name.startswith("_") and name not in ("_reconstruct", "_frombuffer"):
-                raise pickle.UnpicklingError(f"refusing {module}.{name}")
+        if (module, name) in _SAFE_GLOBALS:
             return super().find_class(module, name)
         raise pickle.UnpicklingError(f"refusing to load global {module}.{name}")
 

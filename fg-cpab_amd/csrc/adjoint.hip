@@ -48,6 +48,7 @@
 //              the wave for lanes that share a cell.
 #include <hip/hip_runtime.h>
 #include <algorithm>
+#include <cmath>
 #include "cpab_device.hpp"
 #include "cpab_launch.hpp"
 #include "cpab_sample.hpp"
@@ -386,10 +387,10 @@ struct ImageIO {
   __device__ __forceinline__ void finish(int, bool, const float (&)[D]) const {}
 };
 
-// Segmented variant (any T).
+// Segmented variant (any T <= kSeg * MAXSEG).
 // One stage of one theta over this workgroup's point range; moments go to
 // bins / keys / mom_b.
-template <int D, bool ADAPTIVE, int BINS, typename P, typename IO>
+template <int D, bool ADAPTIVE, int BINS, int MAXSEG = kMaxSeg, typename P, typename IO>
 __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ gtab, int nP, int T,
                                                const Cells& g, const IO& io, float* bins,
                                                int* keys, float* __restrict__ mom_b) {
@@ -409,22 +410,29 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
     float p[D];
     io.start(pi, p);
 
+    // The adjoint seed first: its reads (for the fused transform_data backward,
+    // the resampling gradient over every channel) are done before the
+    // checkpoints take their registers.
+    float lam[D];
+    io.seed(pi, valid, lam);
+
     // Phase 1: checkpoint (position before step seg*kSeg) pushed per segment.
-    float ck[D][kMaxSeg];
+    float ck[D][MAXSEG];
 #pragma unroll
     for (int k = 0; k < D; ++k)
 #pragma unroll
-      for (int i = 0; i < kMaxSeg; ++i) ck[k][i] = 0.0f;
+      for (int i = 0; i < MAXSEG; ++i) ck[k][i] = 0.0f;
     for (int seg = 0; seg < nseg; ++seg) {
 #pragma unroll
       for (int k = 0; k < D; ++k) stack_push(ck[k], p[k]);
       const int len = min(kSeg, T - seg * kSeg);
+      // Not unrolled: in 1D the compiler otherwise unrolls this short loop into
+      // a register-hungry block that spills beside the register variant.
+#pragma unroll 1
       for (int s = 0; s < len; ++s) replay_step<D, ADAPTIVE>(tab, lookup<D>(p, g), p, h, hh, g);
     }
 
     // Phase 2: reverse sweep.
-    float lam[D];
-    io.seed(pi, valid, lam);
     float m[PP];
 #pragma unroll
     for (int k = 0; k < PP; ++k) m[k] = 0.0f;
@@ -675,12 +683,44 @@ struct StageLds {
   }
 };
 
+// Whether the positions of this row's trajectories may be recovered through
+// the inverse one-step maps: the largest ||M_c||_2 over the row's cells (the
+// row's amp_row[0 .. namp) block maxima) at most amp_max = kRecoverGrowth^(1/T).
+// Wave-uniform (read into a scalar register).
+__device__ __forceinline__ bool recover_ok(const float* __restrict__ amp_row, int namp,
+                                          float amp_max) {
+  float a = 0.0f;
+  for (int i = __lane_id(); i < namp; i += 64) a = fmaxf(a, amp_row[i]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+  return __builtin_amdgcn_readfirstlane(a <= amp_max ? 1 : 0) != 0;
+}
+
+// Row stability of the register variant: the per-row block maxima of ||M_c||_2
+// and the bound they are held to.
+struct Recover {
+  const float* __restrict__ amp;  // [rows, namp]
+  int namp;
+  float amp_max;
+};
+
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS, typename IO>
 __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, const float* Ag,
                                           const float* Gg, int nP, int T, const Cells& g,
-                                          const IO& io, float* __restrict__ mom_b) {
+                                          const IO& io, float* __restrict__ mom_b,
+                                          const Recover& rec, size_t row) {
   if constexpr (TS > 0) {
     static_assert(BINS != kBinsGlobal, "the register variant accumulates in LDS");
+    if constexpr (!ADAPTIVE) {
+      // Rows whose inverse maps could amplify the recovered positions' rounding
+      // beyond kRecoverGrowth replay each segment from a checkpoint instead.
+      if (!recover_ok(rec.amp + row * rec.namp, rec.namp, rec.amp_max)) {
+        constexpr int kSegs = (TS + kSeg - 1) / kSeg;
+        if (LDS_A) segmented_body<D, false, BINS, kSegs>(as_lds(L.ldsA), Gg, nP, TS, g, io, L.bins, L.keys, mom_b);
+        else segmented_body<D, false, BINS, kSegs>(Ag, Gg, nP, TS, g, io, L.bins, L.keys, mom_b);
+        return;
+      }
+    }
     if (LDS_A) register_body<D, ADAPTIVE, BINS, TS>(as_lds(L.ldsA), Gg, nP, g, io, L.bins, L.keys, mom_b);
     else register_body<D, ADAPTIVE, BINS, TS>(Ag, Gg, nP, g, io, L.bins, L.keys, mom_b);
   } else {
@@ -713,9 +753,9 @@ template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kernel(
     int nP, int batched, int T, Cells g, int nC, int K, const float* __restrict__ points,
     const float* __restrict__ stage_points, const float* __restrict__ As,
-    const float* __restrict__ Gs, const float* __restrict__ grad_out, float* __restrict__ moments,
-    float* __restrict__ partials, uint64_t* __restrict__ dense_parts, float* __restrict__ lam,
-    float* __restrict__ grad_points) {
+    const float* __restrict__ Gs, Recover rec, const float* __restrict__ grad_out,
+    float* __restrict__ moments, float* __restrict__ partials, uint64_t* __restrict__ dense_parts,
+    float* __restrict__ lam, float* __restrict__ grad_points) {
   extern __shared__ float lds[];
   __shared__ int touched_cnt;
   const int b = blockIdx.y;
@@ -735,7 +775,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kerne
     io.lam_out = k == 0 ? (grad_points ? grad_points + (size_t)b * plane : nullptr)
                         : lam + (size_t)b * plane;
     L.begin(Ag, R, &touched_cnt);
-    run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, nP, T, g, io, moments + row * R);
+    run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, nP, T, g, io, moments + row * R, rec, row);
     // Every lane is done with this stage's tables before they are written out
     // (and, for the next stage, overwritten).
     const size_t part = row * gridDim.x + blockIdx.x;
@@ -751,7 +791,8 @@ template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward_kernel(
     ImageShape s, int T, Cells g, int nC, const float* __restrict__ axes,
     const float* __restrict__ final_points, const float* __restrict__ As,
-    const float* __restrict__ Gs, const float* __restrict__ data, const float* __restrict__ grad_out,
+    const float* __restrict__ Gs, Recover rec, const float* __restrict__ data,
+    const float* __restrict__ grad_out,
     float* __restrict__ moments, float* __restrict__ partials, uint64_t* __restrict__ dense_parts,
     float* __restrict__ grad_data) {
   extern __shared__ float lds[];
@@ -769,7 +810,8 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
   io.data = data + (size_t)b * s.C * s.plane_in;
   io.gdata = grad_data ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
   L.begin(Ag, R, &touched_cnt);
-  run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, s.nP, T, g, io, moments + (size_t)b * R);
+  run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, s.nP, T, g, io, moments + (size_t)b * R, rec,
+                                          (size_t)b);
   const size_t part = (size_t)b * gridDim.x + blockIdx.x;
   L.end(partials + part * R, dense_parts + (size_t)b * ((gridDim.x + 63) / 64), (int)blockIdx.x,
         moments + (size_t)b * R, nC, &touched_cnt);
@@ -797,7 +839,7 @@ struct BackwardJob {
   Geometry geo;
   int64_t nP, n_batch;
   int batched, T, K;
-  const float *points, *stage_points, *As, *G, *grad_out;
+  const float *points, *stage_points, *As, *G, *amp, *grad_out;
   float *moments, *partials, *lam, *grad_points;
   uint64_t* dense_parts;
   const ImageShape* image;
@@ -809,20 +851,22 @@ template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 hipError_t go(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
   const size_t lds = stage_lds_bytes<D, LDS_A, BINS>(j.geo.nC);
   const Cells g{j.geo.nx, j.geo.ny, j.geo.nz};
+  const Recover rec{j.amp, adjoint_table_blocks(j.geo.nC),
+                    (float)std::pow((double)kRecoverGrowth, 1.0 / (double)j.T)};
   const dim3 grid((unsigned)cfg.chunks, (unsigned)j.n_batch), block((unsigned)cfg.block);
   if (j.image) {
     auto kernel = image_backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
     hipError_t e = allow_lds(kernel, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, grid, block, lds, s, *j.image, j.T, g, j.geo.nC, j.axes,
-                       j.final_points, j.As, j.G, j.data, j.grad_out, j.moments, j.partials,
+                       j.final_points, j.As, j.G, rec, j.data, j.grad_out, j.moments, j.partials,
                        j.dense_parts, j.grad_data);
   } else {
     auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
     hipError_t e = allow_lds(kernel, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, grid, block, lds, s, (int)j.nP, j.batched, j.T, g, j.geo.nC, j.K,
-                       j.points, j.stage_points, j.As, j.G, j.grad_out, j.moments, j.partials,
+                       j.points, j.stage_points, j.As, j.G, rec, j.grad_out, j.moments, j.partials,
                        j.dense_parts, j.lam, j.grad_points);
   }
   return hipGetLastError();
@@ -881,7 +925,8 @@ hipError_t dispatch_any(const BackwardJob& j, int adaptive, const LaunchCfg& cfg
 
 hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
                            int K, int adaptive, const float* points, const float* stage_points,
-                           const float* As, const float* G, const float* grad_out, float* moments,
+                           const float* As, const float* G, const float* amp,
+                           const float* grad_out, float* moments,
                            float* partials, uint64_t* dense_parts, float* lam, float* grad_points,
                            const LaunchCfg& cfg, hipStream_t s) {
   BackwardJob j{};
@@ -895,6 +940,7 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
   j.stage_points = stage_points;
   j.As = As;
   j.G = G;
+  j.amp = amp;
   j.grad_out = grad_out;
   j.moments = moments;
   j.partials = partials;
@@ -906,7 +952,7 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
 
 hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
                                  int adaptive, const float* axes, const float* final_points,
-                                 const float* As, const float* G, const float* data,
+                                 const float* As, const float* G, const float* amp, const float* data,
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
                                  hipStream_t s) {
@@ -918,6 +964,7 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
   j.K = 1;
   j.As = As;
   j.G = G;
+  j.amp = amp;
   j.grad_out = grad_out;
   j.moments = moments;
   j.partials = partials;

@@ -76,37 +76,61 @@ __global__ void project_kernel(int64_t n_theta, int D, int d, const float* __res
   grad[i] = acc;
 }
 
-// One thread per cell row of the table: the reverse-sweep entry of cell i
-// (cpab_device.hpp, RevStride): G = h A_lin + (h^2/2) A_lin^2
-// (adjoint_increment) and the inverse one-step map (inverse_step_map); the
-// cell's sums zeroed; the first n_words threads also clear the dense-part
-// masks.
+// Reverse-sweep table.  Each workgroup of kTableThreads covers one block of
+// one row's cells (row = blockIdx.x / nblk, block = blockIdx.x % nblk), one
+// thread per cell: the entry of the cell (cpab_device.hpp, RevStride):
+// G = h A_lin + (h^2/2) A_lin^2 (adjoint_increment) and the inverse one-step
+// map (inverse_step_map); the cell's sums zeroed.  The workgroup's largest
+// ||M_c||_2 of the inverse maps (inverse_map_norm) goes to amp[blockIdx.x]:
+// the backward reads a row's nblk entries to bound how much the recovered
+// positions' rounding can grow.  Thread i of the grid also clears
+// dense_parts[i] for i < n_words.
+constexpr int kTableThreads = 256;
+
 template <int D>
-__global__ void adjoint_table_kernel(int64_t n_cells, float h, const float* __restrict__ As,
-                                     float* __restrict__ G, float* __restrict__ moments,
-                                     uint64_t* __restrict__ dense_parts, int64_t n_words) {
+__global__ __launch_bounds__(kTableThreads) void adjoint_table_kernel(
+    int64_t rows, int nC, int nblk, float h, const float* __restrict__ As, float* __restrict__ G,
+    float* __restrict__ moments, float* __restrict__ amp, uint64_t* __restrict__ dense_parts,
+    int64_t n_words) {
   constexpr int P = D * (D + 1);
   constexpr int S = RevStride<D>::S;
   constexpr int GS = D == 1 ? 1 : (D == 2 ? 4 : 12);   // floats of the G part
   constexpr int IW = D == 1 ? 2 : 4;                   // row stride of the inverse map
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i < n_words) dense_parts[i] = 0;
-  if (i >= n_cells) return;
-  float a[P], e[S], inv[P];
+  __shared__ float wave_max[kTableThreads / 64];
+  const int64_t lin = blockIdx.x * (int64_t)kTableThreads + threadIdx.x;
+  if (lin < n_words) dense_parts[lin] = 0;
+  const int64_t row = blockIdx.x / nblk;
+  const int c = (int)(blockIdx.x - row * nblk) * kTableThreads + (int)threadIdx.x;
+  float norm = 0.0f;
+  if (row < rows && c < nC) {
+    const int64_t i = row * nC + c;
+    float a[P], e[S], inv[P];
 #pragma unroll
-  for (int k = 0; k < S; ++k) e[k] = 0.0f;
+    for (int k = 0; k < S; ++k) e[k] = 0.0f;
 #pragma unroll
-  for (int k = 0; k < P; ++k) a[k] = As[i * P + k];
-  adjoint_increment<D>(a, h, (h * 0.5f) * h, e);
-  inverse_step_map<D>(a, h, inv);
+    for (int k = 0; k < P; ++k) a[k] = As[i * P + k];
+    adjoint_increment<D>(a, h, (h * 0.5f) * h, e);
+    inverse_step_map<D>(a, h, inv);
+    norm = inverse_map_norm<D>(inv);
 #pragma unroll
-  for (int r = 0; r < D; ++r)
+    for (int r = 0; r < D; ++r)
 #pragma unroll
-    for (int j = 0; j <= D; ++j) e[GS + r * IW + j] = inv[r * (D + 1) + j];
+      for (int j = 0; j <= D; ++j) e[GS + r * IW + j] = inv[r * (D + 1) + j];
 #pragma unroll
-  for (int k = 0; k < S; ++k) G[i * S + k] = e[k];
+    for (int k = 0; k < S; ++k) G[i * S + k] = e[k];
 #pragma unroll
-  for (int k = 0; k < P; ++k) moments[i * P + k] = 0.0f;
+    for (int k = 0; k < P; ++k) moments[i * P + k] = 0.0f;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) norm = fmaxf(norm, __shfl_xor(norm, off));
+  if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = norm;
+  __syncthreads();
+  if (threadIdx.x == 0 && row < rows) {
+    float m = wave_max[0];
+#pragma unroll
+    for (int w = 1; w < kTableThreads / 64; ++w) m = fmaxf(m, wave_max[w]);
+    amp[blockIdx.x] = m;
+  }
 }
 
 // One thread per (row, cell): S = the HBM sum in `moments` plus
@@ -456,18 +480,24 @@ hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
   return hipGetLastError();
 }
 
-hipError_t launch_adjoint_table(int ndim, int64_t n_cells, int T, const float* As, float* G,
-                                float* moments, uint64_t* dense_parts, int64_t n_words,
+int adjoint_table_blocks(int nC) { return (nC + kTableThreads - 1) / kTableThreads; }
+
+hipError_t launch_adjoint_table(int ndim, int64_t rows, int nC, int T, const float* As, float* G,
+                                float* moments, float* amp, uint64_t* dense_parts, int64_t n_words,
                                 hipStream_t s) {
-  if (n_cells <= 0) return hipSuccess;
+  if (rows <= 0 || nC <= 0) return hipSuccess;
   const float h = 1.0f / (float)T;
-  const dim3 g(grid_for(std::max(n_cells, n_words), 256)), b(256);
-  if (ndim == 1)
-    hipLaunchKernelGGL(adjoint_table_kernel<1>, g, b, 0, s, n_cells, h, As, G, moments, dense_parts, n_words);
-  else if (ndim == 2)
-    hipLaunchKernelGGL(adjoint_table_kernel<2>, g, b, 0, s, n_cells, h, As, G, moments, dense_parts, n_words);
-  else
-    hipLaunchKernelGGL(adjoint_table_kernel<3>, g, b, 0, s, n_cells, h, As, G, moments, dense_parts, n_words);
+  const int nblk = adjoint_table_blocks(nC);
+  // Enough workgroups for one per (row, cell block) and one thread per mask word.
+  const int64_t blocks = std::max<int64_t>(rows * nblk, (n_words + kTableThreads - 1) / kTableThreads);
+  const dim3 g((unsigned)blocks), b(kTableThreads);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, g, b, 0, s, rows, nC, nblk, h, As, G, moments, amp, dense_parts,
+                       n_words);
+  };
+  if (ndim == 1) go(adjoint_table_kernel<1>);
+  else if (ndim == 2) go(adjoint_table_kernel<2>);
+  else go(adjoint_table_kernel<3>);
   return hipGetLastError();
 }
 

@@ -284,10 +284,11 @@ int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 // Workspace of a K-stage backward (rows = K * n_batch): with full LDS bins the
 // dense-part masks [rows, ceil(chunks/64)] and the partial tables
 // [rows, chunks, nC, ppc]; then the inter-stage adjoint [n_batch, ndim, nP]
-// (K > 1) and the reverse-sweep table [rows, nC, 4|12|24] (G and the inverse
-// one-step map per cell, cpab_device.hpp RevStride).
+// (K > 1), the reverse-sweep table [rows, nC, 4|12|24] (G and the inverse
+// one-step map per cell, cpab_device.hpp RevStride) and the per-block norms of
+// the inverse maps [rows, adjoint_table_blocks(nC)].
 struct BackwardWorkspace {
-  int64_t dense_words, partials_offset, lam_offset, g_offset, total;
+  int64_t dense_words, partials_offset, lam_offset, g_offset, amp_offset, total;
 };
 
 int adj_stride(int ndim) { return ndim == 1 ? 4 : (ndim == 2 ? 12 : 24); }
@@ -300,7 +301,8 @@ BackwardWorkspace backward_workspace(const cpab::Geometry& g, int64_t nP, int64_
   w.partials_offset = align_up(w.dense_words * 8);
   w.lam_offset = align_up(w.partials_offset + parts * g.nC * g.ppc() * 4);
   w.g_offset = K > 1 ? align_up(w.lam_offset + n_batch * g.ndim * nP * 4) : w.lam_offset;
-  w.total = w.g_offset + (int64_t)K * n_batch * g.nC * adj_stride(g.ndim) * 4;
+  w.amp_offset = align_up(w.g_offset + (int64_t)K * n_batch * g.nC * adj_stride(g.ndim) * 4);
+  w.total = w.amp_offset + (int64_t)K * n_batch * cpab::adjoint_table_blocks(g.nC) * 4;
   return w;
 }
 
@@ -348,16 +350,17 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   float* partials = reinterpret_cast<float*>(ws + w.partials_offset);
   float* lam = K > 1 ? reinterpret_cast<float*>(ws + w.lam_offset) : nullptr;
   float* G = reinterpret_cast<float*>(ws + w.g_offset);
-  // G table; the HBM sums and dense-part masks cleared.
-  rc = check_hip(cpab::launch_adjoint_table(ndim, rows * g.nC, nstepsolver, As, G, moments, dense,
-                                            w.dense_words, s),
+  float* amp = reinterpret_cast<float*>(ws + w.amp_offset);
+  // G table and inverse-map norms; the HBM sums and dense-part masks cleared.
+  rc = check_hip(cpab::launch_adjoint_table(ndim, rows, g.nC, nstepsolver, As, G, moments, amp,
+                                            dense, w.dense_words, s),
                  who);
   if (rc) return rc;
   hipEvent_t ev;
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_backward(g, nP, n_batch, batched ? 1 : 0, nstepsolver, K, adaptive,
-                                       points, stage_points, As, G, grad_out, moments, partials,
-                                       dense, lam, grad_points, cfg, s),
+                                       points, stage_points, As, G, amp, grad_out, moments,
+                                       partials, dense, lam, grad_points, cfg, s),
                  who);
   prof_end(timed, ev, "backward", s);
   if (rc) return rc;
@@ -574,7 +577,8 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   uint64_t* dense = reinterpret_cast<uint64_t*>(ws);
   float* partials = reinterpret_cast<float*>(ws + w.partials_offset);
   float* G = reinterpret_cast<float*>(ws + w.g_offset);
-  rc = check_hip(cpab::launch_adjoint_table(ndim, n_batch * g.nC, nstepsolver, As, G, moments,
+  float* amp = reinterpret_cast<float*>(ws + w.amp_offset);
+  rc = check_hip(cpab::launch_adjoint_table(ndim, n_batch, g.nC, nstepsolver, As, G, moments, amp,
                                             dense, w.dense_words, s),
                  "cpab_transform_data_backward");
   if (rc) return rc;
@@ -586,7 +590,7 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   hipEvent_t ev;
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, axes,
-                                             final_points, As, G, data, grad_out, moments,
+                                             final_points, As, G, amp, data, grad_out, moments,
                                              partials, dense, grad_data, cfg, s),
                  "cpab_transform_data_backward");
   prof_end(timed, ev, "image_backward", s);

@@ -45,11 +45,13 @@ hipError_t launch_affine_expm(int ndim, int64_t n_theta, int nC, int d, const fl
 hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
                           const int32_t* col_ptr, const int32_t* row_idx, const float* vals,
                           float* grad_theta, hipStream_t s);
-// G [n_cells, RevStride]: per cell h A + (h^2/2) A^2 and the inverse one-step
-// map (cpab_device.hpp), h = 1/T; zeroes
-// moments [n_cells, ppc] (the HBM sums) and dense_parts [n_words].
-hipError_t launch_adjoint_table(int ndim, int64_t n_cells, int T, const float* As, float* G,
-                                float* moments, uint64_t* dense_parts, int64_t n_words,
+// G [rows, nC, RevStride]: per cell h A + (h^2/2) A^2 and the inverse one-step
+// map (cpab_device.hpp), h = 1/T; amp [rows, adjoint_table_blocks(nC)]: the
+// largest ||M_c||_2 of the inverse maps over each block of a row's cells;
+// zeroes moments [rows, nC, ppc] (the HBM sums) and dense_parts [n_words].
+int adjoint_table_blocks(int nC);
+hipError_t launch_adjoint_table(int ndim, int64_t rows, int nC, int T, const float* As, float* G,
+                                float* moments, float* amp, uint64_t* dense_parts, int64_t n_words,
                                 hipStream_t s);
 // moments [rows, nC, ppc] from the reverse sweep's per-cell sums S, in place:
 // the HBM sums in `moments` plus the partial tables [rows, nparts, nC, ppc] of
@@ -72,14 +74,19 @@ hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, in
                               int adaptive, const float* points, const float* Trels,
                               const float* As, int32_t* cells, hipStream_t s);
 // lam: [n_batch, ndim, nP] scratch carrying the adjoint between stages (K > 1).
-// G: the reverse-sweep table of launch_adjoint_table, same rows as As.
+// G, amp: the reverse-sweep table and its per-block norms from
+// launch_adjoint_table, same rows as As.  The register variant recovers
+// positions through the inverse maps only for rows whose amplification bound
+// (max ||M_c||_2)^T stays within kRecoverGrowth; other rows replay from
+// checkpoints.
 // The per-cell sums S go to moments (HBM sums, zero on entry) or, for a
 // full-bin workgroup that touched a quarter of the cells or more, to its
 // partial table [rows, chunks, nC, ppc] with its bit set in dense_parts
 // [rows, ceil(chunks/64)] (zero on entry).  launch_finish_moments follows.
 hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
                            int K, int adaptive, const float* points, const float* stage_points,
-                           const float* As, const float* G, const float* grad_out, float* moments,
+                           const float* As, const float* G, const float* amp,
+                           const float* grad_out, float* moments,
                            float* partials, uint64_t* dense_parts, float* lam, float* grad_points,
                            const LaunchCfg& cfg, hipStream_t s);
 
@@ -90,7 +97,7 @@ hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_
                                 float* final_points, const LaunchCfg& cfg, hipStream_t s);
 hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
                                  int adaptive, const float* axes, const float* final_points,
-                                 const float* As, const float* G, const float* data,
+                                 const float* As, const float* G, const float* amp, const float* data,
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
                                  hipStream_t s);

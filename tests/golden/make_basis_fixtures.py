@@ -11,6 +11,12 @@ zero_boundary=False / volume_perservation=True (utility.py:36-56,
 tesselation.py:282-290) and the 1D/3D nodal-basis column order
 (tesselation.py:216-307).  Each .npz holds the CSR arrays of B, its shape and
 the cell vertices (verts) of the tessellation.
+
+It also keeps, for PICKLE_CASES, the basis cache file exactly as the
+reference's Tesselation writes it through its save_obj (pickle of the
+instance __dict__, tesselation.py:101-104, utility.py:70-73), as
+refcache_<cache file name>.pkl: data for the test that this package's
+restricted loader reads caches the reference left in a basis_files/ folder.
 """
 import importlib.util
 import os
@@ -54,6 +60,20 @@ def load_reference_core():
     return mods["tesselation"]
 
 
+# Small cases whose reference-written cache file is kept (1D through the SVD
+# null space, 2D through the nodal basis).
+PICKLE_CASES = [
+    ([5], False, False),
+    ([3, 2], True, False),
+]
+
+
+def cache_name(nc, zb, vp):
+    """The reference's cache file name (tesselation.py:64-71), without .pkl."""
+    return ("cpab_basis_dim%d_tess%s_vo%d_zb%d_vp%d_nodal_v2"
+            % (len(nc), "_".join(map(str, nc)), int(not zb), int(zb), int(vp)))
+
+
 def fixture_name(nc, zb, vp):
     return "basis_%s_zb%d_vp%d.npz" % ("x".join(map(str, nc)), int(zb), int(vp))
 
@@ -70,6 +90,14 @@ def main():
                                 data=B.data, indices=B.indices, indptr=B.indptr,
                                 shape=np.array(B.shape), verts=np.asarray(T.verts, dtype=np.float64))
             print(fixture_name(nc, zb, vp), B.shape, B.nnz)
+        for nc, zb, vp in PICKLE_CASES:
+            n = len(nc)
+            # override=True: computed and saved by the reference's own save_obj
+            cls[n](nc, [0] * n, [1] * n, zb, vp, tmp + "/", True)
+            src = os.path.join(tmp, cache_name(nc, zb, vp) + ".pkl")
+            with open(src, "rb") as f_in, open(os.path.join(HERE, "refcache_" + cache_name(nc, zb, vp) + ".pkl"), "wb") as f_out:
+                f_out.write(f_in.read())
+            print("refcache_" + cache_name(nc, zb, vp) + ".pkl")
 
 
 if __name__ == "__main__":

@@ -63,3 +63,19 @@ def assert_adjoint_close(got, ref):
     3e-6 normwise on the kernel-test cases).
     """
     assert_grad_close(got, ref, rtol=1e-5, atol_frac=2e-6)
+
+
+def recover_growth(As, T=50):
+    """Per theta row, the bound (max_c ||M_c||_2)^T on how much the register
+    backward's recovered positions can amplify their rounding, M_c being the
+    inverse of cell c's explicit-midpoint step map (the criterion the library
+    applies to choose between recovering positions and replaying them from
+    checkpoints, evaluated here in float64).  As: [rows, nC, nd, nd + 1]."""
+    A = np.asarray(As, np.float64)
+    nd = A.shape[-2]
+    h = float(np.float32(1.0) / np.float32(T))
+    h2 = h * float(np.float32(h * np.float32(0.5)))
+    L = A[..., :nd]
+    E = np.eye(nd) + h * L + h2 * (L @ L)
+    s = np.linalg.norm(np.linalg.inv(E), ord=2, axis=(-2, -1))
+    return s.max(axis=-1) ** T

@@ -10,6 +10,7 @@ import pickle
 
 import numpy as np
 import pytest
+import scipy.sparse as sp
 
 from cpab.core.tesselation import Tesselation1D, Tesselation2D, Tesselation3D
 from cpab.core.utility import load_obj, save_obj
@@ -130,15 +131,44 @@ def test_cache_roundtrip_and_name(tmp_path):
     assert name.endswith(".pkl")
 
 
-def test_cache_loader_refuses_code(tmp_path):
-    class Evil:
-        def __reduce__(self):
-            return (print, ("pwned",))
+class _Call:
+    """Pickles as a call of fn(*args) when loaded."""
 
+    def __init__(self, fn, *args):
+        self.fn, self.args = fn, args
+
+    def __reduce__(self):
+        return (self.fn, self.args)
+
+
+@pytest.mark.parametrize("fn,args", [
+    (print, ("pwned",)),
+    # public callables of numpy itself: writing files, loading native code
+    (np.savetxt, ("{out}", np.arange(3))),
+    (np.save, ("{out}", np.arange(3))),
+    (np.ctypeslib.load_library, ("libm", "/usr/lib")),
+    (np.memmap, ("{out}",)),
+    (np.load, ("{out}",)),
+    # a scipy.sparse module function (only the matrix classes are allowed)
+    (sp.save_npz, ("{out}", sp.csr_matrix(np.eye(2)))),
+])
+def test_cache_loader_refuses_code(tmp_path, fn, args):
+    out = str(tmp_path / "written")
+    args = tuple(a.format(out=out) if isinstance(a, str) else a for a in args)
     path = str(tmp_path / "evil")
     with open(path + ".pkl", "wb") as f:
-        pickle.dump({"x": Evil()}, f)
+        pickle.dump({"x": _Call(fn, *args)}, f)
     with pytest.raises(pickle.UnpicklingError):
         load_obj(path)
-    save_obj({"a": np.arange(3)}, path)
-    assert (load_obj(path)["a"] == np.arange(3)).all()
+    assert not any(p.name.startswith("written") for p in tmp_path.iterdir())
+
+
+def test_cache_loader_reads_arrays_and_sparse(tmp_path):
+    path = str(tmp_path / "ok")
+    obj = {"a": np.arange(3), "s": np.float64(2.5), "i": np.int64(7),
+           "B": sp.csr_matrix(np.eye(3)), "C": sp.coo_matrix(np.eye(2)), "t": (1, [2.0], {"k": "v"})}
+    save_obj(obj, path)
+    back = load_obj(path)
+    assert (back["a"] == np.arange(3)).all() and back["s"] == 2.5 and back["i"] == 7
+    assert (back["B"] != obj["B"]).nnz == 0 and (back["C"].toarray() == np.eye(2)).all()
+    assert back["t"] == (1, [2.0], {"k": "v"})

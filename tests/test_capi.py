@@ -1,15 +1,36 @@
 """C ABI checks that need no GPU: the library loads, exports every symbol
 include/cpab_hip.h declares, and rejects bad arguments before any HIP call
-(the reference's TORCH_CHECK set, transformer_cuda.cu:38-48,183-197)."""
+(the reference's TORCH_CHECK set, transformer_cuda.cu:38-48,183-197).
+
+The argument checks pass made-up device addresses that validation must
+reject before anything is launched.  They run in a child process that sees
+no GPU (HIP_VISIBLE_DEVICES=-1, ROCR_VISIBLE_DEVICES=-1, set before the
+library initialises HIP), so that if validation ever let a call through, the
+launch would fail with a HIP error instead of touching those addresses."""
 import ctypes
 import os
 import re
+import subprocess
+import sys
 
 import pytest
 
 from cpab.pytorch import _native
 
 ROOT = os.path.dirname(os.path.dirname(os.path.realpath(__file__)))
+HERE = os.path.dirname(os.path.realpath(__file__))
+
+
+def _run_without_gpu(check):
+    """Run the module-level function `check` of this file in a child process
+    with every GPU hidden."""
+    env = dict(os.environ, HIP_VISIBLE_DEVICES="-1", ROCR_VISIBLE_DEVICES="-1",
+               CUDA_VISIBLE_DEVICES="-1")
+    paths = [HERE, ROOT, os.path.join(ROOT, "fg-cpab_amd")]
+    code = f"import sys; sys.path[:0] = {paths!r}; import test_capi; test_capi.{check}()"
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
 
 
 def _declared():
@@ -37,6 +58,10 @@ def _err(lib):
 
 
 def test_forward_rejects_bad_steps_and_ndim():
+    _run_without_gpu("_check_forward_rejects_bad_steps_and_ndim")
+
+
+def _check_forward_rejects_bad_steps_and_ndim():
     lib = _native.load_library()
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     rc = lib.cpab_forward(2, 10, 1, 0, 101, 4, 4, 1, 0, p, p, p, p, None)
@@ -57,6 +82,10 @@ def test_forward_rejects_bad_steps_and_ndim():
 
 
 def test_backward_rejects_null_and_small_workspace():
+    _run_without_gpu("_check_backward_rejects_null_and_small_workspace")
+
+
+def _check_backward_rejects_null_and_small_workspace():
     lib = _native.load_library()
     p = ctypes.c_void_p(16)
     rc = lib.cpab_backward(2, 10, 1, 0, 50, 4, 4, 1, 0, p, p, p, None, None, None, 0, None)
@@ -66,6 +95,10 @@ def test_backward_rejects_null_and_small_workspace():
 
 
 def test_trace_and_interp_validation():
+    _run_without_gpu("_check_trace_and_interp_validation")
+
+
+def _check_trace_and_interp_validation():
     lib = _native.load_library()
     p = ctypes.c_void_p(16)
     rc = lib.cpab_trace_cells(1, 10, 1, 0, 50, 4, 1, 1, 0, p, p, p, p, None)
@@ -84,6 +117,10 @@ def test_missing_library_raises(tmp_path):
 
 
 def test_chain_validation():
+    _run_without_gpu("_check_chain_validation")
+
+
+def _check_chain_validation():
     lib = _native.load_library()
     p = ctypes.c_void_p(16)
     rc = lib.cpab_chain_forward(2, 10, 1, 0, 0, 50, 4, 4, 1, 0, p, p, p, p, None, None)
@@ -98,6 +135,10 @@ def test_chain_validation():
 
 
 def test_misaligned_tables_rejected():
+    _run_without_gpu("_check_misaligned_tables_rejected")
+
+
+def _check_misaligned_tables_rejected():
     lib = _native.load_library()
     p = ctypes.c_void_p(64)
     bad = ctypes.c_void_p(68)  # float-aligned, not 16-byte aligned

@@ -11,8 +11,8 @@ from cpab.pytorch._native import native
 from cpab.pytorch.transformer import basis_tables
 from oracle import oracle as orc
 
-from helpers import (assert_adjoint_close, assert_grad_close, cpab_for, meshgrid, seeded_theta,
-                     uniform_points)
+from helpers import (assert_adjoint_close, assert_grad_close, cpab_for, meshgrid, recover_growth,
+                     seeded_theta, uniform_points)
 
 pytestmark = pytest.mark.gpu
 
@@ -210,12 +210,24 @@ def test_backward_parity(cuda, tess, kind, n, adaptive):
     assert_grad_close(mom, ref_m, rtol=2e-5)
 
 
-@pytest.mark.parametrize("tess,kind,scale", [([20, 20], "uniform", 2.0), ([30, 30], "mesh", 2.0),
-                                             ([4, 4, 4], "mesh", 1.5), ([50], "line", 3.0)])
-def test_backward_parity_strong_field(cuda, tess, kind, scale):
-    # Large theta: strong, fast-changing fields, where the backward's positions
-    # (recovered step by step through each cell's inverse one-step map) and the
-    # factored adjoint see the largest h*|A|.
+@pytest.mark.parametrize("tess,kind,scale,recovered", [
+    # growth bound (max ||M_c||_2)^50 at most 16: positions recovered through
+    # the inverse one-step maps, up to the bound
+    ([20, 20], "uniform", 1.0, True), ([50], "line", 1.0, True), ([4, 4, 4], "mesh", 1.5, True),
+    ([10, 10, 10], "uniform", 1.7, True),
+    # beyond it: every segment replayed from a checkpoint (exact positions)
+    ([20, 20], "uniform", 2.0, False), ([30, 30], "mesh", 2.0, False), ([50], "line", 3.0, False),
+    ([50], "line", 6.0, False), ([50], "line", 10.0, False), ([20, 20], "uniform", 4.0, False),
+    ([20, 20], "uniform", 8.0, False), ([16, 16], "mesh", 6.0, False),
+    ([4, 4, 4], "mesh", 8.0, False), ([10, 10, 10], "uniform", 6.0, False)])
+def test_backward_parity_strong_field(cuda, tess, kind, scale, recovered):
+    # Large theta: strong, fast-changing fields, where the factored adjoint sees
+    # the largest h*|A| and where recovering positions backwards through the
+    # inverse maps would amplify their rounding by up to (max ||M_c||_2)^T
+    # (1e4 .. 1e7 at the strongest cases here: errors of 1e-3 .. 0.4 in the
+    # positions).  The library recovers positions only below a bound of 16 and
+    # otherwise replays each segment from a checkpoint; `recovered` records
+    # which side of the bound each case sits on, so both paths are covered.
     T = cpab_for(tess)
     nd = len(tess)
     theta = seeded_theta(T, 2, scale, 110 + nd)
@@ -227,6 +239,8 @@ def test_backward_parity_strong_field(cuda, tess, kind, scale):
         pts = meshgrid([64, 48] if nd == 2 else [17, 13, 11])
     g = np.random.default_rng(112).standard_normal((2, nd, pts.shape[-1])).astype(np.float32)
     As, mom, gp = _backward_case(T, theta, pts, g, cuda)
+    growth = recover_growth(As)
+    assert ((growth <= 16.0).all() if recovered else (growth > 16.0).all()), growth
     ref_m, ref_gp = orc.backward(pts, As, g, tess, 50)
     assert_adjoint_close(gp, ref_gp)
     assert_grad_close(mom, ref_m, rtol=2e-5)
@@ -392,10 +406,14 @@ def test_interp_unaligned_grid(cuda):
     np.testing.assert_array_equal(gg.cpu().numpy(), rg)
 
 
-@pytest.mark.parametrize("tess,kind,adaptive", [([50], "line", 0), ([16, 16], "mesh", 0),
-                                                ([16, 16], "batched", 1), ([4, 4, 4], "uniform", 0),
-                                                ([10, 10, 10], "mesh", 0)])
-def test_chain_matches_stagewise(cuda, tess, kind, adaptive):
+@pytest.mark.parametrize("tess,kind,adaptive,scale", [([50], "line", 0, 0.3), ([16, 16], "mesh", 0, 0.3),
+                                                      ([16, 16], "batched", 1, 0.3),
+                                                      ([4, 4, 4], "uniform", 0, 0.3),
+                                                      ([10, 10, 10], "mesh", 0, 0.3),
+                                                      # strong stages: checkpoint replay
+                                                      ([16, 16], "mesh", 0, 5.0),
+                                                      ([50], "line", 0, 6.0)])
+def test_chain_matches_stagewise(cuda, tess, kind, adaptive, scale):
     # cpab_chain_forward / cpab_chain_backward against the stage-by-stage
     # composition the reference's transform_grid_chain performs
     # (cpab/cpab.py:270-278): stage outputs and stage inputs bit-exact; the
@@ -405,7 +423,7 @@ def test_chain_matches_stagewise(cuda, tess, kind, adaptive):
     p = T.params
     nd = len(tess)
     K, nb = 3, 2
-    theta = (np.random.default_rng(81).standard_normal((K * nb, p.d)) * 0.3).astype(np.float32)
+    theta = (np.random.default_rng(81).standard_normal((K * nb, p.d)) * scale).astype(np.float32)
     if kind == "line":
         pts = np.linspace(0, 1, 3000, dtype=np.float32)[None]
     elif kind == "mesh":
@@ -425,6 +443,8 @@ def test_chain_matches_stagewise(cuda, tess, kind, adaptive):
                            out, sp)
     A = As.cpu().numpy().reshape(K, nb, p.nC, nd, nd + 1)
     R = Tr.cpu().numpy().reshape(K, nb, p.nC, nd, nd + 1)
+    if scale > 1.0:
+        assert (recover_growth(A.reshape(K * nb, p.nC, nd, nd + 1)) > 16.0).all()
     xs = [pts]
     for s in range(K):
         if nd == 1:
@@ -458,16 +478,20 @@ def _image_order(x, outs):
     return np.ascontiguousarray(sp.transpose(0, 1, *range(nd + 1, 1, -1))).reshape(B, nd, -1)
 
 
-@pytest.mark.parametrize("tess,ins,outs,adaptive", [([10], (50,), (70,), 0),
-                                                    ([6, 5], (40, 48), (36, 44), 0),
-                                                    ([6, 5], (40, 48), (36, 44), 1),
-                                                    ([3, 3, 3], (10, 12, 9), (11, 9, 13), 0),
-                                                    # last axis % 16 == 0 and the one before % 4 == 0:
-                                                    # the tiled walk
-                                                    ([6, 5], (40, 48), (36, 48), 0),
-                                                    ([6, 5], (40, 48), (20, 32), 1),
-                                                    ([3, 3, 3], (10, 12, 9), (6, 8, 32), 0)])
-def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive):
+@pytest.mark.parametrize("tess,ins,outs,adaptive,scale", [([10], (50,), (70,), 0, 0.5),
+                                                          ([6, 5], (40, 48), (36, 44), 0, 0.5),
+                                                          ([6, 5], (40, 48), (36, 44), 1, 0.5),
+                                                          ([3, 3, 3], (10, 12, 9), (11, 9, 13), 0, 0.5),
+                                                          # last axis % 16 == 0 and the one before
+                                                          # % 4 == 0: the tiled walk
+                                                          ([6, 5], (40, 48), (36, 48), 0, 0.5),
+                                                          ([6, 5], (40, 48), (20, 32), 1, 0.5),
+                                                          ([3, 3, 3], (10, 12, 9), (6, 8, 32), 0, 0.5),
+                                                          # strong fields: checkpoint replay
+                                                          ([6, 5], (40, 48), (36, 48), 0, 5.0),
+                                                          ([3, 3, 3], (10, 12, 9), (6, 8, 32), 0, 8.0),
+                                                          ([10], (50,), (70,), 0, 6.0)])
+def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive, scale):
     # cpab_transform_data_forward / _backward against the unfused composition
     # the reference runs (transform_grid of the meshgrid, interpolate, and the
     # autograd backward through both): image and final points bit-exact,
@@ -476,7 +500,7 @@ def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive):
     p = T.params
     nd = len(tess)
     B, C = 2, 2
-    theta = seeded_theta(T, B, 0.5, 91)
+    theta = seeded_theta(T, B, scale, 91)
     rng = np.random.default_rng(92)
     data = rng.random((B, C, *ins)).astype(np.float32)
     grid = T.uniform_meshgrid(list(outs))
@@ -490,6 +514,8 @@ def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive):
         ik = (np.arange(int(np.prod(outs))) // int(np.prod(outs[:k]))) % outs[k]
         np.testing.assert_array_equal(ax_np[offs[k] + ik], grid_np[k])
     As = _As_gpu(T, theta, cuda)
+    if scale > 1.0:
+        assert (recover_growth(As.cpu().numpy()) > 16.0).all()
     Tr = torch.empty_like(As)
     native().expm(nd, As, 1.0 / 50, Tr)
     out = torch.empty((B, C, *outs), device=cuda)
