@@ -36,6 +36,8 @@ _SIGNATURES = {
     "cpab_backward_workspace_size": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int]),
     "cpab_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int,
                                _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp]),
+    "cpab_backward_noalloc": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                       _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "cpab_chain_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
                                     _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                     _c_vp]),
@@ -162,6 +164,16 @@ class Native:
                                       int(adaptive), _ptr(points), _ptr(As), _ptr(grad_out),
                                       _ptr(moments), _ptr(grad_points), _ptr(workspace), wbytes,
                                       _stream(points.device)), "cpab_backward")
+
+    def backward_noalloc(self, ndim, points, batched, n_theta, nP, T, nc, adaptive, As, grad_out,
+                         moments, grad_points):
+        """cpab_backward without a caller workspace (the library's per-GPU
+        scratch array; calls on one GPU must not overlap)."""
+        ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
+        _check(self.lib.cpab_backward_noalloc(ndim, nP, n_theta, int(batched), int(T), ncx, ncy,
+                                              ncz, int(adaptive), _ptr(points), _ptr(As),
+                                              _ptr(grad_out), _ptr(moments), _ptr(grad_points),
+                                              _stream(points.device)), "cpab_backward_noalloc")
 
     def chain_forward(self, ndim, points, batched, n_batch, n_stages, nP, T, nc, adaptive, Trels,
                       As, out, stage_points):

@@ -317,11 +317,13 @@ int64_t workspace_size_impl(int ndim, int64_t nP, int64_t n_batch, int K, int nC
   return std::max(a, b);
 }
 
+// `timing`: record the backward kernel with the optional HIP-event timing
+// (off for the allocation-free entry point: the event pool may create events).
 int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int batched, int K,
                   int nstepsolver, int ncx, int ncy, int ncz, int adaptive, const float* points,
                   const float* stage_points, const float* As, const float* grad_out,
                   float* moments, float* grad_points, void* workspace, int64_t workspace_bytes,
-                  void* stream) {
+                  void* stream, bool timing = true) {
   cpab::Geometry g{};
   int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
   if (rc) return rc;
@@ -357,7 +359,7 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
                  who);
   if (rc) return rc;
   hipEvent_t ev;
-  const bool timed = prof_begin(s, &ev);
+  const bool timed = timing && prof_begin(s, &ev);
   rc = check_hip(cpab::launch_backward(g, nP, n_batch, batched ? 1 : 0, nstepsolver, K, adaptive,
                                        points, stage_points, As, G, amp, grad_out, moments,
                                        partials, dense, lam, grad_points, cfg, s),
@@ -368,6 +370,42 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
                                                nstepsolver, partials, dense, As, moments,
                                                s),
                    who);
+}
+
+// ---- allocation-free backward --------------------------------------------
+// The workspace of cpab_backward_noalloc: one array per GPU, in the library's
+// code object.  Host code never passes `scratch` itself (in host code the name
+// is only a stand-in, not a device address): each device's address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+constexpr int64_t kScratchBytes = CPAB_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// Device address of this device's `scratch` (nullptr after an error, with the
+// message set).
+void* scratch_on_current_device() {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    check_hip(e, "cpab_backward_noalloc: hipGetDevice");
+    return nullptr;
+  }
+  if (dev < 0 || dev >= 64) {
+    fail(CPAB_ERR_DEVICE, "cpab_backward_noalloc: device %d beyond the supported 64", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      check_hip(e != hipSuccess ? e : hipErrorInvalidSymbol, "cpab_backward_noalloc: hipGetSymbolAddress");
+      return nullptr;
+    }
+    addr[dev] = p;
+  }
+  return addr[dev];
 }
 
 // Image geometry of the fused transform_data calls (validated like the
@@ -503,6 +541,34 @@ int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nsteps
   return backward_impl("cpab_backward", ndim, nP, n_theta, batched, 1, nstepsolver, ncx, ncy, ncz,
                        adaptive, points, nullptr, As, grad_out, moments, grad_points, workspace,
                        workspace_bytes, stream);
+}
+
+int cpab_backward_noalloc(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
+                          int ncx, int ncy, int ncz, int adaptive, const float* points,
+                          const float* As, const float* grad_out, float* moments,
+                          float* grad_points, void* stream) {
+  // The size check needs only the geometry; backward_impl repeats the full
+  // validation before anything is enqueued.
+  cpab::Geometry g{};
+  int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
+  if (rc) return rc;
+  if ((rc = check_steps(nstepsolver))) return rc;
+  if ((rc = check_points(nP, n_theta, ndim))) return rc;
+  if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
+  if (n_theta > 0 && nP > 0) {
+    const int64_t need =
+        backward_workspace(g, nP, n_theta, 1, backward_cfg(g, nP, n_theta, nstepsolver, adaptive)).total;
+    if (need > kScratchBytes)
+      return fail(CPAB_ERR_INVALID,
+                  "cpab_backward_noalloc: this problem needs %lld bytes of workspace, beyond the "
+                  "%lld-byte no-allocation limit; use cpab_backward with a workspace",
+                  (long long)need, (long long)kScratchBytes);
+  }
+  void* ws = scratch_on_current_device();
+  if (ws == nullptr) return CPAB_ERR_DEVICE;
+  return backward_impl("cpab_backward_noalloc", ndim, nP, n_theta, batched, 1, nstepsolver, ncx,
+                       ncy, ncz, adaptive, points, nullptr, As, grad_out, moments, grad_points, ws,
+                       kScratchBytes, stream, /*timing=*/false);
 }
 
 int cpab_chain_backward(int ndim, int64_t nP, int64_t n_batch, int batched, int n_stages,

@@ -110,6 +110,25 @@ int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nsteps
                   float* grad_points, void* workspace, int64_t workspace_bytes,
                   void* stream);
 
+/* Device memory the library keeps per GPU for cpab_backward_noalloc. */
+#define CPAB_NOALLOC_SCRATCH_BYTES (32LL << 20)
+
+/* Allocation-free cpab_backward.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * results and kernels as cpab_backward without the workspace: the workspace
+ * is a library-owned device array of CPAB_NOALLOC_SCRATCH_BYTES on each GPU
+ * (held until the process ends), and the call allocates nothing.  Problems
+ * whose cpab_backward_workspace_size(...) exceeds it are rejected with
+ * CPAB_ERR_INVALID before anything is enqueued.  Every call on one GPU uses
+ * that GPU's one array: calls that overlap on a GPU (other streams, other
+ * host threads) race and must be serialised by the caller.  Kernel timing
+ * (cpab_profile_enable) does not cover these calls. */
+int cpab_backward_noalloc(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
+                          int ncx, int ncy, int ncz, int adaptive, const float* points,
+                          const float* As, const float* grad_out, float* moments,
+                          float* grad_points, void* stream);
+
 /* Chain of n_stages transforms (cpab/cpab.py:237-280, Cpab.transform_grid_chain:
  * stage s maps the output of stage s-1 with theta_chain[s]; the reference runs
  * one cpab_gpu.forward per stage from a Python loop).  Tables hold
