@@ -20,6 +20,13 @@ ships no tests or golden vectors for this path, and its CUDA cannot run here):
   forward_closed_1d   scipy solve_ivp of the ODE; order preservation
   backward            float64 finite differences of the midpoint scheme
                       (1D/2D/3D); closed form at theta = 0; linearity in the seed
+  adaptive substeps   (forward_trels / forward_midpoint / backward with
+                      adaptive=True) one corrected step against an independent
+                      float64 evaluation of p + (h/2)(A_c[p;1] + A_ce[q;1]) with a
+                      different field per cell (1D/2D/3D); bit-identity with the
+                      plain scheme on trajectories that never cross (and for the
+                      backward at T = 1); the bound on the corrected endpoint's
+                      offset for a cell-independent field
   interp_forward/     textbook bilinear; torch grid_sample (align_corners=True,
   interp_backward     border padding); finite differences
   (basis, host code)  fixtures written by the reference's tesselation.py

@@ -161,6 +161,133 @@ def test_adjoint_matches_finite_differences(nd, tess, scale):
     assert abs(fd_p - an_p) <= 1e-6 * max(1.0, abs(an_p)), (fd_p, an_p)
 
 
+# ---- adaptive substeps (Heun correction on a cell crossing) -----------------
+# cpab_ops_2d.cu:202-219 (Trels forward) and :294-332 (midpoint replay of the
+# backward), cpab_ops_1d.cu:229-261, cpab_ops_3d.cu:209-225: a step whose
+# endpoint q lies in another cell ce is replaced by p + (h/2) (A_c [p;1] +
+# A_ce [q;1]).  Pinned below by an independent float64 evaluation of one step
+# (T = 1, so h = 1) with a different field in every cell, by the identity of
+# adaptive and plain stepping on trajectories that never cross, and by the
+# order of the corrected step for a cell-independent field.
+
+def _step_cases(nd):
+    tess = {1: [6], 2: [4, 3], 3: [2, 3, 2]}[nd]
+    nC = {1: 6, 2: 48, 3: 60}[nd]
+    rng = np.random.default_rng(120 + nd)
+    As = rng.standard_normal((1, nC, nd, nd + 1)) * {1: 0.25, 2: 0.25, 3: 0.06}[nd]
+    pts = 0.05 + 0.9 * rng.random((nd, 400))
+    return tess, As, pts
+
+
+def _vel(A, p):
+    """A [nP, nd, nd+1] applied to p [nd, nP]: velocity [nd, nP] (float64)."""
+    return np.einsum("nij,jn->in", A[:, :, :-1], p) + A[:, :, -1].T
+
+
+@pytest.mark.parametrize("nd", [1, 2, 3])
+def test_adaptive_replay_step_closed_form(nd):
+    tess, As, pts = _step_cases(nd)
+    out = orc.forward_midpoint(pts, As, tess, 1, adaptive=True, dtype=np.float64)[0]
+    c = orc.cells(nd, pts, tess)
+    A0 = As[0, c]
+    q = pts + _vel(A0, pts + 0.5 * _vel(A0, pts))   # explicit midpoint, h = 1
+    ce = orc.cells(nd, q, tess)
+    cross = ce != c
+    heun = pts + 0.5 * (_vel(A0, pts) + _vel(As[0, ce], q))
+    ref = np.where(cross[None], heun, q)
+    assert 20 < cross.sum() < 380, cross.sum()   # both branches exercised
+    np.testing.assert_allclose(out, ref, rtol=0, atol=1e-14)
+    plain = orc.forward_midpoint(pts, As, tess, 1, adaptive=False, dtype=np.float64)[0]
+    np.testing.assert_allclose(plain, q, rtol=0, atol=1e-14)
+    assert np.abs(out - plain)[:, cross].max() > 1e-6   # the correction changes crossing steps
+
+
+@pytest.mark.parametrize("nd", [2, 3])
+def test_adaptive_trels_step_closed_form(nd):
+    tess, As, pts = _step_cases(nd)
+    Tr = np.stack([sla.expm(_aug(A))[:nd] for A in As[0]])[None]   # h = 1
+    out = orc.forward_trels(pts, Tr, As, tess, 1, adaptive=True, dtype=np.float64)[0]
+    c = orc.cells(nd, pts, tess)
+    s = _vel(Tr[0, c], pts)   # the one-step map applied like a velocity: Tr [p; 1]
+    ce = orc.cells(nd, s, tess)
+    cross = ce != c
+    heun = pts + 0.5 * (_vel(As[0, c], pts) + _vel(As[0, ce], s))
+    ref = np.where(cross[None], heun, s)
+    assert 20 < cross.sum() < 380, cross.sum()
+    np.testing.assert_allclose(out, ref, rtol=0, atol=1e-13)
+
+
+@pytest.mark.parametrize("nd,tess", [(1, [50]), (2, [20, 20]), (3, [4, 4, 4])])
+def test_adaptive_identical_without_crossings(nd, tess):
+    # Trajectories that never change cell take no correction: forward, replay
+    # and backward (moments and point adjoints) are bit-identical with and
+    # without adaptive substeps.  The backward's reverse sweep differentiates
+    # the plain midpoint step in each visited cell either way, so with T = 1
+    # (one step, at the start point) the two backwards agree even on crossings.
+    T = cpab_for(tess)
+    p = T.params
+    th = (np.random.default_rng(130 + nd).standard_normal((2, p.d)) * 0.5).astype(np.float32)
+    As = orc.affine(th, p.basis).reshape(2, p.nC, nd, nd + 1)
+    pts = uniform_points(nd, 4000, 131)
+    end, cl = orc.forward_midpoint(pts, As, tess, 50, return_cells=True)
+    # no cell change under either theta, the last step's endpoint included
+    still = ((cl == cl[:, :, :1]).all(axis=2) &
+             (np.stack([orc.cells(nd, e, tess) for e in end]) == cl[:, :, 0])).all(axis=0)
+    assert 100 < still.sum() < 4000
+    q = np.ascontiguousarray(pts[:, still])
+    g = np.random.default_rng(132).standard_normal((2, nd, q.shape[1])).astype(np.float32)
+    np.testing.assert_array_equal(orc.forward_midpoint(q, As, tess, 50, adaptive=True),
+                                  orc.forward_midpoint(q, As, tess, 50))
+    m1, l1 = orc.backward(q, As, g, tess, 50, adaptive=True)
+    m0, l0 = orc.backward(q, As, g, tess, 50)
+    np.testing.assert_array_equal(m1, m0)
+    np.testing.assert_array_equal(l1, l0)
+    if nd > 1:
+        Tr = orc.expm(nd, As, 1.0 / 50)
+        end, ct = orc.forward_trels(pts, Tr, As, tess, 50, return_cells=True)
+        keep = ((ct == ct[:, :, :1]).all(axis=2) &
+                (np.stack([orc.cells(nd, e, tess) for e in end]) == ct[:, :, 0])).all(axis=0)
+        fixed = np.ascontiguousarray(pts[:, keep])
+        np.testing.assert_array_equal(orc.forward_trels(fixed, Tr, As, tess, 50, adaptive=True),
+                                      orc.forward_trels(fixed, Tr, As, tess, 50))
+    g_all = np.random.default_rng(133).standard_normal((2, nd, pts.shape[1])).astype(np.float32)
+    m1, l1 = orc.backward(pts, As, g_all, tess, 1, adaptive=True)
+    m0, l0 = orc.backward(pts, As, g_all, tess, 1)
+    np.testing.assert_array_equal(m1, m0)
+    np.testing.assert_array_equal(l1, l0)
+
+
+def test_adaptive_uniform_field_order():
+    # One field in every cell: a corrected step is trapezoidal with the exact
+    # (Trels) or midpoint endpoint.  For linear fields that is
+    #   Trels:    I + hM + h^2M^2/2 + h^3M^3/4 + ...   (exact flow: h^3 M^3 / 6)
+    #   midpoint: I + hM + h^2M^2/2 + h^3M^3/4          (midpoint: no h^3 term)
+    # so with k corrected steps the endpoint moves from the plain one by about
+    # k h^3 ||M^3 p|| / 12 (Trels) or / 4 (midpoint), and never more.
+    nd, tess, T = 2, [6, 6], 20
+    A = np.array([[0.9, -1.3, 0.2], [1.1, 0.4, -0.3]])
+    As = np.broadcast_to(A, (1, 4 * 36, 2, 3)).copy()
+    pts = 0.2 + 0.6 * uniform_points(2, 500, 134).astype(np.float64)
+    h = 1.0 / T
+    M = _aug(A)
+    ph = np.vstack([pts, np.ones(500)])
+    bound = (h ** 3) * np.linalg.norm(np.linalg.matrix_power(M, 3), 2) * np.linalg.norm(ph, axis=0)
+    Tr = np.broadcast_to(sla.expm(h * M)[:2], As.shape).copy()
+    out_t, ct = orc.forward_trels(pts, Tr, As, tess, T, adaptive=True, return_cells=True,
+                                  dtype=np.float64)
+    plain_t = orc.forward_trels(pts, Tr, As, tess, T, dtype=np.float64)
+    k = (np.diff(ct[0], axis=1) != 0).sum(axis=1) + 1   # steps that may have been corrected
+    growth = np.exp(np.linalg.norm(M, 2))
+    d = np.linalg.norm(out_t[0] - plain_t[0], axis=0)
+    assert (d <= growth * k * bound / 12 * 1.01 + 1e-13).all()
+    assert d.max() > 0
+    out_m = orc.forward_midpoint(pts, As, tess, T, adaptive=True, dtype=np.float64)
+    plain_m = orc.forward_midpoint(pts, As, tess, T, dtype=np.float64)
+    d = np.linalg.norm(out_m[0] - plain_m[0], axis=0)
+    assert (d <= growth * k * bound / 4 * 1.01 + 1e-13).all()
+    assert d.max() > 0
+
+
 def test_moments_closed_form_at_zero_theta():
     # theta = 0: lambda stays g and p stays p0, so M_c = sum_{n in c} g_n [p_n; 1]^T
     # (T*h = 1) and grad_points = g.
