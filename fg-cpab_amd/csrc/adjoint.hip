@@ -44,8 +44,8 @@
 //              HBM with global atomics.  Flushes that find no slot go
 //              straight to HBM.  The HBM table holds sums S; a separate pass
 //              forms the moments in place.
-//   global     every flush is a global_atomic_add_f32, pre-aggregated across
-//              the wave for lanes that share a cell.
+// The cache takes at most 104 KiB of LDS (3D), within the 160 KiB a gfx950
+// workgroup may use, so every tessellation runs one of the two.
 #include <hip/hip_runtime.h>
 #include <algorithm>
 #include <cmath>
@@ -182,7 +182,7 @@ __device__ __forceinline__ float stack_pop(float (&a)[N]) {
   return v;
 }
 
-enum Bins { kBinsGlobal = 0, kBinsFull = 1, kBinsCache = 2 };
+enum Bins { kBinsFull = 1, kBinsCache = 2 };
 
 template <int P>
 __device__ __forceinline__ void flush_lds(float* bins, int c, const float (&m)[P]) {
@@ -274,41 +274,6 @@ __device__ __forceinline__ void wg_range(int nP, int& lo, int& hi) {
   hi = (int)std::min<int64_t>(l + span, nP);
 }
 
-// Global flush for a converged wave (all 64 lanes active; `need` marks the
-// lanes that flush).  Lanes flushing the same cell are summed with a
-// wave-wide butterfly and the lowest of them issues the atomics, which is
-// what cpab_ops_2d.cu:6-59 does with __match_any_sync.  A readfirstlane /
-// ballot loop peels one cell group at a time; once the next group is small
-// (incoherent points) every remaining lane adds its own values instead.
-template <int P>
-__device__ __forceinline__ void flush_global(float* __restrict__ mom, bool need, int c,
-                                             const float (&m)[P]) {
-  const int lane = __lane_id();
-  uint64_t todo = __ballot(need);
-  while (todo) {
-    const int leader = __ffsll((unsigned long long)todo) - 1;
-    const int lc = __shfl(c, leader);
-    const bool in = need && c == lc;
-    const uint64_t grp = __ballot(in) & todo;
-    if (__popcll(grp) < 4) {
-      if ((todo >> lane) & 1) {
-#pragma unroll
-        for (int k = 0; k < P; ++k) unsafeAtomicAdd(mom + (size_t)P * c + k, m[k]);
-      }
-      break;
-    }
-    todo &= ~grp;
-#pragma unroll
-    for (int k = 0; k < P; ++k) {
-      float v = in ? m[k] : 0.0f;
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-      if (lane == leader) unsafeAtomicAdd(mom + (size_t)P * lc + k, v);
-    }
-  }
-}
-
-
 // Where the trajectories of one stage start and where their adjoint seed
 // comes from.  PlainIO: point and seed arrays [D, nP] (cpab_backward, chain
 // stages).  ImageIO: the fused transform_data backward, where point q is an
@@ -398,9 +363,9 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
   const float h = 1.0f / (float)T;
   const float hh = h * 0.5f;
   const int nseg = (T + kSeg - 1) / kSeg;
-  // The loop bound is uniform so every wave stays converged (the global flush
-  // needs all 64 lanes); lanes past the range replay a clamped point and
-  // contribute nothing.
+  // The loop bound is uniform so every wave stays converged (the last flush
+  // pre-adds runs of lanes across the wave); lanes past the range replay a
+  // clamped point and contribute nothing.
   int lo, hi;
   wg_range(nP, lo, hi);
   for (int base = lo; base < hi; base += blockDim.x) {
@@ -461,10 +426,8 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
           const bool need = valid && c != prev && prev >= 0;
           if (BINS == kBinsFull) {
             if (need) flush_lds<PP>(bins, prev, m);
-          } else if (BINS == kBinsCache) {
-            if (need) flush_cache<PP>(keys, bins, mom_b, prev, m);
           } else {
-            flush_global<PP>(mom_b, need, prev, m);
+            if (need) flush_cache<PP>(keys, bins, mom_b, prev, m);
           }
           if (c != prev) {
 #pragma unroll
@@ -475,12 +438,12 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
         }
       }
     }
-    if (BINS == kBinsFull) {
-      if (valid) flush_lds<PP>(bins, prev, m);
-    } else if (BINS == kBinsCache) {
-      if (valid) flush_cache<PP>(keys, bins, mom_b, prev, m);
-    } else {
-      flush_global<PP>(mom_b, valid, prev, m);
+    float r[PP];
+    bool on;
+    wave_run_sums<PP>(valid, prev, m, r, on);
+    if (on) {
+      if (BINS == kBinsFull) flush_lds<PP>(bins, prev, r);
+      else flush_cache<PP>(keys, bins, mom_b, prev, r);
     }
     io.finish(pi, valid, lam);
   }
@@ -634,11 +597,11 @@ struct StageLds {
     if (BINS == kBinsFull) {
       for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
       if (threadIdx.x == 0) *touched_cnt = 0;
-    } else if (BINS == kBinsCache) {
+    } else {
       for (int i = threadIdx.x; i < kCacheSlots; i += blockDim.x) keys[i] = -1;
       for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) bins[i] = 0.0f;
     }
-    if (LDS_A || BINS != kBinsGlobal) __syncthreads();
+    __syncthreads();
   }
   // After every lane is done: full bins -> a dense workgroup's table into its
   // partial (and its bit `part` into the row's dense-part mask), a sparse
@@ -648,7 +611,7 @@ struct StageLds {
                                       uint64_t* __restrict__ dense_parts, int part,
                                       float* __restrict__ mom_b, int nC, int* touched_cnt) const {
     constexpr int PP = Dim<D>::P;
-    if (LDS_A || BINS != kBinsGlobal) __syncthreads();
+    __syncthreads();
     if (BINS == kBinsFull) {
       auto cell_touched = [&](int i) {
         bool t = false;
@@ -673,7 +636,7 @@ struct StageLds {
           for (int k = 0; k < PP; ++k) unsafeAtomicAdd(mom_b + (size_t)i * PP + k, bins[i * PP + k]);
         }
       }
-    } else if (BINS == kBinsCache) {
+    } else {
       for (int i = threadIdx.x; i < kCacheSlots * PP; i += blockDim.x) {
         const int slot = i / PP;
         const int c = keys[slot];
@@ -710,7 +673,6 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
                                           const IO& io, float* __restrict__ mom_b,
                                           const Recover& rec, size_t row) {
   if constexpr (TS > 0) {
-    static_assert(BINS != kBinsGlobal, "the register variant accumulates in LDS");
     if constexpr (!ADAPTIVE) {
       // Rows whose inverse maps could amplify the recovered positions' rounding
       // beyond kRecoverGrowth replay each segment from a checkpoint instead.
@@ -729,8 +691,8 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
   }
 }
 
-// TS == 0: segmented variant; TS > 0: register variant (full LDS bins or the
-// LDS cell cache, no global-atomic flushes).
+// TS == 0: segmented variant; TS > 0: register variant.  Both accumulate in
+// full LDS bins or the LDS cell cache.
 // One workgroup = one theta (blockIdx.y) x one contiguous point range
 // (blockIdx.x).  A chain of K stages (Cpab.transform_grid_chain) runs its
 // stages last to first inside the kernel: stage k reads its input points from
@@ -781,7 +743,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kerne
     const size_t part = row * gridDim.x + blockIdx.x;
     L.end(partials + part * R, dense_parts + row * ((gridDim.x + 63) / 64), (int)blockIdx.x,
           moments + row * R, nC, &touched_cnt);
-    if (k > 0 && (LDS_A || BINS != kBinsGlobal)) __syncthreads();
+    if (k > 0) __syncthreads();
   }
 }
 
@@ -875,39 +837,32 @@ hipError_t go(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
 template <int D>
 hipError_t dispatch(const BackwardJob& j, int adaptive, const LaunchCfg& cfg, hipStream_t s) {
 #define CPAB_GO(AD, LA, LB, TS) return go<D, AD, LA, LB, TS>(j, cfg, s)
-  if constexpr (D <= 2) {
-    if (cfg.reg_steps == kRegSteps && j.T == kRegSteps && cfg.lds_bins) {
-      const int key = (adaptive ? 2 : 0) | (cfg.lds_table ? 1 : 0);
-      switch (key) {
-        case 0: CPAB_GO(false, false, kBinsFull, kRegSteps);
-        case 1: CPAB_GO(false, true, kBinsFull, kRegSteps);
-        case 2: CPAB_GO(true, false, kBinsFull, kRegSteps);
-        default: CPAB_GO(true, true, kBinsFull, kRegSteps);
+  // Register variant (the launch policy asks for it with full bins in 1D/2D,
+  // and without adaptive substeps in 3D, whose 150 VGPRs of trajectory leave
+  // no room for the adaptive step).
+  if (cfg.reg_steps == kRegSteps && j.T == kRegSteps) {
+    if constexpr (D <= 2) {
+      if (cfg.lds_bins) {
+        if (adaptive) CPAB_GO(true, false, kBinsFull, kRegSteps);
+        CPAB_GO(false, false, kBinsFull, kRegSteps);
+      }
+    } else {
+      if (!adaptive) {
+        if (cfg.lds_bins) CPAB_GO(false, false, kBinsFull, kRegSteps);
+        CPAB_GO(false, false, kBinsCache, kRegSteps);
       }
     }
-  } else {
-    // 3D: 150 VGPRs of trajectory; the adaptive step does not fit beside it.
-    if (!adaptive && cfg.reg_steps == kRegSteps && j.T == kRegSteps &&
-        (cfg.lds_bins || cfg.lds_cache)) {
-      if (cfg.lds_bins) CPAB_GO(false, false, kBinsFull, kRegSteps);
-      CPAB_GO(false, false, kBinsCache, kRegSteps);
-    }
   }
-  const int bins = cfg.lds_bins ? kBinsFull : (cfg.lds_cache ? kBinsCache : kBinsGlobal);
-  const int key = (adaptive ? 6 : 0) + (cfg.lds_table ? 3 : 0) + bins;
+  const int key = (adaptive ? 4 : 0) + (cfg.lds_table ? 2 : 0) + (cfg.lds_bins ? 1 : 0);
   switch (key) {
-    case 0: CPAB_GO(false, false, kBinsGlobal, 0);
+    case 0: CPAB_GO(false, false, kBinsCache, 0);
     case 1: CPAB_GO(false, false, kBinsFull, 0);
-    case 2: CPAB_GO(false, false, kBinsCache, 0);
-    case 3: CPAB_GO(false, true, kBinsGlobal, 0);
-    case 4: CPAB_GO(false, true, kBinsFull, 0);
-    case 5: CPAB_GO(false, true, kBinsCache, 0);
-    case 6: CPAB_GO(true, false, kBinsGlobal, 0);
-    case 7: CPAB_GO(true, false, kBinsFull, 0);
-    case 8: CPAB_GO(true, false, kBinsCache, 0);
-    case 9: CPAB_GO(true, true, kBinsGlobal, 0);
-    case 10: CPAB_GO(true, true, kBinsFull, 0);
-    default: CPAB_GO(true, true, kBinsCache, 0);
+    case 2: CPAB_GO(false, true, kBinsCache, 0);
+    case 3: CPAB_GO(false, true, kBinsFull, 0);
+    case 4: CPAB_GO(true, false, kBinsCache, 0);
+    case 5: CPAB_GO(true, false, kBinsFull, 0);
+    case 6: CPAB_GO(true, true, kBinsCache, 0);
+    default: CPAB_GO(true, true, kBinsFull, 0);
   }
 #undef CPAB_GO
 }

@@ -40,11 +40,6 @@ int check_hip(hipError_t e, const char* what) {
   return fail(CPAB_ERR_DEVICE, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
 }
 
-int env_int(const char* name, int dflt) {
-  const char* s = std::getenv(name);
-  return (s && *s) ? std::atoi(s) : dflt;
-}
-
 struct DeviceInfo {
   int cus = 0;
   int lds = 0;
@@ -65,7 +60,6 @@ DeviceInfo device_info() {
     d.lds = (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
                 ? v
                 : 64 * 1024;
-    d.lds = env_int("CPAB_LDS_BUDGET", d.lds);
   }
   return d;
 }
@@ -122,68 +116,68 @@ int check_points(int64_t nP, int64_t n_theta, int ndim) {
   } while (0)
 
 // ---- launch-shape policy ---------------------------------------------------
+// Fixed per problem shape and device (CU count, LDS per workgroup); each
+// choice below was measured on MI355X (sweeps over block size, workgroups per
+// CU and LDS staging).
 
 cpab::LaunchCfg forward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta) {
   const DeviceInfo dev = device_info();
-  const int64_t table = (int64_t)g.nC * g.ppc() * 4;
+  (void)g;
   cpab::LaunchCfg c{};
-  // The kernel keeps the current cell's map in registers and re-reads the
-  // table only when a lane changes cell, so the table is read through L1/L2 by
-  // default; staging it in LDS would cap occupancy for little gain.
-  c.lds_table = table <= dev.lds ? env_int("CPAB_FWD_LDS", 0) : 0;
-  c.block = std::min(1024, std::max(64, env_int("CPAB_FWD_BLOCK", 512) / 64 * 64));  // launch bound
-  const int64_t resident = c.lds_table ? std::max<int64_t>(1, std::min<int64_t>(2048 / c.block, dev.lds / std::max<int64_t>(table, 1)))
-                                       : std::max(1, 2048 / c.block);
-  // Two rounds of resident workgroups per CU.
-  const int64_t want = (int64_t)dev.cus * resident * env_int("CPAB_FWD_WAVES", 2);
+  // The kernels keep the current cell's map in registers and re-read the table
+  // only when a lane changes cell, through L1/L2.
+  c.block = 512;
+  // Two rounds of resident workgroups (2048 lanes per CU) per CU.
+  const int64_t want = (int64_t)dev.cus * (2048 / c.block) * 2;
   int64_t chunks = std::max<int64_t>(1, div_up(want, std::max<int64_t>(n_theta, 1)));
   chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
-  c.chunks = std::max(1, env_int("CPAB_FWD_CHUNKS", (int)chunks));
-  c.lds_bins = 0;
-  c.lds_cache = 0;
-  c.lds_chain = env_int("CPAB_FWD_LDS_CHAIN", 1) ? dev.lds : 0;
-  c.reg_steps = 0;
+  c.chunks = (int)chunks;
+  // 2D chains stage each stage's table in LDS when it fits.
+  c.lds_chain = dev.lds;
   return c;
 }
 
-cpab::LaunchCfg backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta, int T,
-                             int adaptive) {
+// Backward: full LDS bins when a theta's nC x ppc table fits in LDS, else the
+// hashed LDS cell cache (at most 104 KiB, 3D).  Register variant for T = 50
+// (cells, and with adaptive substeps positions, in VGPRs; one 1024-lane
+// workgroup per CU, 768 with adaptive substeps); otherwise the segmented
+// variant, with the affine table in LDS beside the bins when both fit.
+// Returns false (message set) if the device's LDS holds neither.
+bool backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta, int T, int adaptive,
+                  cpab::LaunchCfg* out) {
   const DeviceInfo dev = device_info();
   const int64_t table = (int64_t)g.nC * g.ppc() * 4;
-  cpab::LaunchCfg c{};
-  c.lds_bins = (table <= dev.lds) ? env_int("CPAB_BWD_LDS_BINS", 1) : 0;
-  // Table too large for LDS: hashed cell cache in LDS, flushed to HBM at the end.
   const int64_t cache = (int64_t)cpab::kCacheSlots * (g.ppc() + 1) * 4;
-  c.lds_cache = (!c.lds_bins && cache <= dev.lds) ? env_int("CPAB_BWD_CACHE", 1) : 0;
-  // Register variant: the trajectory's cells (and, with adaptive substeps, its
-  // positions) in VGPRs, one workgroup per CU; the per-cell tables are read
-  // through L1/L2 (re-read only when a lane changes cell).  Without adaptive
-  // substeps: 1024 threads (4 waves per SIMD); with them: 768 threads (3 waves
-  // per SIMD, the positions take D x 50 VGPRs).
-  const bool reg = T == cpab::kRegSteps && g.nC <= 65535 && env_int("CPAB_BWD_REG", 1) &&
-                   (g.ndim <= 2 ? c.lds_bins != 0 : (!adaptive && (c.lds_bins || c.lds_cache)));
+  cpab::LaunchCfg c{};
+  c.lds_bins = table <= dev.lds ? 1 : 0;
+  c.lds_cache = (!c.lds_bins && cache <= dev.lds) ? 1 : 0;
+  if (!c.lds_bins && !c.lds_cache) {
+    fail(CPAB_ERR_DEVICE, "the backward needs %lld bytes of LDS per workgroup, the device has %d",
+         (long long)cache, dev.lds);
+    return false;
+  }
+  const bool reg = T == cpab::kRegSteps && g.nC <= 65535 &&
+                   (g.ndim <= 2 ? c.lds_bins != 0 : !adaptive);
   c.reg_steps = reg ? cpab::kRegSteps : 0;
-  const int64_t used = c.lds_bins ? table : (c.lds_cache ? cache : 0);
-  c.lds_table = (used + table <= dev.lds) ? env_int("CPAB_BWD_LDS_TABLE", reg ? 0 : 1) : 0;
+  const int64_t used = c.lds_bins ? table : cache;
+  c.lds_table = (!reg && used + table <= dev.lds) ? 1 : 0;
   const int64_t lds = used + (c.lds_table ? table : 0);
-  const int limit = (reg && !adaptive) ? 1024 : 768;  // kernel launch bound
   int wg_per_cu;
   if (reg) {
-    c.block = env_int("CPAB_BWD_BLOCK", limit);
-    wg_per_cu = std::max(1, limit / std::max(1, c.block));
+    c.block = adaptive ? 768 : 1024;  // the kernel's launch bound
+    wg_per_cu = 1;
   } else {
-    // The cache variant runs one workgroup per CU (104 KiB of LDS in 3D): make
-    // it 12 waves.
-    c.block = env_int("CPAB_BWD_BLOCK", c.lds_cache ? 768 : 512);
-    wg_per_cu = std::max(1, 2048 / std::max(1, c.block));  // 32 waves per CU
-    if (lds > 0) wg_per_cu = (int)std::max<int64_t>(1, std::min<int64_t>(wg_per_cu, dev.lds / lds));
+    // 32 waves per CU as 512-lane workgroups, as many as LDS allows; the cache
+    // variant runs one workgroup per CU (104 KiB of LDS in 3D): 12 waves.
+    c.block = c.lds_cache ? 768 : 512;
+    wg_per_cu = (int)std::max<int64_t>(1, std::min<int64_t>(2048 / c.block, dev.lds / lds));
   }
-  c.block = std::min(limit, std::max(64, c.block / 64 * 64));
   const int64_t want = (int64_t)dev.cus * wg_per_cu;
   int64_t chunks = std::max<int64_t>(1, div_up(want, std::max<int64_t>(n_theta, 1)));
   chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
-  c.chunks = std::max(1, env_int("CPAB_BWD_CHUNKS", (int)chunks));
-  return c;
+  c.chunks = (int)chunks;
+  *out = c;
+  return true;
 }
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
@@ -312,9 +306,11 @@ int64_t workspace_size_impl(int ndim, int64_t nP, int64_t n_batch, int K, int nC
   g.ndim = ndim;
   g.nC = nC;
   // Whichever variant runs (register or segmented) fits.
-  const int64_t a = backward_workspace(g, nP, n_batch, K, backward_cfg(g, nP, n_batch, cpab::kRegSteps, 0)).total;
-  const int64_t b = backward_workspace(g, nP, n_batch, K, backward_cfg(g, nP, n_batch, 0, 1)).total;
-  return std::max(a, b);
+  cpab::LaunchCfg reg, seg;
+  if (!backward_cfg(g, nP, n_batch, cpab::kRegSteps, 0, &reg) || !backward_cfg(g, nP, n_batch, 0, 1, &seg))
+    return 0;
+  return std::max(backward_workspace(g, nP, n_batch, K, reg).total,
+                  backward_workspace(g, nP, n_batch, K, seg).total);
 }
 
 // `timing`: record the backward kernel with the optional HIP-event timing
@@ -342,7 +338,8 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(points, 4); CPAB_ALIGNED(grad_out, 4);
   CPAB_ALIGNED(workspace, 16);
   if (K > 1) CPAB_REQUIRE(stage_points);
-  const cpab::LaunchCfg cfg = backward_cfg(g, nP, n_batch, nstepsolver, adaptive);
+  cpab::LaunchCfg cfg;
+  if (!backward_cfg(g, nP, n_batch, nstepsolver, adaptive, &cfg)) return CPAB_ERR_DEVICE;
   const BackwardWorkspace w = backward_workspace(g, nP, n_batch, K, cfg);
   if (workspace == nullptr || workspace_bytes < w.total)
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
@@ -556,8 +553,9 @@ int cpab_backward_noalloc(int ndim, int64_t nP, int64_t n_theta, int batched, in
   if ((rc = check_points(nP, n_theta, ndim))) return rc;
   if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
   if (n_theta > 0 && nP > 0) {
-    const int64_t need =
-        backward_workspace(g, nP, n_theta, 1, backward_cfg(g, nP, n_theta, nstepsolver, adaptive)).total;
+    cpab::LaunchCfg cfg;
+    if (!backward_cfg(g, nP, n_theta, nstepsolver, adaptive, &cfg)) return CPAB_ERR_DEVICE;
+    const int64_t need = backward_workspace(g, nP, n_theta, 1, cfg).total;
     if (need > kScratchBytes)
       return fail(CPAB_ERR_INVALID,
                   "cpab_backward_noalloc: this problem needs %lld bytes of workspace, beyond the "
@@ -634,7 +632,8 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(workspace, 16);
   CPAB_REQUIRE(grad_out); CPAB_REQUIRE(moments);
   hipStream_t s = as_stream(stream);
-  const cpab::LaunchCfg cfg = backward_cfg(g, img.nP, n_batch, nstepsolver, adaptive);
+  cpab::LaunchCfg cfg;
+  if (!backward_cfg(g, img.nP, n_batch, nstepsolver, adaptive, &cfg)) return CPAB_ERR_DEVICE;
   const BackwardWorkspace w = backward_workspace(g, img.nP, n_batch, 1, cfg);
   if (workspace == nullptr || workspace_bytes < w.total)
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",

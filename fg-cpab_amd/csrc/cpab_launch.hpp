@@ -22,15 +22,15 @@ constexpr int kInterpTile0 = 32;
 constexpr int kInterpTileLast = 32;
 constexpr int kInterpThreads = 256;
 
-// Launch-shape knobs (chosen per problem by the C-ABI layer, overridable for tuning).
+// Launch shape, chosen per problem by the C-ABI layer (capi.cpp).
 struct LaunchCfg {
   int block;        // threads per workgroup
   int chunks;       // workgroups per theta (gridDim.x)
-  int lds_table;    // stage the per-theta cell table in LDS
-  int lds_bins;     // accumulate moments in full LDS bins (per-workgroup partials)
-  int lds_cache;    // else: accumulate in the hashed LDS cell cache (else global atomics)
+  int lds_table;    // backward, segmented variant: stage the per-theta affine table in LDS
+  int lds_bins;     // backward: accumulate moments in full LDS bins (per-workgroup partials)
+  int lds_cache;    // backward: else accumulate in the hashed LDS cell cache
   int reg_steps;    // backward: compile-time step count of the register variant (0 = segmented)
-  int lds_chain;    // forward: LDS bytes available for the per-stage table of a 2D chain (0 = off)
+  int lds_chain;    // forward: LDS bytes available for the per-stage table of a 2D chain
 };
 
 hipError_t launch_fill(float* dst, int64_t n, float value, hipStream_t s);

@@ -196,28 +196,25 @@ __device__ __forceinline__ void steps_3d(float& px, float& py, float& pz, float*
 }
 
 // PPT independent trajectories per lane give the scheduler two dependency
-// chains (lookup -> table read -> affine apply) to interleave.
+// chains (lookup -> table read -> affine apply) to interleave.  The per-cell
+// tables are read through L1/L2: a lane re-reads its cell's map only when some
+// lane of its wave changed cell, so staging the table in LDS bought nothing and
+// capped occupancy.
 //
 // K > 1 runs a chain (Cpab.transform_grid_chain): stage s integrates with the
 // tables of row (s * n_batch + b) of Trels / As, starting from the previous
 // stage's result; the input of every stage s >= 1 is saved to
-// stage_points[s-1] (if not null) for the backward.  LDS staging of the table
-// is used only for K == 1.
-template <bool ADAPTIVE, bool LDS, int PPT>
+// stage_points[s-1] (if not null) for the backward.
+template <bool ADAPTIVE, int PPT>
 __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T, int nx, int ny,
                                                     int K, const float* __restrict__ points,
                                                     const float* __restrict__ Trels,
                                                     const float* __restrict__ As,
                                                     float* __restrict__ out,
                                                     float* __restrict__ stage_points) {
-  extern __shared__ float lds[];
   const int b = blockIdx.y;
   const int n_batch = gridDim.y;
   const int nC = 4 * nx * ny;
-  if (LDS) {
-    stage(lds, Trels + (size_t)b * nC * 6, nC * 6);
-    __syncthreads();
-  }
   const float h = 1.0f / (float)T;
   const float hh = 0.5f * h;
   const float* __restrict__ pts = points + (batched ? (size_t)b * 2 * nP : 0);
@@ -246,7 +243,7 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
           }
         }
       }
-      steps_2d<ADAPTIVE, LDS, PPT>(px, py, lds, Tg, Ag, T, nx, ny, hh);
+      steps_2d<ADAPTIVE, false, PPT>(px, py, nullptr, Tg, Ag, T, nx, ny, hh);
     }  // stages
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
@@ -323,21 +320,16 @@ __global__ __launch_bounds__(1024) void chain2d_lds_kernel(int nP, int batched, 
   }
 }
 
-template <bool ADAPTIVE, bool LDS>
+template <bool ADAPTIVE>
 __global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T, int nx, int ny,
                                                     int nz, int K, const float* __restrict__ points,
                                                     const float* __restrict__ Trels,
                                                     const float* __restrict__ As,
                                                     float* __restrict__ out,
                                                     float* __restrict__ stage_points) {
-  extern __shared__ float lds[];
   const int b = blockIdx.y;
   const int n_batch = gridDim.y;
   const int nC = 5 * nx * ny * nz;
-  if (LDS) {
-    stage(lds, Trels + (size_t)b * nC * 12, nC * 12);
-    __syncthreads();
-  }
   const float h = 1.0f / (float)T;
   const float hh = 0.5f * h;
   const float* __restrict__ pts = points + (batched ? (size_t)b * 3 * nP : 0);
@@ -354,7 +346,7 @@ __global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T,
         sp[p + nP] = py;
         sp[p + 2 * (size_t)nP] = pz;
       }
-      steps_3d<ADAPTIVE, LDS>(px, py, pz, lds, Tg, Ag, T, nx, ny, nz, hh);
+      steps_3d<ADAPTIVE, false>(px, py, pz, nullptr, Tg, Ag, T, nx, ny, nz, hh);
     }  // stages
     o[p] = px;
     o[p + nP] = py;
@@ -515,9 +507,7 @@ hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_batch, int ba
   if (nP <= 0 || n_batch <= 0 || K <= 0) return hipSuccess;
   const dim3 grid((unsigned)cfg.chunks, (unsigned)n_batch), block((unsigned)cfg.block);
   const size_t tab = (size_t)g.nC * g.ppc() * sizeof(float);
-  const bool lds_table = cfg.lds_table && K == 1;
-  const size_t lds = lds_table ? tab : 0;
-  if (g.ndim == 2 && K > 1 && cfg.lds_chain && tab <= (size_t)cfg.lds_chain) {
+  if (g.ndim == 2 && K > 1 && tab <= (size_t)cfg.lds_chain) {
     // one pass over the points, one point per lane
     const int64_t need = (nP + (int64_t)cfg.block - 1) / (int64_t)cfg.block;
     const dim3 gridc((unsigned)need, (unsigned)n_batch);
@@ -529,37 +519,24 @@ hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_batch, int ba
                                       stage_points);
   }
   if (g.ndim == 2) {
-    if (adaptive) {
-      return lds_table
-                 ? launch_with_lds(fwd2d_kernel<true, true, 1>, grid, block, lds, s, (int)nP,
-                                   batched, T, g.nx, g.ny, K, points, Trels, As, out, stage_points)
-                 : launch_with_lds(fwd2d_kernel<true, false, 1>, grid, block, lds, s, (int)nP,
-                                   batched, T, g.nx, g.ny, K, points, Trels, As, out, stage_points);
-    }
+    if (adaptive)
+      return launch_with_lds(fwd2d_kernel<true, 1>, grid, block, 0, s, (int)nP, batched, T, g.nx,
+                             g.ny, K, points, Trels, As, out, stage_points);
     // Two points per lane: no more workgroups than it takes to cover nP once
     // (a lane's second point would otherwise duplicate work on a clamped index).
     const int64_t need = (nP + 2 * (int64_t)cfg.block - 1) / (2 * (int64_t)cfg.block);
     const dim3 grid2((unsigned)std::max<int64_t>(1, std::min<int64_t>(cfg.chunks, need)),
                      (unsigned)n_batch);
-    return lds_table
-               ? launch_with_lds(fwd2d_kernel<false, true, 2>, grid2, block, lds, s, (int)nP,
-                                 batched, T, g.nx, g.ny, K, points, Trels, As, out, stage_points)
-               : launch_with_lds(fwd2d_kernel<false, false, 2>, grid2, block, lds, s, (int)nP,
-                                 batched, T, g.nx, g.ny, K, points, Trels, As, out, stage_points);
+    return launch_with_lds(fwd2d_kernel<false, 2>, grid2, block, 0, s, (int)nP, batched, T, g.nx,
+                           g.ny, K, points, Trels, As, out, stage_points);
   }
   // 3D: the kernel takes nz as an extra argument.
   auto go = [&](auto kernel) -> hipError_t {
-    if (lds > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(kernel, grid, block, lds, s, (int)nP, batched, T, g.nx, g.ny, g.nz, K,
+    hipLaunchKernelGGL(kernel, grid, block, 0, s, (int)nP, batched, T, g.nx, g.ny, g.nz, K,
                        points, Trels, As, out, stage_points);
     return hipGetLastError();
   };
-  if (adaptive) return lds_table ? go(fwd3d_kernel<true, true>) : go(fwd3d_kernel<true, false>);
-  return lds_table ? go(fwd3d_kernel<false, true>) : go(fwd3d_kernel<false, false>);
+  return adaptive ? go(fwd3d_kernel<true>) : go(fwd3d_kernel<false>);
 }
 
 hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,

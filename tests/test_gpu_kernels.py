@@ -269,16 +269,13 @@ def test_backward_segmented_steps(cuda, tess, kind, nstep):
     assert_grad_close(mom, ref_m, rtol=2e-5)
 
 
-@pytest.mark.parametrize("mode", ["cache", "global"])
 @pytest.mark.parametrize("kind,n", [("mesh", 0), ("uniform", 120000)])
-def test_backward_3d_moment_paths(cuda, monkeypatch, mode, kind, n):
-    # [10,10,10]: the 5000 x 12 moment table does not fit in LDS.  "cache" is the
-    # hashed LDS cell cache: meshgrid points keep the cells of a workgroup few;
-    # 120k uniform points under one theta touch more distinct cells per
+def test_backward_3d_moment_paths(cuda, kind, n):
+    # [10,10,10]: the 5000 x 12 moment table does not fit in LDS, so sums go to
+    # the hashed LDS cell cache: meshgrid points keep the cells of a workgroup
+    # few; 120k uniform points under one theta touch more distinct cells per
     # workgroup than the cache has slots, so flushes also take the HBM
-    # fallback.  "global" switches the cache off (wave-aggregated HBM atomics).
-    if mode == "global":
-        monkeypatch.setenv("CPAB_BWD_CACHE", "0")
+    # fallback.
     T = cpab_for([10, 10, 10])
     theta = seeded_theta(T, 1, 0.5, 71)
     pts = meshgrid([40, 36, 30]) if kind == "mesh" else uniform_points(3, n, 72)
@@ -287,6 +284,46 @@ def test_backward_3d_moment_paths(cuda, monkeypatch, mode, kind, n):
     ref_m, ref_gp = orc.backward(pts, As, g, [10, 10, 10], 50)
     assert_adjoint_close(gp, ref_gp)
     assert_grad_close(mom, ref_m, rtol=2e-5)
+
+
+def _random_field_case(nc, n_theta, nP, scale, seed, mesh=None):
+    """Per-cell fields drawn independently (no basis: the kernels take any
+    table), for tessellations too large to build a basis for in a test."""
+    nd = len(nc)
+    nC = {1: nc[0], 2: 4 * nc[0] * nc[1], 3: 5 * int(np.prod(nc))}[nd]
+    rng = np.random.default_rng(seed)
+    As = (rng.standard_normal((n_theta, nC, nd, nd + 1)) * scale).astype(np.float32)
+    pts = meshgrid(mesh) if mesh else rng.random((nd, nP)).astype(np.float32)
+    g = rng.standard_normal((n_theta, nd, pts.shape[-1])).astype(np.float32)
+    return As, pts, g
+
+
+@pytest.mark.parametrize("nc,mesh,nstep", [
+    # 2D table beyond LDS (9216 cells x 6 floats = 221 KiB): the cell cache,
+    # segmented variant, for uniform points (cache misses go to HBM) and a mesh
+    ([48, 48], None, 50), ([48, 48], [80, 72], 50), ([48, 48], None, 37),
+    # 3D with more than 65535 cells: no register variant (16-bit cell ids), so
+    # the segmented variant with the cell cache
+    ([24, 24, 24], None, 50), ([24, 24, 24], [30, 28, 26], 50)])
+def test_backward_large_tessellations(cuda, nc, mesh, nstep):
+    nd = len(nc)
+    As_np, pts, g = _random_field_case(nc, 2, 20000, 0.4, 170 + nd, mesh)
+    nC = As_np.shape[1]
+    As = _dev(As_np, cuda)
+    Tr = torch.empty_like(As)
+    native().expm(nd, As, 1.0 / nstep, Tr)
+    nP = pts.shape[-1]
+    out = torch.empty((2, nd, nP), device=cuda)
+    native().forward(nd, _dev(pts, cuda), False, 2, nP, nstep, nc, 0, Tr, As, out)
+    np.testing.assert_array_equal(out.cpu().numpy(),
+                                  orc.forward_trels(pts, Tr.cpu().numpy(), As_np, nc, nstep))
+    mom = torch.empty((2, nC, nd * (nd + 1)), device=cuda)
+    gp = torch.empty((2, nd, nP), device=cuda)
+    ws = torch.empty(native().backward_workspace_size(nd, nP, 2, nC), dtype=torch.uint8, device=cuda)
+    native().backward(nd, _dev(pts, cuda), False, 2, nP, nstep, nc, 0, As, _dev(g, cuda), mom, gp, ws)
+    ref_m, ref_gp = orc.backward(pts, As_np, g, nc, nstep)
+    assert_adjoint_close(gp.cpu().numpy(), ref_gp)
+    assert_grad_close(mom.cpu().numpy(), ref_m, rtol=2e-5)
 
 
 @pytest.mark.parametrize("chain", [False, True])
