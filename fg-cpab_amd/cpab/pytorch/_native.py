@@ -36,6 +36,9 @@ _SIGNATURES = {
     "cpab_backward_workspace_size": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int]),
     "cpab_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int,
                                _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp]),
+    "cpab_backward_project": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                       _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp,
+                                       _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp]),
     "cpab_backward_noalloc": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
                                        _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "cpab_chain_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
@@ -43,15 +46,17 @@ _SIGNATURES = {
                                     _c_vp]),
     "cpab_chain_backward_workspace_size": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int, _c_int]),
     "cpab_chain_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
-                                     _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                                     _c_vp, _c_vp, _c_i64, _c_vp]),
+                                     _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_int,
+                                     _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
+                                     _c_vp]),
     "cpab_transform_data_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int,
                                              _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
                                              _c_vp, _c_vp, _c_vp]),
     "cpab_transform_data_backward_workspace_size": (_c_i64, [_c_int, _c_i64, _c_vp, _c_int]),
     "cpab_transform_data_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int,
                                               _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
-                                              _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp]),
+                                              _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                              _c_vp, _c_vp, _c_i64, _c_vp]),
     "cpab_project": (_c_int, [_c_i64, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "cpab_sum_batch": (_c_int, [_c_i64, _c_i64, _c_vp, _c_vp, _c_vp]),
     "cpab_interp_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
@@ -165,6 +170,18 @@ class Native:
                                       _ptr(moments), _ptr(grad_points), _ptr(workspace), wbytes,
                                       _stream(points.device)), "cpab_backward")
 
+    def backward_project(self, ndim, points, batched, n_theta, nP, T, nc, adaptive, As, grad_out,
+                         tab, moments, grad_theta, grad_points, workspace):
+        """cpab_backward and the projection onto the basis (tab: basis_tables)
+        in one launch."""
+        ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
+        wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        _check(self.lib.cpab_backward_project(
+            ndim, nP, n_theta, int(batched), int(T), ncx, ncy, ncz, int(adaptive), _ptr(points),
+            _ptr(As), _ptr(grad_out), tab["d"], _ptr(tab["col_ptr"]), _ptr(tab["row_idx"]),
+            _ptr(tab["vals_t"]), _ptr(moments), _ptr(grad_theta), _ptr(grad_points),
+            _ptr(workspace), wbytes, _stream(points.device)), "cpab_backward_project")
+
     def backward_noalloc(self, ndim, points, batched, n_theta, nP, T, nc, adaptive, As, grad_out,
                          moments, grad_points):
         """cpab_backward without a caller workspace (the library's per-GPU
@@ -187,15 +204,20 @@ class Native:
         return int(self.lib.cpab_chain_backward_workspace_size(ndim, nP, n_batch, n_stages, nC))
 
     def chain_backward(self, ndim, points, batched, n_batch, n_stages, nP, T, nc, adaptive,
-                       stage_points, As, grad_out, moments, grad_points, workspace):
+                       stage_points, As, grad_out, moments, grad_points, workspace, tab=None,
+                       grad_theta=None):
+        """tab (basis_tables) and grad_theta [n_stages * n_batch, d]: also
+        project every row's moments onto the basis."""
         ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
         wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-        _check(self.lib.cpab_chain_backward(ndim, nP, n_batch, int(batched), n_stages, int(T),
-                                            ncx, ncy, ncz, int(adaptive), _ptr(points),
-                                            _ptr(stage_points), _ptr(As), _ptr(grad_out),
-                                            _ptr(moments), _ptr(grad_points), _ptr(workspace),
-                                            wbytes, _stream(points.device)),
-               "cpab_chain_backward")
+        proj = tab is not None and grad_theta is not None
+        _check(self.lib.cpab_chain_backward(
+            ndim, nP, n_batch, int(batched), n_stages, int(T), ncx, ncy, ncz, int(adaptive),
+            _ptr(points), _ptr(stage_points), _ptr(As), _ptr(grad_out),
+            tab["d"] if proj else 0, _ptr(tab["col_ptr"]) if proj else None,
+            _ptr(tab["row_idx"]) if proj else None, _ptr(tab["vals_t"]) if proj else None,
+            _ptr(moments), _ptr(grad_theta) if proj else None, _ptr(grad_points),
+            _ptr(workspace), wbytes, _stream(points.device)), "cpab_chain_backward")
 
     def transform_data_forward(self, ndim, data, axes, outsize, T, nc, adaptive, Trels, As, out,
                                final_points):
@@ -210,13 +232,20 @@ class Native:
             ndim, n_batch, _lengths(outsize), nC))
 
     def transform_data_backward(self, ndim, data, axes, outsize, T, nc, adaptive, final_points,
-                                As, grad_out, moments, grad_data, workspace):
+                                As, grad_out, moments, grad_data, workspace, tab=None,
+                                grad_theta=None):
+        """tab (basis_tables) and grad_theta [n_batch, d]: also project the
+        moments onto the basis."""
         ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
         wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        proj = tab is not None and grad_theta is not None
         _check(self.lib.cpab_transform_data_backward(
             ndim, data.shape[0], data.shape[1], _lengths(data.shape[2:]), _lengths(outsize),
             int(T), ncx, ncy, ncz, int(adaptive), _ptr(axes), _ptr(final_points), _ptr(As),
-            _ptr(data), _ptr(grad_out), _ptr(moments), _ptr(grad_data), _ptr(workspace), wbytes,
+            _ptr(data), _ptr(grad_out), tab["d"] if proj else 0,
+            _ptr(tab["col_ptr"]) if proj else None, _ptr(tab["row_idx"]) if proj else None,
+            _ptr(tab["vals_t"]) if proj else None, _ptr(moments),
+            _ptr(grad_theta) if proj else None, _ptr(grad_data), _ptr(workspace), wbytes,
             _stream(data.device)), "cpab_transform_data_backward")
 
     def project(self, moments, D, d, col_ptr, row_idx, vals, grad_theta):

@@ -9,8 +9,8 @@ the integrated points ``[n_theta, ndim, nP]`` and differentiates w.r.t. theta
   forward   A = B theta and expm(A/T) in one launch (cpab_affine_expm) ->
             integrate (cpab_forward), or A = B theta (cpab_affine) and the 1D
             closed form                                 (transformer.py:72-126)
-  backward  fused replay + adjoint + moments (cpab_backward) -> dtheta = B^T M
-            (cpab_project) [-> sum over theta for shared points]
+  backward  fused replay + adjoint + moments, and dtheta = B^T M, in one
+            launch (cpab_backward_project) [-> sum over theta for shared points]
                                                         (transformer.py:128-168)
 
 ``CPAB_chain_transformer`` runs a whole chain of stages (the Python loop of
@@ -156,17 +156,15 @@ class _CPABFunction(torch.autograd.Function):
         want_points = ctx.compute_points_grad and ctx.needs_input_grad[0]
         gp = (torch.empty((n_theta, ndim, nP), device=dev, dtype=torch.float32)
               if want_points else None)
-        lib.backward(ndim, points, ctx.batched, n_theta, nP, ctx.nstepsolver, ctx.nc,
-                     ctx.adaptive_substeps, As, grad, moments, gp, ws)
+        tab = basis_tables(params, dev)
+        grad_theta = torch.empty((n_theta, tab["d"]), device=dev, dtype=torch.float32)
+        # moments and their projection dtheta = B^T vec(M) in one launch
+        lib.backward_project(ndim, points, ctx.batched, n_theta, nP, ctx.nstepsolver, ctx.nc,
+                             ctx.adaptive_substeps, As, grad, tab, moments, grad_theta, gp, ws)
         if want_points and points.dim() == 2:
             summed = torch.empty((ndim, nP), device=dev, dtype=torch.float32)
             lib.sum_batch(gp, summed)
             gp = summed
-
-        tab = basis_tables(params, dev)
-        grad_theta = torch.empty((n_theta, tab["d"]), device=dev, dtype=torch.float32)
-        lib.project(moments.view(n_theta, -1), tab["D"], tab["d"], tab["col_ptr"],
-                    tab["row_idx"], tab["vals_t"], grad_theta)
         return gp, grad_theta, None, None
 
 
@@ -248,17 +246,15 @@ class _CPABChainFunction(torch.autograd.Function):
         want_points = ctx.needs_input_grad[0]
         gp = (torch.empty((n_batch, ndim, nP), device=dev, dtype=torch.float32)
               if want_points else None)
+        tab = basis_tables(params, dev)
+        grad_theta = torch.empty((K * n_batch, tab["d"]), device=dev, dtype=torch.float32)
         lib.chain_backward(ndim, points, ctx.batched, n_batch, K, nP, ctx.nstepsolver, ctx.nc,
-                           ctx.adaptive_substeps, stage_points, As, grad, moments, gp, ws)
+                           ctx.adaptive_substeps, stage_points, As, grad, moments, gp, ws,
+                           tab=tab, grad_theta=grad_theta)
         if want_points and points.dim() == 2:
             summed = torch.empty((ndim, nP), device=dev, dtype=torch.float32)
             lib.sum_batch(gp, summed)
             gp = summed
-
-        tab = basis_tables(params, dev)
-        grad_theta = torch.empty((K * n_batch, tab["d"]), device=dev, dtype=torch.float32)
-        lib.project(moments.view(K * n_batch, -1), tab["D"], tab["d"], tab["col_ptr"],
-                    tab["row_idx"], tab["vals_t"], grad_theta)
         return gp, grad_theta.view(K, n_batch, tab["d"]), None
 
 
@@ -344,12 +340,11 @@ class _CPABImageFunction(torch.autograd.Function):
         ws_bytes = lib.transform_data_backward_workspace_size(ndim, n, ctx.outsize, nC)
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
         grad_data = torch.empty_like(data) if ctx.needs_input_grad[0] else None
-        lib.transform_data_backward(ndim, data, axes, ctx.outsize, ctx.T, ctx.nc, ctx.adaptive,
-                                    final, As, grad, moments, grad_data, ws)
-        grad_theta = None
+        tab, grad_theta = None, None
         if ctx.needs_input_grad[1]:
             tab = basis_tables(params, dev)
             grad_theta = torch.empty((n, tab["d"]), device=dev, dtype=torch.float32)
-            lib.project(moments.view(n, -1), tab["D"], tab["d"], tab["col_ptr"], tab["row_idx"],
-                        tab["vals_t"], grad_theta)
+        lib.transform_data_backward(ndim, data, axes, ctx.outsize, ctx.T, ctx.nc, ctx.adaptive,
+                                    final, As, grad, moments, grad_data, ws, tab=tab,
+                                    grad_theta=grad_theta)
         return grad_data, grad_theta, None, None, None

@@ -42,38 +42,64 @@ __global__ void affine_kernel(int64_t n_theta, int rows, int d, const float* __r
   As[i] = acc;
 }
 
-// One thread per (theta, column j of B): grad[b, j] = sum_k B[row_k, j] * M[b, row_k],
-// in ascending row order.  The column is read eight entries at a time (indices
-// and values, then the eight gathers) so the loads overlap; the products are
-// still added one by one in order.
-__global__ void project_kernel(int64_t n_theta, int D, int d, const float* __restrict__ M,
-                               const int32_t* __restrict__ col_ptr,
-                               const int32_t* __restrict__ row_idx,
-                               const float* __restrict__ vals, float* __restrict__ grad) {
-  constexpr int U = 8;
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= n_theta * d) return;
-  const int64_t b = i / d;
-  const int j = (int)(i - b * d);
+// grad[b, j] = sum_k B[row_k, j] * M[b, row_k] over the CSC column j of B,
+// added in ascending k with one fma per entry (a fixed order).  Each column is
+// served by kProjSeg lanes: they load its entries and gather the moments
+// together (a column of the 3D basis has up to 80 entries, and walking it
+// entry by entry from one lane made the projection a chain of dependent
+// memory round trips), stage the (value, moment) pairs in LDS, and the
+// segment's first lane adds them in order.  Columns longer than kProjCap
+// entries take several rounds.
+constexpr int kProjSeg = 16;                        // lanes per column
+constexpr int kProjThreads = 256;
+constexpr int kProjCols = kProjThreads / kProjSeg;  // columns per workgroup
+constexpr int kProjCap = 128;                       // entries staged per round
+
+__global__ __launch_bounds__(kProjThreads) void project_kernel(
+    int64_t n_theta, int D, int d, const float* __restrict__ M, const int32_t* __restrict__ col_ptr,
+    const int32_t* __restrict__ row_idx, const float* __restrict__ vals, float* __restrict__ grad) {
+  constexpr int PER = kProjCap / kProjSeg;  // entries per lane per round
+  __shared__ float2 stage[kProjCols][kProjCap];
+  const int seg = threadIdx.x / kProjSeg, lane = threadIdx.x % kProjSeg;
+  const int64_t i = blockIdx.x * (int64_t)kProjCols + seg;
+  const bool live = i < n_theta * d;
+  const int64_t b = live ? i / d : 0;
+  const int j = live ? (int)(i - b * d) : 0;
   const float* m = M + b * D;
+  const int k0 = live ? col_ptr[j] : 0, k1 = live ? col_ptr[j + 1] : 0;
+  // rounds: uniform over the workgroup (its longest column decides)
+  int rounds = (k1 - k0 + kProjCap - 1) / kProjCap;
+  __shared__ int max_rounds;
+  if (threadIdx.x == 0) max_rounds = 0;
+  __syncthreads();
+  if (lane == 0 && rounds > 0) atomicMax(&max_rounds, rounds);
+  __syncthreads();
+  rounds = max_rounds;
   float acc = 0.0f;
-  const int e = col_ptr[j + 1];
-  for (int k = col_ptr[j]; k < e; k += U) {
-    int r[U];
-    float v[U], x[U];
+  for (int r = 0; r < rounds; ++r) {
+    const int base = k0 + r * kProjCap;
+    int idx[PER];
+    float v[PER];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool ok = k + u < e;
-      r[u] = ok ? row_idx[k + u] : 0;
-      v[u] = ok ? vals[k + u] : 0.0f;
+    for (int u = 0; u < PER; ++u) {
+      const int k = base + lane + u * kProjSeg;
+      const bool ok = k < k1;
+      idx[u] = ok ? row_idx[k] : 0;
+      v[u] = ok ? vals[k] : 0.0f;
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) x[u] = m[r[u]];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (k + u < e) acc = fmaf(v[u], x[u], acc);
+    for (int u = 0; u < PER; ++u) {
+      const bool ok = base + lane + u * kProjSeg < k1;
+      stage[seg][lane + u * kProjSeg] = make_float2(v[u], ok ? m[idx[u]] : 0.0f);
+    }
+    __syncthreads();
+    if (lane == 0) {
+      const int n = min(kProjCap, k1 - base);
+      for (int k = 0; k < n; ++k) acc = fmaf(stage[seg][k].x, stage[seg][k].y, acc);
+    }
+    __syncthreads();
   }
-  grad[i] = acc;
+  if (live && lane == 0) grad[i] = acc;
 }
 
 // Reverse-sweep table.  Each workgroup of kTableThreads covers one block of
@@ -153,7 +179,9 @@ __global__ void finish_moments_kernel(int64_t n_cells, int nC, int nparts, float
     const int NW = (nparts + 63) / 64;
     const int64_t row = i / nC;
     const float* src = partials + row * nparts * R + (i - row * nC) * P;
-    constexpr int U = 4;  // parts loaded together, then added in order
+    // parts whose loads are issued together, then added in order (all of a
+    // C2 row's 16 in one batch; 3D rows have no partial tables)
+    constexpr int U = D == 3 ? 4 : 16;
     for (int q = 0; q < NW; ++q) {
       uint64_t bits = dense_parts[row * NW + q];
       while (bits) {
@@ -475,8 +503,8 @@ hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
                           float* grad_theta, hipStream_t s) {
   const int64_t n = n_theta * d;
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(project_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, n_theta, D, d,
-                     moments, col_ptr, row_idx, vals, grad_theta);
+  hipLaunchKernelGGL(project_kernel, dim3(grid_for(n, kProjCols)), dim3(kProjThreads), 0, s,
+                     n_theta, D, d, moments, col_ptr, row_idx, vals, grad_theta);
   return hipGetLastError();
 }
 

@@ -300,6 +300,25 @@ BackwardWorkspace backward_workspace(const cpab::Geometry& g, int64_t nP, int64_
   return w;
 }
 
+// Optional projection of the backward's moments onto the basis, enqueued by
+// the backward entry point after the moments: grad_theta [rows, d] from B's
+// CSC tables.
+struct Projection {
+  int d = 0;
+  const int32_t* col_ptr = nullptr;
+  const int32_t* row_idx = nullptr;
+  const float* vals = nullptr;
+  float* grad_theta = nullptr;  // null: moments only
+};
+
+int check_projection(const Projection& pr) {
+  if (!pr.grad_theta) return CPAB_OK;
+  if (pr.d < 0) return fail(CPAB_ERR_INVALID, "negative d");
+  if (pr.d > 0) { CPAB_REQUIRE(pr.col_ptr); CPAB_REQUIRE(pr.row_idx); CPAB_REQUIRE(pr.vals); }
+  return CPAB_OK;
+}
+
+
 int64_t workspace_size_impl(int ndim, int64_t nP, int64_t n_batch, int K, int nC) {
   if (ndim < 1 || ndim > 3 || nP <= 0 || n_batch <= 0 || nC <= 0 || K < 1) return 0;
   cpab::Geometry g{};
@@ -313,13 +332,26 @@ int64_t workspace_size_impl(int ndim, int64_t nP, int64_t n_batch, int K, int nC
                   backward_workspace(g, nP, n_batch, K, seg).total);
 }
 
+// Moments from the backward's per-cell sums, then (optionally) their projection.
+int finish_and_project(const char* who, int ndim, int64_t rows, int nC, const cpab::LaunchCfg& cfg,
+                       int T, const float* partials, const uint64_t* dense, const float* As,
+                       float* moments, const Projection& pr, hipStream_t s) {
+  int rc = check_hip(cpab::launch_finish_moments(ndim, rows, nC, cfg.lds_bins ? cfg.chunks : 0, T,
+                                                 partials, dense, As, moments, s),
+                     who);
+  if (rc || !pr.grad_theta || pr.d == 0) return rc;
+  return check_hip(cpab::launch_project(rows, nC * ndim * (ndim + 1), pr.d, moments, pr.col_ptr,
+                                        pr.row_idx, pr.vals, pr.grad_theta, s),
+                   who);
+}
+
 // `timing`: record the backward kernel with the optional HIP-event timing
 // (off for the allocation-free entry point: the event pool may create events).
 int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int batched, int K,
                   int nstepsolver, int ncx, int ncy, int ncz, int adaptive, const float* points,
                   const float* stage_points, const float* As, const float* grad_out,
                   float* moments, float* grad_points, void* workspace, int64_t workspace_bytes,
-                  void* stream, bool timing = true) {
+                  void* stream, const Projection& pr = Projection(), bool timing = true) {
   cpab::Geometry g{};
   int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
   if (rc) return rc;
@@ -328,12 +360,18 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   if (K < 1 || K > 4096) return fail(CPAB_ERR_INVALID, "n_stages must be in [1, 4096], got %d", K);
   if ((int64_t)K * n_batch >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "n_stages * n_batch too large");
   if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
+  if ((rc = check_projection(pr))) return rc;
   if (n_batch == 0) return CPAB_OK;
   CPAB_REQUIRE(moments);
   hipStream_t s = as_stream(stream);
   const int R = g.nC * g.ppc();
   const int64_t rows = (int64_t)K * n_batch;
-  if (nP == 0) return check_hip(cpab::launch_fill(moments, rows * R, 0.0f, s), who);
+  if (nP == 0) {
+    rc = check_hip(cpab::launch_fill(moments, rows * R, 0.0f, s), who);
+    if (rc == CPAB_OK && pr.grad_theta)
+      rc = check_hip(cpab::launch_fill(pr.grad_theta, rows * pr.d, 0.0f, s), who);
+    return rc;
+  }
   CPAB_REQUIRE(points); CPAB_REQUIRE(As); CPAB_REQUIRE(grad_out);
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(points, 4); CPAB_ALIGNED(grad_out, 4);
   CPAB_ALIGNED(workspace, 16);
@@ -363,10 +401,8 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
                  who);
   prof_end(timed, ev, "backward", s);
   if (rc) return rc;
-  return check_hip(cpab::launch_finish_moments(ndim, rows, g.nC, cfg.lds_bins ? cfg.chunks : 0,
-                                               nstepsolver, partials, dense, As, moments,
-                                               s),
-                   who);
+  return finish_and_project(who, ndim, rows, g.nC, cfg, nstepsolver, partials, dense, As, moments,
+                            pr, s);
 }
 
 // ---- allocation-free backward --------------------------------------------
@@ -440,9 +476,11 @@ extern "C" {
 
 const char* cpab_last_error_string(void) { return g_last_error.c_str(); }
 
-// 200: the fused transform_data entry points take the uniform grid's per-axis
-// coordinates instead of the meshgrid.
-int cpab_abi_version(void) { return 200; }
+// 300: the backward entry points can also project the moments onto the basis
+// (cpab_backward_project; projection arguments of the chain and
+// transform_data backwards).  200: the fused transform_data entry points take
+// the uniform grid's per-axis coordinates instead of the meshgrid.
+int cpab_abi_version(void) { return 300; }
 
 int cpab_affine(int ndim, int64_t n_theta, int nC, int d, const float* theta,
                 const int32_t* row_ptr, const int32_t* col_idx, const float* vals, float* As,
@@ -540,6 +578,24 @@ int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nsteps
                        workspace_bytes, stream);
 }
 
+int cpab_backward_project(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
+                          int ncx, int ncy, int ncz, int adaptive, const float* points,
+                          const float* As, const float* grad_out, int d, const int32_t* col_ptr,
+                          const int32_t* row_idx, const float* vals, float* moments,
+                          float* grad_theta, float* grad_points, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
+  Projection pr;
+  pr.d = d;
+  pr.col_ptr = col_ptr;
+  pr.row_idx = row_idx;
+  pr.vals = vals;
+  pr.grad_theta = grad_theta;
+  CPAB_REQUIRE(grad_theta);
+  return backward_impl("cpab_backward_project", ndim, nP, n_theta, batched, 1, nstepsolver, ncx,
+                       ncy, ncz, adaptive, points, nullptr, As, grad_out, moments, grad_points,
+                       workspace, workspace_bytes, stream, pr);
+}
+
 int cpab_backward_noalloc(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
                           int ncx, int ncy, int ncz, int adaptive, const float* points,
                           const float* As, const float* grad_out, float* moments,
@@ -566,17 +622,25 @@ int cpab_backward_noalloc(int ndim, int64_t nP, int64_t n_theta, int batched, in
   if (ws == nullptr) return CPAB_ERR_DEVICE;
   return backward_impl("cpab_backward_noalloc", ndim, nP, n_theta, batched, 1, nstepsolver, ncx,
                        ncy, ncz, adaptive, points, nullptr, As, grad_out, moments, grad_points, ws,
-                       kScratchBytes, stream, /*timing=*/false);
+                       kScratchBytes, stream, Projection(), /*timing=*/false);
 }
 
 int cpab_chain_backward(int ndim, int64_t nP, int64_t n_batch, int batched, int n_stages,
                         int nstepsolver, int ncx, int ncy, int ncz, int adaptive,
                         const float* points, const float* stage_points, const float* As,
-                        const float* grad_out, float* moments, float* grad_points,
-                        void* workspace, int64_t workspace_bytes, void* stream) {
+                        const float* grad_out, int d, const int32_t* col_ptr,
+                        const int32_t* row_idx, const float* vals, float* moments,
+                        float* grad_theta, float* grad_points, void* workspace,
+                        int64_t workspace_bytes, void* stream) {
+  Projection pr;
+  pr.d = d;
+  pr.col_ptr = col_ptr;
+  pr.row_idx = row_idx;
+  pr.vals = vals;
+  pr.grad_theta = grad_theta;
   return backward_impl("cpab_chain_backward", ndim, nP, n_batch, batched, n_stages, nstepsolver,
                        ncx, ncy, ncz, adaptive, points, stage_points, As, grad_out, moments,
-                       grad_points, workspace, workspace_bytes, stream);
+                       grad_points, workspace, workspace_bytes, stream, pr);
 }
 
 int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
@@ -618,8 +682,10 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
                                  const int64_t* in_size, const int64_t* out_size, int nstepsolver,
                                  int ncx, int ncy, int ncz, int adaptive, const float* axes,
                                  const float* final_points, const float* As, const float* data,
-                                 const float* grad_out, float* moments, float* grad_data,
-                                 void* workspace, int64_t workspace_bytes, void* stream) {
+                                 const float* grad_out, int d, const int32_t* col_ptr,
+                                 const int32_t* row_idx, const float* vals, float* moments,
+                                 float* grad_theta, float* grad_data, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
   cpab::Geometry g{};
   int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
   if (rc) return rc;
@@ -627,6 +693,13 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
   cpab::ImageShape img;
   if ((rc = image_shape(ndim, n_batch, n_channels, in_size, out_size, &img))) return rc;
+  Projection pr;
+  pr.d = d;
+  pr.col_ptr = col_ptr;
+  pr.row_idx = row_idx;
+  pr.vals = vals;
+  pr.grad_theta = grad_theta;
+  if ((rc = check_projection(pr))) return rc;
   if (n_batch == 0) return CPAB_OK;
   CPAB_REQUIRE(axes); CPAB_REQUIRE(final_points); CPAB_REQUIRE(As); CPAB_REQUIRE(data);
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(workspace, 16);
@@ -660,10 +733,8 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
                  "cpab_transform_data_backward");
   prof_end(timed, ev, "image_backward", s);
   if (rc) return rc;
-  return check_hip(cpab::launch_finish_moments(ndim, n_batch, g.nC, cfg.lds_bins ? cfg.chunks : 0,
-                                               nstepsolver, partials, dense, As, moments,
-                                               s),
-                   "cpab_transform_data_backward");
+  return finish_and_project("cpab_transform_data_backward", ndim, n_batch, g.nC, cfg, nstepsolver,
+                            partials, dense, As, moments, pr, s);
 }
 
 int cpab_project(int64_t n_theta, int D, int d, const float* moments, const int32_t* col_ptr,

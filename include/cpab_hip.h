@@ -110,6 +110,19 @@ int cpab_backward(int ndim, int64_t nP, int64_t n_theta, int batched, int nsteps
                   float* grad_points, void* workspace, int64_t workspace_bytes,
                   void* stream);
 
+/* cpab_backward followed by cpab_project of its moments, in one call: moments
+ * as cpab_backward writes them, grad_theta [n_theta, d] as
+ * cpab_project(n_theta, nC*ndim*(ndim+1), d, moments, col_ptr, row_idx, vals,
+ * ...) writes it, bit for bit.  Replaces the
+ * reference backward's cpab_gpu.backward_moments[_and_points] call and the
+ * torch.sparse.mm projection after it (cpab/pytorch/transformer.py:141-166). */
+int cpab_backward_project(int ndim, int64_t nP, int64_t n_theta, int batched, int nstepsolver,
+                          int ncx, int ncy, int ncz, int adaptive, const float* points,
+                          const float* As, const float* grad_out, int d, const int32_t* col_ptr,
+                          const int32_t* row_idx, const float* vals, float* moments,
+                          float* grad_theta, float* grad_points, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
 /* Device memory the library keeps per GPU for cpab_backward_noalloc. */
 #define CPAB_NOALLOC_SCRATCH_BYTES (32LL << 20)
 
@@ -152,16 +165,21 @@ int64_t cpab_chain_backward_workspace_size(int ndim, int64_t nP, int64_t n_batch
 /* Backward of cpab_chain_forward in one launch: replaces the n_stages
  * autograd nodes of the reference's chain, each a
  * cpab_gpu.backward_moments_and_points call (transformer_cuda.cpp:122-153)
- * whose grad_points seeds the stage below.  moments [n_stages, n_batch, nC,
- * ndim*(ndim+1)] (overwritten); grad_points (may be NULL) = adjoint of the
- * stage-0 input points, [n_batch, ndim, nP] (sum over n_batch for shared
- * points, as cpab_sum_batch does).  stage_points as written by
- * cpab_chain_forward (may be NULL when n_stages == 1). */
+ * whose grad_points seeds the stage below, and their projections
+ * (transformer.py:165-166).  moments [n_stages, n_batch, nC, ndim*(ndim+1)]
+ * (overwritten); grad_theta (may be NULL) [n_stages, n_batch, d]: each row's
+ * moments projected through B's CSC tables (col_ptr, row_idx, vals, as
+ * cpab_project takes them; ignored when grad_theta is NULL); grad_points (may
+ * be NULL) = adjoint of the stage-0 input points, [n_batch, ndim, nP] (sum
+ * over n_batch for shared points, as cpab_sum_batch does).  stage_points as
+ * written by cpab_chain_forward (may be NULL when n_stages == 1). */
 int cpab_chain_backward(int ndim, int64_t nP, int64_t n_batch, int batched, int n_stages,
                         int nstepsolver, int ncx, int ncy, int ncz, int adaptive,
                         const float* points, const float* stage_points, const float* As,
-                        const float* grad_out, float* moments, float* grad_points,
-                        void* workspace, int64_t workspace_bytes, void* stream);
+                        const float* grad_out, int d, const int32_t* col_ptr,
+                        const int32_t* row_idx, const float* vals, float* moments,
+                        float* grad_theta, float* grad_points, void* workspace,
+                        int64_t workspace_bytes, void* stream);
 
 /* grad_theta[b, j] = sum_k vals[k] * moments[b, row_idx[k]] over the CSC column
  * j of B (D = rows of B).  Replaces torch.sparse.mm(B^T, M^T) in
@@ -202,16 +220,20 @@ int64_t cpab_transform_data_backward_workspace_size(int ndim, int64_t n_batch,
  * gradient at each final point (the interp backward, summed over channels)
  * seeds the adjoint of that pixel's trajectory, as the reference's autograd
  * does through interpolate's backward and cpab_gpu.backward_moments_and_points
- * (transformer_cuda.cpp:122-153).  moments [n_batch, nC, ndim*(ndim+1)]
- * (overwritten); grad_data [n_batch, C, *in_size] (may be NULL; overwritten).
- * grad_out is the image gradient [n_batch, C, *out_size]; axes as for the
- * forward. */
+ * (transformer_cuda.cpp:122-153), then the projection
+ * (transformer.py:165-166).  moments [n_batch, nC, ndim*(ndim+1)]
+ * (overwritten); grad_theta (may be NULL) [n_batch, d] through B's CSC tables
+ * as in cpab_chain_backward; grad_data [n_batch, C, *in_size] (may be NULL;
+ * overwritten).  grad_out is the image gradient [n_batch, C, *out_size]; axes
+ * as for the forward. */
 int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
                                  const int64_t* in_size, const int64_t* out_size, int nstepsolver,
                                  int ncx, int ncy, int ncz, int adaptive, const float* axes,
                                  const float* final_points, const float* As, const float* data,
-                                 const float* grad_out, float* moments, float* grad_data,
-                                 void* workspace, int64_t workspace_bytes, void* stream);
+                                 const float* grad_out, int d, const int32_t* col_ptr,
+                                 const int32_t* row_idx, const float* vals, float* moments,
+                                 float* grad_theta, float* grad_data, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
 
 /* Border-clamped linear/bilinear/trilinear resampling of data
  * [n_batch, C, *in_size] at grid [n_batch, ndim, prod(out_size)] (coordinate 0

@@ -49,8 +49,8 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    # 200: the fused transform_data entry points take the grid's per-axis coordinates
-    assert _native.load_library().cpab_abi_version() >= 200
+    # 300: backward launches form the moments and project them (fused tail)
+    assert _native.load_library().cpab_abi_version() >= 300
 
 
 def _err(lib):
@@ -125,12 +125,16 @@ def _check_chain_validation():
     p = ctypes.c_void_p(16)
     rc = lib.cpab_chain_forward(2, 10, 1, 0, 0, 50, 4, 4, 1, 0, p, p, p, p, None, None)
     assert rc == 1 and "n_stages" in _err(lib)
-    rc = lib.cpab_chain_backward(2, 10, 1, 0, 3, 50, 4, 4, 1, 0, p, None, p, p, p, None, None, 0,
-                                 None)
+    rc = lib.cpab_chain_backward(2, 10, 1, 0, 3, 50, 4, 4, 1, 0, p, None, p, p, 0, None, None,
+                                 None, p, None, None, None, 0, None)
     assert rc == 1 and "stage_points" in _err(lib)
-    rc = lib.cpab_chain_backward(2, 10, 1, 0, 5000, 50, 4, 4, 1, 0, p, p, p, p, p, None, None, 0,
-                                 None)
+    rc = lib.cpab_chain_backward(2, 10, 1, 0, 5000, 50, 4, 4, 1, 0, p, p, p, p, 0, None, None,
+                                 None, p, None, None, None, 0, None)
     assert rc == 1 and "n_stages" in _err(lib)
+    # a projection needs B's tables
+    rc = lib.cpab_backward_project(2, 10, 1, 0, 50, 4, 4, 1, 0, p, p, p, 5, None, None, None, p,
+                                   p, None, None, 0, None)
+    assert rc == 1 and "col_ptr" in _err(lib)
     assert lib.cpab_chain_backward_workspace_size(2, 10, 1, 0, 64) == 0
 
 

@@ -581,3 +581,93 @@ def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive, scale):
     _, mag = orc.interp_backward(nd, data, xT, outs, np.abs(gout), dtype=np.float64)
     err = np.abs(gd.cpu().numpy().astype(np.float64) - rd)
     assert (err <= 1e-4 * mag + 1e-12).all(), float((err / (mag + 1e-30)).max())
+
+
+@pytest.mark.parametrize("case", ["dense", "sparse", "cache3d", "chain", "image"])
+def test_fused_projection_matches_project(cuda, case):
+    # The backward launch forms each row's moments and projects them onto the
+    # basis in its last workgroup; the projection must equal cpab_project of
+    # the same moments bit for bit (same summation order), and the moments the
+    # oracle's within the backward's tolerance.
+    tess = {"dense": [20, 20], "sparse": [16, 16], "cache3d": [10, 10, 10], "chain": [16, 16],
+            "image": [6, 5]}[case]
+    T = cpab_for(tess)
+    p = T.params
+    nd = len(tess)
+    tab = basis_tables(p, cuda)
+    ppc = nd * (nd + 1)
+
+    def project(mom):
+        gt = torch.empty((mom.shape[0], tab["d"]), device=cuda)
+        native().project(mom.view(mom.shape[0], -1), tab["D"], tab["d"], tab["col_ptr"],
+                         tab["row_idx"], tab["vals_t"], gt)
+        return gt
+
+    if case in ("dense", "sparse", "cache3d"):
+        n_theta = 3
+        theta = seeded_theta(T, n_theta, 0.5, 260)
+        pts = (uniform_points(nd, 30000, 261) if case != "sparse" else meshgrid([96, 80]))
+        g = np.random.default_rng(262).standard_normal((n_theta, nd, pts.shape[-1])).astype(np.float32)
+        As = _As_gpu(T, theta, cuda)
+        nP = pts.shape[-1]
+        mom = torch.empty((n_theta, p.nC, ppc), device=cuda)
+        gth = torch.empty((n_theta, tab["d"]), device=cuda)
+        gp = torch.empty((n_theta, nd, nP), device=cuda)
+        ws = torch.empty(native().backward_workspace_size(nd, nP, n_theta, p.nC), dtype=torch.uint8,
+                         device=cuda)
+        native().backward_project(nd, _dev(pts, cuda), False, n_theta, nP, 50, p.nc, 0, As,
+                                  _dev(g, cuda), tab, mom, gth, gp, ws)
+        ref_m, ref_gp = orc.backward(pts, As.cpu().numpy(), g, p.nc, 50)
+        assert_adjoint_close(gp.cpu().numpy(), ref_gp)
+    elif case == "chain":
+        K, nb = 4, 2
+        theta = (np.random.default_rng(263).standard_normal((K * nb, p.d)) * 0.3).astype(np.float32)
+        pts = meshgrid([64, 48])
+        nP = pts.shape[-1]
+        As = _As_gpu(T, theta, cuda)
+        Tr = torch.empty_like(As)
+        native().expm(nd, As, 1.0 / 50, Tr)
+        out = torch.empty((nb, nd, nP), device=cuda)
+        sp = torch.empty((K - 1, nb, nd, nP), device=cuda)
+        native().chain_forward(nd, _dev(pts, cuda), False, nb, K, nP, 50, p.nc, 0, Tr, As, out, sp)
+        g = np.random.default_rng(264).standard_normal((nb, nd, nP)).astype(np.float32)
+        mom = torch.empty((K * nb, p.nC, ppc), device=cuda)
+        gth = torch.empty((K * nb, tab["d"]), device=cuda)
+        ws = torch.empty(native().chain_backward_workspace_size(nd, nP, nb, K, p.nC),
+                         dtype=torch.uint8, device=cuda)
+        native().chain_backward(nd, _dev(pts, cuda), False, nb, K, nP, 50, p.nc, 0, sp, As,
+                                _dev(g, cuda), mom, None, ws, tab=tab, grad_theta=gth)
+        A = As.cpu().numpy().reshape(K, nb, p.nC, nd, nd + 1)
+        xs = [pts] + [sp[s].cpu().numpy() for s in range(K - 1)]
+        lam, refs = g, [None] * K
+        for s in reversed(range(K)):
+            refs[s], lam = orc.backward(xs[s], A[s], lam, p.nc, 50)
+        ref_m = np.concatenate(refs)
+    else:
+        B, C, ins, outs = 2, 2, (40, 48), (36, 48)
+        theta = seeded_theta(T, B, 0.5, 265)
+        rng = np.random.default_rng(266)
+        data = rng.random((B, C, *ins)).astype(np.float32)
+        axes = T._uniform_axes(list(outs))
+        As = _As_gpu(T, theta, cuda)
+        Tr = torch.empty_like(As)
+        native().expm(nd, As, 1.0 / 50, Tr)
+        nP = int(np.prod(outs))
+        out = torch.empty((B, C, *outs), device=cuda)
+        fin = torch.empty((B, nd, nP), device=cuda)
+        native().transform_data_forward(nd, _dev(data, cuda), axes, list(outs), 50, p.nc, 0, Tr, As,
+                                        out, fin)
+        gout = rng.standard_normal((B, C, *outs)).astype(np.float32)
+        mom = torch.empty((B, p.nC, ppc), device=cuda)
+        gth = torch.empty((B, tab["d"]), device=cuda)
+        ws = torch.empty(native().transform_data_backward_workspace_size(nd, B, list(outs), p.nC),
+                         dtype=torch.uint8, device=cuda)
+        native().transform_data_backward(nd, _dev(data, cuda), axes, list(outs), 50, p.nc, 0, fin,
+                                         As, _dev(gout, cuda), mom, None, ws, tab=tab,
+                                         grad_theta=gth)
+        grid = T.uniform_meshgrid(list(outs)).cpu().numpy()
+        xT = orc.forward_trels(grid, Tr.cpu().numpy(), As.cpu().numpy(), p.nc, 50)
+        rg, _ = orc.interp_backward(nd, data, xT, outs, gout, want_data=False)
+        ref_m, _ = orc.backward(grid, As.cpu().numpy(), rg, p.nc, 50)
+    assert_grad_close(mom.cpu().numpy(), ref_m, rtol=2e-5)
+    np.testing.assert_array_equal(gth.cpu().numpy(), project(mom).cpu().numpy())
