@@ -132,8 +132,6 @@ cpab::LaunchCfg forward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta
   int64_t chunks = std::max<int64_t>(1, div_up(want, std::max<int64_t>(n_theta, 1)));
   chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
   c.chunks = (int)chunks;
-  // 2D chains stage each stage's table in LDS when it fits.
-  c.lds_chain = dev.lds;
   return c;
 }
 
@@ -254,7 +252,7 @@ int forward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int bat
   if (ndim > 1) CPAB_REQUIRE(Trels);
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(Trels, 16); CPAB_ALIGNED(points, 4);
   hipStream_t s = as_stream(stream);
-  hipEvent_t ev;
+  hipEvent_t ev = nullptr;
   const bool timed = prof_begin(s, &ev);
   if (ndim == 1) {
     rc = check_hip(cpab::launch_forward_1d(g, nP, n_batch, batched ? 1 : 0, K, points, As, out,
@@ -393,7 +391,7 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
                                             dense, w.dense_words, s),
                  who);
   if (rc) return rc;
-  hipEvent_t ev;
+  hipEvent_t ev = nullptr;
   const bool timed = timing && prof_begin(s, &ev);
   rc = check_hip(cpab::launch_backward(g, nP, n_batch, batched ? 1 : 0, nstepsolver, K, adaptive,
                                        points, stage_points, As, G, amp, grad_out, moments,
@@ -661,7 +659,7 @@ int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(Trels, 16);
   hipStream_t s = as_stream(stream);
   const cpab::LaunchCfg cfg = forward_cfg(g, img.nP, n_batch);
-  hipEvent_t ev;
+  hipEvent_t ev = nullptr;
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_image_forward(g, img, n_batch, nstepsolver, adaptive, axes, Trels,
                                             As, data, out, final_points, cfg, s),
@@ -725,7 +723,7 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
                    "cpab_transform_data_backward");
     if (rc) return rc;
   }
-  hipEvent_t ev;
+  hipEvent_t ev = nullptr;
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, axes,
                                              final_points, As, G, amp, data, grad_out, moments,
@@ -824,7 +822,7 @@ int cpab_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
   int rc = check_interp(ndim, B, C, in_size, out_size);
   if (rc) return rc;
   CPAB_REQUIRE(data); CPAB_REQUIRE(grid); CPAB_REQUIRE(out);
-  hipEvent_t ev;
+  hipEvent_t ev = nullptr;
   const bool timed = prof_begin(as_stream(stream), &ev);
   rc = check_hip(cpab::launch_interp_forward(ndim, B, C, in_size, out_size, data, grid, out,
                                              as_stream(stream)),
@@ -840,7 +838,7 @@ int cpab_interp_backward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
   int rc = check_interp(ndim, B, C, in_size, out_size);
   if (rc) return rc;
   CPAB_REQUIRE(data); CPAB_REQUIRE(grid); CPAB_REQUIRE(grad_out);
-  hipEvent_t ev;
+  hipEvent_t ev = nullptr;
   const bool timed = prof_begin(as_stream(stream), &ev);
   rc = check_hip(cpab::launch_interp_backward(ndim, B, C, in_size, out_size, data, grid,
                                               grad_out, grad_grid, grad_data, as_stream(stream)),

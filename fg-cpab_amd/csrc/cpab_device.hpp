@@ -113,14 +113,6 @@ __device__ __forceinline__ int tri_2d_inside(float xc, float yc, float fx, float
   return tri_2d(lx, ly);
 }
 
-// Inside rule on in-range coordinates: 4 * square + tri_2d.
-__device__ __forceinline__ int base_plus_tri(float xc, float yc, float fx, float fy) {
-  int base;
-  float lx, ly;
-  const int t = tri_2d_inside(xc, yc, fx, fy, base, lx, ly);
-  return base + t;
-}
-
 // 4 * square + tri_2d(lx, ly) in two adds with a carry-in.  With
 // b3 = lx < ly and b1 = (1 - lx) < ly, tri_2d = 3*b3 ^ b1 = 2*b3 + (b3 ^ b1),
 // so the cell is 2 * (2 * square + b3) + (b3 ^ b1).  Each "x + x + bit" is one
@@ -139,12 +131,9 @@ __device__ __forceinline__ int cell_from_square(int square, float lx, float ly) 
 
 // Square (cx, cy) holds triangles 4*(cx + cy*nx) + {0 top, 1 right, 2 bottom, 3 left}.
 // A wave whose lanes all lie in (0, kClampHi]^2, where the lookup clamp is the
-// identity, takes the inside rule on the raw coordinates.  Otherwise a
-// wave-uniform branch clamps, and applies the boundary rules to lanes outside
-// (0,1)^2.  CARRY picks cell_from_square for the inside rule (fewer VALU ops,
-// for throughput-bound callers) over the select form (a shorter dependency
-// chain, without the scalar xor, for latency-bound ones).
-template <bool CARRY = true>
+// identity, takes the inside rule on the raw coordinates (cell_from_square).
+// Otherwise a wave-uniform branch clamps, and applies the boundary rules to
+// lanes outside (0,1)^2.
 __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   const float fx = (float)nx, fy = (float)ny;
   // One ballot per compare keeps the masks in SGPRs (a ballot of a combined
@@ -156,7 +145,6 @@ __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   int base;
   float lx, ly;
   if (!edge) {
-    if (!CARRY) return base_plus_tri(px, py, fx, fy);
     const float sx = __builtin_floorf(px * fx), sy = __builtin_floorf(py * fy);
     return cell_from_square((int)fmaf(sy, fx, sx), fmaf(px, fx, -sx), fmaf(py, fy, -sy));
   }

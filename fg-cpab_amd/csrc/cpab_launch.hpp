@@ -30,7 +30,6 @@ struct LaunchCfg {
   int lds_bins;     // backward: accumulate moments in full LDS bins (per-workgroup partials)
   int lds_cache;    // backward: else accumulate in the hashed LDS cell cache
   int reg_steps;    // backward: compile-time step count of the register variant (0 = segmented)
-  int lds_chain;    // forward: LDS bytes available for the per-stage table of a 2D chain
 };
 
 hipError_t launch_fill(float* dst, int64_t n, float value, hipStream_t s);

@@ -5,12 +5,13 @@
 //          (cpab_ops_2d.cu:164-230, cpab_ops_3d.cu:169-241), optional Heun
 //          correction on a cell crossing (adaptive_substeps).
 //
-// MI355X layout: one workgroup integrates a contiguous chunk of points for ONE
-// theta, so that theta's whole per-cell table (nC x 6 floats in 2D) is staged
-// once into LDS and every step's table fetch is an LDS read instead of a
-// random L2 gather.  Points are SoA ([ndim, nP] rows) and each lane owns whole
-// trajectories, so global reads and writes are fully coalesced.  The integrator
-// is fp32 VALU-bound; no MFMA is involved.
+// MI355X layout: the workgroups of one grid row (blockIdx.y) integrate the
+// points of ONE theta, so the L1/L2 serve that theta's per-cell table (nC x 6
+// floats in 2D); each lane keeps its current cell's one-step map in registers
+// and re-reads it only when some lane of its wave changes cell.  Points are
+// SoA ([ndim, nP] rows) and each lane owns whole trajectories, so global reads
+// and writes are fully coalesced.  The integrator is fp32 VALU-bound; no MFMA
+// is involved.
 #include <hip/hip_runtime.h>
 #include <algorithm>
 #include <math.h>
@@ -96,21 +97,13 @@ __global__ __launch_bounds__(256) void fwd1d_closed_kernel(int nP, int batched, 
 // 2D / 3D fixed-step forward
 // ---------------------------------------------------------------------------
 
-// Cooperative copy of n floats (n % 2 == 0, 8-byte aligned) global -> LDS.
-__device__ __forceinline__ void stage(float* __restrict__ dst, const float* __restrict__ src,
-                                      int n) {
-  const float2* s2 = reinterpret_cast<const float2*>(src);
-  float2* d2 = reinterpret_cast<float2*>(dst);
-  for (int i = threadIdx.x; i < n / 2; i += blockDim.x) d2[i] = s2[i];
-}
-
 // T fixed steps of one transform for PPT points per lane (2D).  The one-step
-// map of the current cell stays in registers; it is re-read (LDS / L1) only at
-// steps where some lane of the wave changed cell, which keeps table traffic and
-// LDS bank conflicts off most steps.  With adaptive_substeps a step that
-// leaves its cell is redone with Heun's rule (cpab_ops_2d.cu:202-219).
-template <bool ADAPTIVE, bool LDS, int PPT, bool CARRY = true>
-__device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT], float* lds,
+// map of the current cell stays in registers; it is re-read (through L1) only
+// at steps where some lane of the wave changed cell, which keeps table traffic
+// off most steps.  With adaptive_substeps a step that leaves its cell is
+// redone with Heun's rule (cpab_ops_2d.cu:202-219).
+template <bool ADAPTIVE, int PPT>
+__device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT],
                                          const float* __restrict__ Tg,
                                          const float* __restrict__ Ag, int T, int nx, int ny,
                                          float hh) {
@@ -118,15 +111,15 @@ __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT], flo
   Aff<2> M[PPT];
 #pragma unroll
   for (int k = 0; k < PPT; ++k) {
-    cur[k] = cell_2d<CARRY>(px[k], py[k], nx, ny);
-    M[k] = LDS ? load_aff2(as_lds(lds), cur[k]) : load_aff2(Tg, cur[k]);
+    cur[k] = cell_2d(px[k], py[k], nx, ny);
+    M[k] = load_aff2(Tg, cur[k]);
   }
   // One step of point k from its cell c (M[k] already holds c's map).
   auto advance = [&](int k, int c) {
     float sx, sy;
     apply2(M[k], px[k], py[k], sx, sy);
     if (ADAPTIVE) {
-      const int ce = cell_2d<CARRY>(sx, sy, nx, ny);
+      const int ce = cell_2d(sx, sy, nx, ny);
       if (ce != c) {
         float v0x, v0y, v1x, v1y;
         apply2(load_aff2(Ag, c), px[k], py[k], v0x, v0y);
@@ -143,9 +136,9 @@ __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT], flo
   auto step = [&]() {
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
-      const int c = cell_2d<CARRY>(px[k], py[k], nx, ny);
+      const int c = cell_2d(px[k], py[k], nx, ny);
       // Divergent branch, skipped (exec = 0) when no lane changed cell.
-      if (c != cur[k]) M[k] = LDS ? load_aff2(as_lds(lds), c) : load_aff2(Tg, c);
+      if (c != cur[k]) M[k] = load_aff2(Tg, c);
       cur[k] = c;
       advance(k, c);
     }
@@ -164,17 +157,17 @@ __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT], flo
 
 // T fixed steps of one transform for one point (3D, cpab_ops_3d.cu:169-241),
 // with the same cell-change caching of the one-step map as steps_2d.
-template <bool ADAPTIVE, bool LDS>
-__device__ __forceinline__ void steps_3d(float& px, float& py, float& pz, float* lds,
+template <bool ADAPTIVE>
+__device__ __forceinline__ void steps_3d(float& px, float& py, float& pz,
                                          const float* __restrict__ Tg,
                                          const float* __restrict__ Ag, int T, int nx, int ny,
                                          int nz, float hh) {
   int cur = cell_3d(px, py, pz, nx, ny, nz);
-  Aff<3> M = LDS ? load_aff3(as_lds(lds), cur) : load_aff3(Tg, cur);
+  Aff<3> M = load_aff3(Tg, cur);
   for (int t = 0; t < T; ++t) {
     const int c = (t == 0) ? cur : cell_3d(px, py, pz, nx, ny, nz);
     // Divergent branch, skipped (exec = 0) when no lane changed cell.
-    if (c != cur) M = LDS ? load_aff3(as_lds(lds), c) : load_aff3(Tg, c);
+    if (c != cur) M = load_aff3(Tg, c);
     cur = c;
     float sx, sy, sz;
     apply3(M, px, py, pz, sx, sy, sz);
@@ -243,7 +236,7 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
           }
         }
       }
-      steps_2d<ADAPTIVE, false, PPT>(px, py, nullptr, Tg, Ag, T, nx, ny, hh);
+      steps_2d<ADAPTIVE, PPT>(px, py, Tg, Ag, T, nx, ny, hh);
     }  // stages
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
@@ -252,70 +245,6 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
         o[p] = px[k];
         o[p + nP] = py[k];
       }
-    }
-  }
-}
-
-// Chain forward (K > 1) with each stage's table staged in LDS.  The grid
-// covers every point in one pass (PPT per lane), so the stage loop is uniform
-// across the workgroup and the table can be swapped between stages; a chain
-// over few points has only a handful of waves per SIMD, and LDS latency
-// instead of L1/L2 latency on the frequent per-wave table re-reads is what
-// keeps them busy.  One point per lane: with so few trajectories, twice the
-// waves (each one stream of dependent steps) hide the per-step branch and
-// scalar work better than two interleaved points per wave (C5, 262,144
-// points x 8 stages: 126 against 176 us).
-template <bool ADAPTIVE, int PPT>
-__global__ __launch_bounds__(1024) void chain2d_lds_kernel(int nP, int batched, int T, int nx,
-                                                          int ny, int K,
-                                                          const float* __restrict__ points,
-                                                          const float* __restrict__ Trels,
-                                                          const float* __restrict__ As,
-                                                          float* __restrict__ out,
-                                                          float* __restrict__ stage_points) {
-  extern __shared__ float lds[];
-  const int b = blockIdx.y;
-  const int n_batch = gridDim.y;
-  const int nC = 4 * nx * ny;
-  const float hh = 0.5f / (float)T;
-  const float* __restrict__ pts = points + (batched ? (size_t)b * 2 * nP : 0);
-  const int stride = gridDim.x * blockDim.x;
-  const int p0 = blockIdx.x * blockDim.x + threadIdx.x;
-  float px[PPT], py[PPT];
-#pragma unroll
-  for (int k = 0; k < PPT; ++k) {
-    const int p = min(p0 + k * stride, nP - 1);
-    px[k] = pts[p];
-    py[k] = pts[p + nP];
-  }
-  for (int st = 0; st < K; ++st) {
-    const size_t row = (size_t)st * n_batch + b;
-    if (st > 0) __syncthreads();  // every lane is done with the previous table
-    stage(lds, Trels + row * nC * 6, nC * 6);
-    __syncthreads();
-    if (st > 0 && stage_points) {
-      float* sp = stage_points + ((size_t)(st - 1) * n_batch + b) * 2 * nP;
-#pragma unroll
-      for (int k = 0; k < PPT; ++k) {
-        const int p = p0 + k * stride;
-        if (p < nP) {
-          sp[p] = px[k];
-          sp[p + nP] = py[k];
-        }
-      }
-    }
-    // One trajectory per lane leaves few waves: the select form of the lookup
-    // (a shorter dependency chain) measured faster here.
-    steps_2d<ADAPTIVE, true, PPT, false>(px, py, lds, Trels + row * nC * 6, As + row * nC * 6, T,
-                                         nx, ny, hh);
-  }
-  float* __restrict__ o = out + (size_t)b * 2 * nP;
-#pragma unroll
-  for (int k = 0; k < PPT; ++k) {
-    const int p = p0 + k * stride;
-    if (p < nP) {
-      o[p] = px[k];
-      o[p + nP] = py[k];
     }
   }
 }
@@ -346,7 +275,7 @@ __global__ __launch_bounds__(1024) void fwd3d_kernel(int nP, int batched, int T,
         sp[p + nP] = py;
         sp[p + 2 * (size_t)nP] = pz;
       }
-      steps_3d<ADAPTIVE, false>(px, py, pz, nullptr, Tg, Ag, T, nx, ny, nz, hh);
+      steps_3d<ADAPTIVE>(px, py, pz, Tg, Ag, T, nx, ny, nz, hh);
     }  // stages
     o[p] = px;
     o[p + nP] = py;
@@ -391,11 +320,11 @@ __global__ __launch_bounds__(1024) void image_forward_kernel(
       x[0] = closed_form_1d(x[0], 1.0f, Ag, nx);
     } else if (ND == 2) {
       float px[1] = {x[0]}, py[1] = {x[1]};
-      steps_2d<ADAPTIVE, false, 1>(px, py, nullptr, Tg, Ag, T, nx, ny, hh);
+      steps_2d<ADAPTIVE, 1>(px, py, Tg, Ag, T, nx, ny, hh);
       x[0] = px[0];
       x[1] = py[0];
     } else {
-      steps_3d<ADAPTIVE, false>(x[0], x[1], x[2], nullptr, Tg, Ag, T, nx, ny, nz, hh);
+      steps_3d<ADAPTIVE>(x[0], x[1], x[2], Tg, Ag, T, nx, ny, nz, hh);
     }
     if (fin) {
 #pragma unroll
@@ -474,16 +403,11 @@ __global__ __launch_bounds__(256) void trace_cells_kernel(int ndim, int nP, int 
 }
 
 template <typename Kern>
-hipError_t launch_with_lds(Kern kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s,
-                           int nP, int batched, int T, int nx, int ny, int K, const float* points,
-                           const float* Trels, const float* As, float* out, float* stage_points) {
-  if (lds > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-  }
-  hipLaunchKernelGGL(kernel, grid, block, lds, s, nP, batched, T, nx, ny, K, points, Trels, As,
-                     out, stage_points);
+hipError_t launch2d(Kern kernel, dim3 grid, dim3 block, hipStream_t s, int nP, int batched, int T,
+                    int nx, int ny, int K, const float* points, const float* Trels,
+                    const float* As, float* out, float* stage_points) {
+  hipLaunchKernelGGL(kernel, grid, block, 0, s, nP, batched, T, nx, ny, K, points, Trels, As, out,
+                     stage_points);
   return hipGetLastError();
 }
 
@@ -506,28 +430,28 @@ hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_batch, int ba
                           hipStream_t s) {
   if (nP <= 0 || n_batch <= 0 || K <= 0) return hipSuccess;
   const dim3 grid((unsigned)cfg.chunks, (unsigned)n_batch), block((unsigned)cfg.block);
-  const size_t tab = (size_t)g.nC * g.ppc() * sizeof(float);
-  if (g.ndim == 2 && K > 1 && tab <= (size_t)cfg.lds_chain) {
-    // one pass over the points, one point per lane
-    const int64_t need = (nP + (int64_t)cfg.block - 1) / (int64_t)cfg.block;
-    const dim3 gridc((unsigned)need, (unsigned)n_batch);
-    return adaptive ? launch_with_lds(chain2d_lds_kernel<true, 1>, gridc, block, tab, s, (int)nP,
-                                      batched, T, g.nx, g.ny, K, points, Trels, As, out,
-                                      stage_points)
-                    : launch_with_lds(chain2d_lds_kernel<false, 1>, gridc, block, tab, s, (int)nP,
-                                      batched, T, g.nx, g.ny, K, points, Trels, As, out,
-                                      stage_points);
-  }
   if (g.ndim == 2) {
     if (adaptive)
-      return launch_with_lds(fwd2d_kernel<true, 1>, grid, block, 0, s, (int)nP, batched, T, g.nx,
+      return launch2d(fwd2d_kernel<true, 1>, grid, block, s, (int)nP, batched, T, g.nx,
                              g.ny, K, points, Trels, As, out, stage_points);
+    if (K > 1) {
+      // A chain runs every stage of a trajectory in one lane, so few points
+      // (C5: 262,144, 4 waves per SIMD) leave the kernel latency-bound: one
+      // point per lane, one pass over the points, and no barrier between
+      // stages (each wave reads the stage tables through L1/L2 at its own
+      // pace; staging them in LDS held every workgroup to its slowest wave at
+      // each stage: C5 forward 123 -> 116 us).
+      const int64_t need1 = (nP + (int64_t)cfg.block - 1) / (int64_t)cfg.block;
+      const dim3 grid1((unsigned)need1, (unsigned)n_batch);
+      return launch2d(fwd2d_kernel<false, 1>, grid1, block, s, (int)nP, batched, T, g.nx,
+                             g.ny, K, points, Trels, As, out, stage_points);
+    }
     // Two points per lane: no more workgroups than it takes to cover nP once
     // (a lane's second point would otherwise duplicate work on a clamped index).
     const int64_t need = (nP + 2 * (int64_t)cfg.block - 1) / (2 * (int64_t)cfg.block);
     const dim3 grid2((unsigned)std::max<int64_t>(1, std::min<int64_t>(cfg.chunks, need)),
                      (unsigned)n_batch);
-    return launch_with_lds(fwd2d_kernel<false, 2>, grid2, block, 0, s, (int)nP, batched, T, g.nx,
+    return launch2d(fwd2d_kernel<false, 2>, grid2, block, s, (int)nP, batched, T, g.nx,
                            g.ny, K, points, Trels, As, out, stage_points);
   }
   // 3D: the kernel takes nz as an extra argument.
