@@ -452,7 +452,9 @@ int image_shape(int ndim, int64_t n_batch, int64_t C, const int64_t* in_size,
     if (in_size[k] < 1 || out_size[k] < 1) return fail(CPAB_ERR_INVALID, "sizes must be >= 1 (axis %d)", k);
     nP *= out_size[k];
     plane *= in_size[k];
-    if (nP >= (1LL << 31) || plane >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "image too large");
+    if (nP >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "image too large");
+    // the gathers address one channel with 32-bit byte offsets
+    if (plane > (1LL << 30)) return fail(CPAB_ERR_INVALID, "one data channel must hold at most 2^30 values");
   }
   if (n_batch * C * std::max(nP, plane) >= (1LL << 40)) return fail(CPAB_ERR_INVALID, "problem too large");
   *img = cpab::ImageShape{};
@@ -794,17 +796,20 @@ static int check_interp(int ndim, int64_t B, int64_t C, const int64_t* in_size,
   if (ndim < 1 || ndim > 3) return fail(CPAB_ERR_INVALID, "interpolation supports ndim 1, 2, 3, got %d", ndim);
   CPAB_REQUIRE(in_size); CPAB_REQUIRE(out_size);
   if (B < 0 || C < 0) return fail(CPAB_ERR_INVALID, "negative batch or channel count");
-  int64_t n = 1;
+  int64_t n = 1, plane = 1;
   for (int k = 0; k < ndim; ++k) {
     if (in_size[k] < 1) return fail(CPAB_ERR_INVALID, "input size %d must be >= 1", k);
     if (out_size[k] < 0) return fail(CPAB_ERR_INVALID, "output size %d must be >= 0", k);
     if (out_size[k] >= (1LL << 31) || in_size[k] >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "size too large");
+    // checked per axis, so that the products cannot overflow
+    if (out_size[k] > 0 && n > ((1LL << 40) - 1) / out_size[k]) return fail(CPAB_ERR_INVALID, "problem too large");
     n *= out_size[k];
+    plane *= in_size[k];
+    // the gathers address one channel with 32-bit byte offsets
+    if (plane > (1LL << 30)) return fail(CPAB_ERR_INVALID, "one data channel must hold at most 2^30 values");
   }
-  if (B * n * (C > 0 ? C : 1) >= (1LL << 40)) return fail(CPAB_ERR_INVALID, "problem too large");
-  int64_t plane = 1;
-  for (int k = 0; k < ndim; ++k) plane *= in_size[k];
-  if (plane >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "one data channel must hold < 2^31 values");
+  const int64_t lim = (1LL << 40) - 1, c1 = C > 0 ? C : 1;
+  if (n > 0 && (B > lim / n || B * n > lim / c1)) return fail(CPAB_ERR_INVALID, "problem too large");
   if (ndim >= 2) {
     // one workgroup per tile, 1D grid (fewer than 2^31 threads)
     const int64_t tiles = div_up(out_size[0], cpab::kInterpTile0) *

@@ -35,8 +35,8 @@ __device__ __forceinline__ float lerp_ref(float a, float b, float t) {
   return __fadd_rn(__fmul_rn(a, u), __fmul_rn(b, t));
 }
 
-// Offset of (x, y, z) inside one [in[0], in[1](, in[2])] plane (< 2^31, checked
-// by the C-ABI layer).
+// Offset of (x, y, z) inside one [in[0], in[1](, in[2])] plane (at most 2^30
+// values, checked by the C-ABI layer).
 template <int ND>
 __device__ __forceinline__ int plane_index(const int* in, int x, int y, int z) {
   if (ND == 1) return x;
@@ -44,106 +44,210 @@ __device__ __forceinline__ int plane_index(const int* in, int x, int y, int z) {
   return (x * in[1] + y) * in[2] + z;
 }
 
-template <int ND>
-__device__ __forceinline__ float sample(const int* in, const float* __restrict__ d, const Axis& ax,
-                                        const Axis& ay, const Axis& az) {
-  if (ND == 1) return lerp_ref(d[ax.i0], d[ax.i1], ax.t);
-  if (ND == 2) {
-    const float c00 = d[plane_index<2>(in, ax.i0, ay.i0, 0)];
-    const float c01 = d[plane_index<2>(in, ax.i0, ay.i1, 0)];
-    const float c10 = d[plane_index<2>(in, ax.i1, ay.i0, 0)];
-    const float c11 = d[plane_index<2>(in, ax.i1, ay.i1, 0)];
-    return lerp_ref(lerp_ref(c00, c10, ax.t), lerp_ref(c01, c11, ax.t), ay.t);
+// d[i] for 0 <= i < 2^30, addressed as a 32-bit byte offset from d.  When d
+// is the same for the whole wave (one data channel) the load takes d as its
+// scalar base and each lane carries one 32-bit offset, instead of a 64-bit
+// address per lane and load.
+__device__ __forceinline__ float load_at(const float* __restrict__ d, int i) {
+  return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(d) + ((uint32_t)i << 2));
+}
+
+// One data channel as a raw buffer resource: its 64-bit base and byte size sit
+// in scalar registers and each lane supplies a 32-bit byte offset (with a
+// pointer that the compiler hoists out of a channel loop, the offsets would
+// become 64-bit per lane and load).  A read past the size returns 0.
+struct ChannelBuf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ ChannelBuf(const float* d, int64_t n)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(d), (short)0,
+                                            (int)(uint32_t)min(n * 4, (int64_t)0xFFFFFFFF),
+                                            0x00020000)) {}   // dword 3 of a raw gfx9 buffer
+  __device__ __forceinline__ float operator()(int i) const {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)((uint32_t)i << 2), 0, 0));
   }
-  float c[2][2][2];
+  // d[i] and d[i + 1] with one 8-byte load (4-byte aligned; the HSA runtime
+  // runs the vector memory path in unaligned mode).
+  __device__ __forceinline__ float2 pair(int i) const {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)((uint32_t)i << 2), 0, 0);
+    const unsigned int lo = v[0], hi = v[1];   // (bit-casting v[k] directly reads v[0] twice)
+    return make_float2(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
+  }
+};
+
+// A data channel read through load_at.
+struct ChannelPtr {
+  const float* __restrict__ d;
+  __device__ __forceinline__ float operator()(int i) const { return load_at(d, i); }
+};
+
+// gd[i] += v (float atomic), addressed like load_at.
+__device__ __forceinline__ void add_at(float* __restrict__ gd, int i, float v) {
+  unsafeAtomicAdd(reinterpret_cast<float*>(reinterpret_cast<char*>(gd) + ((uint32_t)i << 2)), v);
+}
+
+// The 2^ND corner values of one sample from channel src (ChannelBuf or
+// ChannelPtr), c[(a << 2) | (b << 1) | e] for the corner
+// (a ? x1 : x0, b ? y1 : y0, e ? z1 : z0) (2D: c[(a << 1) | b]).
+template <int ND, class Src>
+__device__ __forceinline__ void gather(const int* in, const Src& src, const Axis& ax,
+                                       const Axis& ay, const Axis& az, float* c) {
+  if (ND == 1) {
+    c[0] = src(ax.i0);
+    c[1] = src(ax.i1);
+    return;
+  }
+  if (ND == 2) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        c[(a << 1) | b] = src(plane_index<2>(in, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, 0));
+    return;
+  }
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int e = 0; e < 2; ++e)
-        c[a][b][e] = d[plane_index<3>(in, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, e ? az.i1 : az.i0)];
-  const float c00 = lerp_ref(c[0][0][0], c[1][0][0], ax.t);
-  const float c01 = lerp_ref(c[0][0][1], c[1][0][1], ax.t);
-  const float c10 = lerp_ref(c[0][1][0], c[1][1][0], ax.t);
-  const float c11 = lerp_ref(c[0][1][1], c[1][1][1], ax.t);
-  return lerp_ref(lerp_ref(c00, c10, ay.t), lerp_ref(c01, c11, ay.t), az.t);
+        c[(a << 2) | (b << 1) | e] =
+            src(plane_index<3>(in, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, e ? az.i1 : az.i0));
 }
 
-// d out / d (x, y, z) for one channel with upstream gradient g (before the
-// (size-1) chain factor), added into dxyz, and the corner scatter for
-// grad_data (gd, may be null).
+// gather() from a ChannelBuf with the corners paired along the contiguous
+// (last) data axis: one 8-byte load reads (.., s) and (.., s + 1) with
+// s = min(i0, size - 2) on that axis, which holds both of its corner indices
+// (i1 = i0 + 1, or both clamped to 0 or to size - 1).  Needs that axis'
+// size >= 2; half the load instructions of gather().
 template <int ND>
-__device__ __forceinline__ void sample_grad(const int* in, const float* __restrict__ d,
-                                            const Axis& ax, const Axis& ay, const Axis& az,
-                                            float g, float* dxyz, float* __restrict__ gd) {
-  const float ux = 1.0f - ax.t, uy = 1.0f - ay.t, uz = 1.0f - az.t;
+__device__ __forceinline__ void gather_pairs(const int* in, const ChannelBuf& src, const Axis& ax,
+                                             const Axis& ay, const Axis& az, float* c) {
+  const Axis& last = ND == 1 ? ax : (ND == 2 ? ay : az);
+  const int s = min(last.i0, in[ND - 1] - 2);
+  const bool lo_up = last.i0 != s;   // i0 == s + 1 (clamped to size - 1)
+  const bool hi_up = last.i1 != s;   // i1 == s + 1
   if (ND == 1) {
-    if (dxyz) dxyz[0] += g * (d[ax.i1] - d[ax.i0]);
-    if (gd) {
-      unsafeAtomicAdd(gd + ax.i0, g * ux);
-      unsafeAtomicAdd(gd + ax.i1, g * ax.t);
-    }
+    const float2 p = src.pair(s);
+    c[0] = lo_up ? p.y : p.x;
+    c[1] = hi_up ? p.y : p.x;
     return;
   }
   if (ND == 2) {
-    const int i00 = plane_index<2>(in, ax.i0, ay.i0, 0), i01 = plane_index<2>(in, ax.i0, ay.i1, 0);
-    const int i10 = plane_index<2>(in, ax.i1, ay.i0, 0), i11 = plane_index<2>(in, ax.i1, ay.i1, 0);
-    if (dxyz) {
-      const float c00 = d[i00], c01 = d[i01], c10 = d[i10], c11 = d[i11];
-      const float c0 = lerp_ref(c00, c10, ax.t), c1 = lerp_ref(c01, c11, ax.t);
-      dxyz[0] += g * uy * (c10 - c00) + g * ay.t * (c11 - c01);
-      dxyz[1] += g * (c1 - c0);
-    }
-    if (gd) {
-      const float g0 = g * uy, g1 = g * ay.t;
-      unsafeAtomicAdd(gd + i00, g0 * ux);
-      unsafeAtomicAdd(gd + i10, g0 * ax.t);
-      unsafeAtomicAdd(gd + i01, g1 * ux);
-      unsafeAtomicAdd(gd + i11, g1 * ax.t);
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const float2 p = src.pair(plane_index<2>(in, a ? ax.i1 : ax.i0, s, 0));
+      c[(a << 1) | 0] = lo_up ? p.y : p.x;
+      c[(a << 1) | 1] = hi_up ? p.y : p.x;
     }
     return;
   }
-  int idx[2][2][2];
-  float c[2][2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const float2 p = src.pair(plane_index<3>(in, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, s));
+      c[(a << 2) | (b << 1) | 0] = lo_up ? p.y : p.x;
+      c[(a << 2) | (b << 1) | 1] = hi_up ? p.y : p.x;
+    }
+}
+
+// The interpolated value from the corners of gather().
+template <int ND>
+__device__ __forceinline__ float blend(const float* c, const Axis& ax, const Axis& ay,
+                                       const Axis& az) {
+  if (ND == 1) return lerp_ref(c[0], c[1], ax.t);
+  if (ND == 2) return lerp_ref(lerp_ref(c[0], c[2], ax.t), lerp_ref(c[1], c[3], ax.t), ay.t);
+  const float c00 = lerp_ref(c[0], c[4], ax.t);
+  const float c01 = lerp_ref(c[1], c[5], ax.t);
+  const float c10 = lerp_ref(c[2], c[6], ax.t);
+  const float c11 = lerp_ref(c[3], c[7], ax.t);
+  return lerp_ref(lerp_ref(c00, c10, ay.t), lerp_ref(c01, c11, ay.t), az.t);
+}
+
+template <int ND>
+__device__ __forceinline__ float sample(const int* in, const float* __restrict__ d, const Axis& ax,
+                                        const Axis& ay, const Axis& az) {
+  float c[1 << ND];
+  gather<ND>(in, ChannelPtr{d}, ax, ay, az, c);
+  return blend<ND>(c, ax, ay, az);
+}
+
+// d out / d (x, y, z) for one channel with upstream gradient g (before the
+// (size-1) chain factor) from the corners of gather(), added into dxyz.
+template <int ND>
+__device__ __forceinline__ void blend_grad(const float* c, const Axis& ax, const Axis& ay,
+                                           const Axis& az, float g, float* dxyz) {
+  if (ND == 1) {
+    dxyz[0] += g * (c[1] - c[0]);
+    return;
+  }
+  const float uy = 1.0f - ay.t;
+  if (ND == 2) {
+    const float c00 = c[0], c01 = c[1], c10 = c[2], c11 = c[3];
+    const float c0 = lerp_ref(c00, c10, ax.t), c1 = lerp_ref(c01, c11, ax.t);
+    dxyz[0] += g * uy * (c10 - c00) + g * ay.t * (c11 - c01);
+    dxyz[1] += g * (c1 - c0);
+    return;
+  }
+  const float uz = 1.0f - az.t;
+  // Along x: the four (y, z) lines; along y: the two z planes; along z: the two halves.
+  const float wyz[2][2] = {{uy * uz, uy * az.t}, {ay.t * uz, ay.t * az.t}};
+  float gx = 0.0f;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) gx += wyz[b][e] * (c[4 | (b << 1) | e] - c[(b << 1) | e]);
+  const float c00 = lerp_ref(c[0], c[4], ax.t);
+  const float c01 = lerp_ref(c[1], c[5], ax.t);
+  const float c10 = lerp_ref(c[2], c[6], ax.t);
+  const float c11 = lerp_ref(c[3], c[7], ax.t);
+  const float gy = uz * (c10 - c00) + az.t * (c11 - c01);
+  const float gz = lerp_ref(c01, c11, ay.t) - lerp_ref(c00, c10, ay.t);
+  dxyz[0] += g * gx;
+  dxyz[1] += g * gy;
+  dxyz[2] += g * gz;
+}
+
+// The corner scatter of grad_data: g times each corner's weight added into gd.
+template <int ND>
+__device__ __forceinline__ void scatter(const int* in, float* __restrict__ gd, const Axis& ax,
+                                        const Axis& ay, const Axis& az, float g) {
+  const float ux = 1.0f - ax.t, uy = 1.0f - ay.t, uz = 1.0f - az.t;
+  if (ND == 1) {
+    add_at(gd, ax.i0, g * ux);
+    add_at(gd, ax.i1, g * ax.t);
+    return;
+  }
+  if (ND == 2) {
+    const float g0 = g * uy, g1 = g * ay.t;
+    add_at(gd, plane_index<2>(in, ax.i0, ay.i0, 0), g0 * ux);
+    add_at(gd, plane_index<2>(in, ax.i1, ay.i0, 0), g0 * ax.t);
+    add_at(gd, plane_index<2>(in, ax.i0, ay.i1, 0), g1 * ux);
+    add_at(gd, plane_index<2>(in, ax.i1, ay.i1, 0), g1 * ax.t);
+    return;
+  }
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        idx[a][b][e] = plane_index<3>(in, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, e ? az.i1 : az.i0);
-        c[a][b][e] = dxyz ? d[idx[a][b][e]] : 0.0f;
+        const float w = (a ? ax.t : ux) * (b ? ay.t : uy) * (e ? az.t : uz);
+        add_at(gd, plane_index<3>(in, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, e ? az.i1 : az.i0), g * w);
       }
+}
+
+// blend_grad into dxyz (may be null) and scatter into gd (may be null).
+template <int ND>
+__device__ __forceinline__ void sample_grad(const int* in, const float* __restrict__ d,
+                                            const Axis& ax, const Axis& ay, const Axis& az,
+                                            float g, float* dxyz, float* __restrict__ gd) {
   if (dxyz) {
-    // Along x: the four (y, z) lines; along y: the two z planes; along z: the two halves.
-    const float wyz[2][2] = {{uy * uz, uy * az.t}, {ay.t * uz, ay.t * az.t}};
-    float gx = 0.0f;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int e = 0; e < 2; ++e) gx += wyz[b][e] * (c[1][b][e] - c[0][b][e]);
-    const float c00 = lerp_ref(c[0][0][0], c[1][0][0], ax.t);
-    const float c01 = lerp_ref(c[0][0][1], c[1][0][1], ax.t);
-    const float c10 = lerp_ref(c[0][1][0], c[1][1][0], ax.t);
-    const float c11 = lerp_ref(c[0][1][1], c[1][1][1], ax.t);
-    const float gy = uz * (c10 - c00) + az.t * (c11 - c01);
-    const float gz = lerp_ref(c01, c11, ay.t) - lerp_ref(c00, c10, ay.t);
-    dxyz[0] += g * gx;
-    dxyz[1] += g * gy;
-    dxyz[2] += g * gz;
+    float c[1 << ND];
+    gather<ND>(in, ChannelPtr{d}, ax, ay, az, c);
+    blend_grad<ND>(c, ax, ay, az, g, dxyz);
   }
-  if (gd) {
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float w = (a ? ax.t : ux) * (b ? ay.t : uy) * (e ? az.t : uz);
-          unsafeAtomicAdd(gd + idx[a][b][e], g * w);
-        }
-  }
+  if (gd) scatter<ND>(in, gd, ax, ay, az, g);
 }
 
 }  // namespace cpab

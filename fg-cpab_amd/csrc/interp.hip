@@ -24,8 +24,14 @@ namespace {
 constexpr int kT0 = kInterpTile0;      // tile extent along i0 (grid rows are contiguous in i0)
 constexpr int kTL = kInterpTileLast;   // tile extent along i_last (output rows are contiguous in i_last)
 constexpr int kThreads = kInterpThreads;
-static_assert(kThreads % kTL == 0 && kT0 % 4 == 0 && 64 % kTL == 0, "tile shape");
-constexpr int kUnroll = 4;   // outputs in flight per lane in the compute loop
+static_assert(kThreads % kTL == 0 && kT0 % 4 == 0 && 64 % kTL == 0 && kT0 % (kThreads / kTL) == 0,
+              "tile shape");
+constexpr int kRows = kThreads / kTL;   // tile rows (along i0) a workgroup covers per pass
+constexpr int kPerLane = kT0 / kRows;   // outputs per lane in a whole tile
+// Outputs per lane whose gathers are issued together: 16 loads in flight per
+// lane in 2D and 3D (the 3D batch of 4 would need ~250 VGPRs in the backward).
+constexpr int gather_batch(int nd) { return nd == 3 ? 2 : 4; }
+static_assert(kPerLane % gather_batch(2) == 0 && kPerLane % gather_batch(3) == 0, "batches");
 constexpr int kXcds = 8;     // MI355X: accelerator complex dies, each with its own L2
 
 struct Shape {
@@ -107,25 +113,61 @@ __global__ __launch_bounds__(kThreads) void interp_fwd_kernel(Shape s,
   load_tile<ND>(s, grid, b, im, t0, tl, n0, nl, crd);
   __syncthreads();
   const int al = threadIdx.x % kTL;   // lanes along i_last
-  const int w = threadIdx.x / kTL;    // kThreads / kTL rows at a time
+  const int w = threadIdx.x / kTL;    // kRows rows at a time
   const int64_t plane_in = (int64_t)s.in[0] * s.in[1] * (ND == 3 ? s.in[2] : 1);
   const int64_t plane_out = (int64_t)s.o0 * s.omid * s.olast;
+  const int64_t ostride = (int64_t)s.omid * s.olast;   // next i0 in the output
+  const bool pairs = s.in[ND - 1] >= 2;                // corners read in pairs
   if (al >= nl) return;
+  if (n0 == kT0) {
+    // Whole tile along i0: a lane's outputs are independent, so the gathers of
+    // gather_batch of them are in flight before the first result is needed.
+    constexpr int NB = gather_batch(ND);
+#pragma unroll
+    for (int j0 = 0; j0 < kPerLane; j0 += NB) {
+      Axis ax[NB], ay[NB], az[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int a0 = w + (j0 + j) * kRows;
+        ax[j] = axis_of(crd[0][al][a0], s.in[0]);
+        ay[j] = axis_of(crd[1][al][a0], s.in[1]);
+        az[j] = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
+      }
+      for (int ch = 0; ch < s.C; ++ch) {
+        const int64_t bc = (int64_t)b * s.C + ch;
+        const ChannelBuf d(data + bc * plane_in, plane_in);
+        float* __restrict__ o = out + bc * plane_out + (int64_t)(t0 + w + j0 * kRows) * ostride +
+                                (int64_t)im * s.olast + tl + al;
+        float c[NB][1 << ND];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          if (pairs) gather_pairs<ND>(s.in, d, ax[j], ay[j], az[j], c[j]);
+          else gather<ND>(s.in, d, ax[j], ay[j], az[j], c[j]);
+        }
+        // keeps the batch's loads issued before the first blend waits for one
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) o[j * kRows * ostride] = blend<ND>(c[j], ax[j], ay[j], az[j]);
+      }
+    }
+    return;
+  }
   for (int ch = 0; ch < s.C; ++ch) {
     const int64_t bc = (int64_t)b * s.C + ch;
     const float* __restrict__ d = data + bc * plane_in;
     float* __restrict__ o = out + bc * plane_out + (int64_t)im * s.olast + tl + al;
-#pragma unroll kUnroll
-    for (int a0 = w; a0 < n0; a0 += kThreads / kTL) {
+    for (int a0 = w; a0 < n0; a0 += kRows) {
       const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
       const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
       const Axis az = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
-      o[(int64_t)(t0 + a0) * s.omid * s.olast] = sample<ND>(s.in, d, ax, ay, az);
+      o[(int64_t)(t0 + a0) * ostride] = sample<ND>(s.in, d, ax, ay, az);
     }
   }
 }
 
-template <int ND>
+// GD: grad_data is requested (its scatter's state would otherwise cost every
+// launch registers).
+template <int ND, bool GD>
 __global__ __launch_bounds__(kThreads) void interp_bwd_kernel(Shape s,
                                                               const float* __restrict__ data,
                                                               const float* __restrict__ grid,
@@ -142,9 +184,62 @@ __global__ __launch_bounds__(kThreads) void interp_bwd_kernel(Shape s,
   const int w = threadIdx.x / kTL;
   const int64_t plane_in = (int64_t)s.in[0] * s.in[1] * (ND == 3 ? s.in[2] : 1);
   const int64_t plane_out = (int64_t)s.o0 * s.omid * s.olast;
-  if (al < nl) {
-#pragma unroll kUnroll
-    for (int a0 = w; a0 < n0; a0 += kThreads / kTL) {
+  const bool pairs = s.in[ND - 1] >= 2;   // corners read in pairs
+  if (al < nl && n0 == kT0) {
+    // Whole tile along i0: the gathers of gather_batch outputs of a lane
+    // overlap.
+    constexpr int NB = gather_batch(ND);
+#pragma unroll
+    for (int j0 = 0; j0 < kPerLane; j0 += NB) {
+      Axis ax[NB], ay[NB], az[NB];
+      float dd[NB][3];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int a0 = w + (j0 + j) * kRows;
+        ax[j] = axis_of(crd[0][al][a0], s.in[0]);
+        ay[j] = axis_of(crd[1][al][a0], s.in[1]);
+        az[j] = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
+        dd[j][0] = dd[j][1] = dd[j][2] = 0.0f;
+      }
+      const int64_t o = ((int64_t)(t0 + w + j0 * kRows) * s.omid + im) * s.olast + tl + al;
+      for (int ch = 0; ch < s.C; ++ch) {
+        const int64_t bc = (int64_t)b * s.C + ch;
+        const ChannelBuf d(data + bc * plane_in, plane_in);
+        const float* __restrict__ go = grad_out + bc * plane_out + o;
+        float g[NB], c[NB][1 << ND];
+        if (grad_grid) {
+#pragma unroll
+          for (int j = 0; j < NB; ++j) {
+            if (pairs) gather_pairs<ND>(s.in, d, ax[j], ay[j], az[j], c[j]);
+            else gather<ND>(s.in, d, ax[j], ay[j], az[j], c[j]);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) g[j] = go[(int64_t)j * kRows * s.omid * s.olast];
+        // keeps the batch's loads issued before the first use of one
+        __builtin_amdgcn_sched_barrier(0);
+        if (grad_grid) {
+#pragma unroll
+          for (int j = 0; j < NB; ++j) blend_grad<ND>(c[j], ax[j], ay[j], az[j], g[j], dd[j]);
+        }
+        if (GD) {
+          float* __restrict__ gd = grad_data + bc * plane_in;
+#pragma unroll
+          for (int j = 0; j < NB; ++j) scatter<ND>(s.in, gd, ax[j], ay[j], az[j], g[j]);
+        }
+      }
+      if (grad_grid) {
+        // (size-1) chain factor of x = g*(size-1); each thread rewrites only
+        // the LDS slots it read.
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int k = 0; k < ND; ++k)
+            crd[k][al][w + (j0 + j) * kRows] = dd[j][k] * (float)(s.in[k] - 1);
+      }
+    }
+  } else if (al < nl) {
+    for (int a0 = w; a0 < n0; a0 += kRows) {
       const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
       const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
       const Axis az = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
@@ -153,11 +248,9 @@ __global__ __launch_bounds__(kThreads) void interp_bwd_kernel(Shape s,
       for (int ch = 0; ch < s.C; ++ch) {
         const int64_t bc = (int64_t)b * s.C + ch;
         sample_grad<ND>(s.in, data + bc * plane_in, ax, ay, az, grad_out[bc * plane_out + o],
-                        grad_grid ? dd : nullptr, grad_data ? grad_data + bc * plane_in : nullptr);
+                        grad_grid ? dd : nullptr, GD ? grad_data + bc * plane_in : nullptr);
       }
       if (grad_grid) {
-        // (size-1) chain factor of x = g*(size-1); each thread rewrites only
-        // the LDS slots it read.
 #pragma unroll
         for (int k = 0; k < ND; ++k) crd[k][al][a0] = dd[k] * (float)(s.in[k] - 1);
       }
@@ -206,7 +299,7 @@ __global__ __launch_bounds__(kThreads) void interp1d_fwd_kernel(int B, int C, in
     const Axis ax = axis_of(grid[e], W);
     for (int ch = 0; ch < C; ++ch) {
       const float* d = data + (b * C + ch) * W;
-      out[(b * C + ch) * nP + p] = lerp_ref(d[ax.i0], d[ax.i1], ax.t);
+      out[(b * C + ch) * nP + p] = lerp_ref(load_at(d, ax.i0), load_at(d, ax.i1), ax.t);
     }
   }
 }
@@ -226,10 +319,10 @@ __global__ __launch_bounds__(kThreads) void interp1d_bwd_kernel(int B, int C, in
       const int64_t bc = b * C + ch;
       const float g = grad_out[bc * nP + p];
       const float* d = data + bc * W;
-      gx += g * (d[ax.i1] - d[ax.i0]);
+      gx += g * (load_at(d, ax.i1) - load_at(d, ax.i0));
       if (grad_data) {
-        unsafeAtomicAdd(grad_data + bc * W + ax.i0, g * (1.0f - ax.t));
-        unsafeAtomicAdd(grad_data + bc * W + ax.i1, g * ax.t);
+        add_at(grad_data + bc * W, ax.i0, g * (1.0f - ax.t));
+        add_at(grad_data + bc * W, ax.i1, g * ax.t);
       }
     }
     if (grad_grid) grad_grid[e] = gx * (float)(W - 1);
@@ -302,12 +395,10 @@ hipError_t launch_interp_backward(int ndim, int64_t B, int64_t C, const int64_t*
     hipLaunchKernelGGL(interp1d_bwd_kernel, dim3((unsigned)g), dim3(kThreads), 0, st, s.B, s.C,
                        s.in[0], s.nP, data, grid, grad_out, grad_grid, grad_data);
   } else {
-    if (ndim == 2)
-      hipLaunchKernelGGL(interp_bwd_kernel<2>, tile_grid(s), dim3(kThreads), 0, st, s, data, grid,
-                         grad_out, grad_grid, grad_data);
-    else
-      hipLaunchKernelGGL(interp_bwd_kernel<3>, tile_grid(s), dim3(kThreads), 0, st, s, data, grid,
-                         grad_out, grad_grid, grad_data);
+    auto kernel = ndim == 2 ? (grad_data ? interp_bwd_kernel<2, true> : interp_bwd_kernel<2, false>)
+                            : (grad_data ? interp_bwd_kernel<3, true> : interp_bwd_kernel<3, false>);
+    hipLaunchKernelGGL(kernel, tile_grid(s), dim3(kThreads), 0, st, s, data, grid, grad_out,
+                       grad_grid, grad_data);
   }
   return hipGetLastError();
 }

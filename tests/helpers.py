@@ -79,3 +79,45 @@ def recover_growth(As, T=50):
     E = np.eye(nd) + h * L + h2 * (L @ L)
     s = np.linalg.norm(np.linalg.inv(E), ord=2, axis=(-2, -1))
     return s.max(axis=-1) ** T
+
+
+def scatter_magnitude(data_shape, grid, outs, gout):
+    """Per data pixel, the sum over its grad_data contributions of |g * w|
+    (float64), w being the corner weight of the point's resampling.
+
+    The reference clamps a corner index but not the fractional part
+    (interpolation.py:3-159), so a point outside [0, 1] gives two weights of
+    opposite sign and magnitude up to ~(size-1) that cancel in the sum (1 - t
+    and t).  A summation-order bound has to scale with the terms' absolute
+    values: summing the same n fp32 terms in two orders differs by at most
+    ~2 n 2^-24 of this magnitude.  grid [B, nd, nP] lists points with
+    coordinate 0 fastest; gout [B, C, *outs] has the last axis fastest."""
+    B, C = data_shape[:2]
+    ins = tuple(data_shape[2:])
+    nd = len(ins)
+    grid = np.asarray(grid, np.float64)
+    gp = np.asarray(gout, np.float64).reshape(B, C, *outs)
+    gp = gp.transpose(0, 1, *range(nd + 1, 1, -1)).reshape(B, C, -1)   # point order
+    mag = np.zeros((B, C, int(np.prod(ins))))
+    strides = [int(np.prod(ins[k + 1:])) for k in range(nd)]
+    for b in range(B):
+        lo, hi, wlo, whi = [], [], [], []
+        for k in range(nd):
+            x = grid[b, k] * (ins[k] - 1)
+            f = np.floor(x)
+            i0 = np.clip(f, 0, ins[k] - 1)
+            lo.append(i0.astype(np.int64) * strides[k])
+            hi.append(np.clip(f + 1, 0, ins[k] - 1).astype(np.int64) * strides[k])
+            t = x - i0
+            wlo.append(np.abs(1.0 - t))
+            whi.append(np.abs(t))
+        for corner in range(1 << nd):
+            idx = np.zeros_like(lo[0])
+            w = np.ones_like(wlo[0])
+            for k in range(nd):
+                up = (corner >> (nd - 1 - k)) & 1
+                idx = idx + (hi[k] if up else lo[k])
+                w = w * (whi[k] if up else wlo[k])
+            for c in range(C):
+                np.add.at(mag[b, c], idx, np.abs(gp[b, c]) * w)
+    return mag.reshape(B, C, *ins)

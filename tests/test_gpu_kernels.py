@@ -12,7 +12,7 @@ from cpab.pytorch.transformer import basis_tables
 from oracle import oracle as orc
 
 from helpers import (assert_adjoint_close, assert_grad_close, cpab_for, meshgrid, recover_growth,
-                     seeded_theta, uniform_points)
+                     scatter_magnitude, seeded_theta, uniform_points)
 
 pytestmark = pytest.mark.gpu
 
@@ -394,7 +394,11 @@ def test_project_bitexact(cuda, tess):
 
 @pytest.mark.parametrize("nd,ins,outs", [(2, (40, 56), (48, 36)), (3, (12, 10, 14), (9, 11, 13)),
                                          (1, (77,), (50,)), (2, (512, 512), (130, 70)),
-                                         (2, (64, 80), (96, 130)), (3, (12, 10, 14), (32, 3, 66))])
+                                         (2, (64, 80), (96, 130)), (3, (12, 10, 14), (32, 3, 66)),
+                                         # last data axis of size 1 or 2 (the whole-tile
+                                         # gathers read corner pairs along it when >= 2)
+                                         (2, (40, 1), (64, 64)), (3, (12, 10, 1), (32, 4, 32)),
+                                         (2, (3, 2), (64, 40)), (3, (5, 3, 2), (32, 2, 32))])
 def test_interp_parity(cuda, nd, ins, outs):
     rng = np.random.default_rng(30 + nd)
     B, C = 2, 3
@@ -414,9 +418,9 @@ def test_interp_parity(cuda, nd, ins, outs):
     # grad_data sums many contributions per pixel with float atomics (clamped
     # border points pile up, several hundred per pixel here) in an order that
     # differs from the oracle's sequential fp32 sum; both round each partial
-    # sum, so the difference is bounded by ~(count * 2^-24) of the summed
-    # contribution magnitudes of the pixel.
-    _, mag = orc.interp_backward(nd, data, grid, outs, np.abs(gout), dtype=np.float64)
+    # sum, so the difference is bounded by ~(2 count 2^-24) of the pixel's
+    # summed contribution magnitudes.
+    mag = scatter_magnitude(data.shape, grid, outs, gout)
     err = np.abs(gd.cpu().numpy().astype(np.float64) - rd)
     assert (err <= 1e-4 * mag + 1e-12).all(), float((err / (mag + 1e-30)).max())
 
@@ -578,7 +582,7 @@ def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive, scale):
     rg, rd = orc.interp_backward(nd, data, xT, outs, gout)
     ref_m, _ = orc.backward(grid_np, A, rg, p.nc, 50, adaptive=bool(adaptive))
     assert_grad_close(mom.cpu().numpy(), ref_m, rtol=2e-5)
-    _, mag = orc.interp_backward(nd, data, xT, outs, np.abs(gout), dtype=np.float64)
+    mag = scatter_magnitude(data.shape, xT, outs, gout)
     err = np.abs(gd.cpu().numpy().astype(np.float64) - rd)
     assert (err <= 1e-4 * mag + 1e-12).all(), float((err / (mag + 1e-30)).max())
 

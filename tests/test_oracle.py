@@ -13,7 +13,7 @@ from scipy.integrate import solve_ivp
 
 from oracle import oracle as orc
 
-from helpers import cpab_for, meshgrid, uniform_points
+from helpers import cpab_for, meshgrid, scatter_magnitude, uniform_points
 
 
 def _random_As(nC, nd, scale, seed, dtype=np.float32):
@@ -364,6 +364,30 @@ def test_interp_matches_textbook_bilinear():
             v = ((1 - tx) * (1 - ty) * data[b, :, x0, y0] + tx * (1 - ty) * data[b, :, x0 + 1, y0]
                  + (1 - tx) * ty * data[b, :, x0, y0 + 1] + tx * ty * data[b, :, x0 + 1, y0 + 1])
             np.testing.assert_allclose(out[b, :, i0, i1], v, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("nd", [1, 2, 3])
+def test_scatter_magnitude(nd):
+    # The grad_data tolerance scale of the GPU tests.  Points inside [0, 1]
+    # have weights in [0, 1], so it equals the float64 scatter of |gout|;
+    # clamped points add cancelling weights of both signs, which the
+    # magnitude counts in full.
+    rng = np.random.default_rng(95 + nd)
+    ins = (9, 7, 5)[:nd]
+    outs = (4, 6, 3)[:nd]
+    data = rng.random((2, 3, *ins)).astype(np.float32)
+    nP = int(np.prod(outs))
+    gout = rng.standard_normal((2, 3, *outs)).astype(np.float32)
+    inside = rng.random((2, nd, nP)).astype(np.float32)
+    _, ref = orc.interp_backward(nd, data, inside, outs, np.abs(gout), dtype=np.float64)
+    np.testing.assert_allclose(scatter_magnitude(data.shape, inside, outs, gout), ref, rtol=1e-12,
+                               atol=1e-12)
+    clamped = (rng.random((2, nd, nP)) * 2.0 - 0.5).astype(np.float32)
+    _, signed = orc.interp_backward(nd, data, clamped, outs, gout, dtype=np.float64)
+    _, plain = orc.interp_backward(nd, data, clamped, outs, np.abs(gout), dtype=np.float64)
+    mag = scatter_magnitude(data.shape, clamped, outs, gout)
+    assert (np.abs(signed) <= mag + 1e-12).all() and (np.abs(plain) <= mag + 1e-12).all()
+    assert (mag > np.abs(plain) + 1e-6).any()
 
 
 @pytest.mark.parametrize("nd", [2, 3])
