@@ -20,7 +20,9 @@
  *     transformer_cuda.cpp:43);
  *   - size limits (CPAB_ERR_INVALID beyond them): fewer than 2^24 cells
  *     (cell ids and table offsets are 24/32-bit in the kernels), nP below
- *     2^31 / 3, and n_theta (n_batch, n_stages * n_batch) below 65536.
+ *     2^31 / 3, n_theta (n_batch, n_stages * n_batch) below 65536, and at
+ *     most 2^30 values per data channel of the image entry points (the
+ *     gathers address a channel with 32-bit byte offsets).
  *
  * Layouts: theta [n_theta, d]; As/Trels [n_theta, nC, ndim, ndim+1] row-major;
  * moments [n_theta, nC, ndim*(ndim+1)]; points/outputs SoA rows [.., ndim, nP].
