@@ -16,8 +16,10 @@ struct Geometry {
 };
 
 // Resampling tiles: one workgroup of kInterpThreads per kInterpTile0 x
-// kInterpTileLast block of (i0, i_last) outputs.  Measured at C3 (16 x 512^2):
-// 32 x 32 tiles 16.5 / 22.6 us (fwd / bwd) against 19.1 / 23.4 us for 32 x 64.
+// kInterpTileLast block of (i0, i_last) outputs.  Swept at C3 (16 x 512^2) and
+// C4 (128^3) against 64 x 32, 32 x 64, 16 x 64 (256 threads), 32 x 32 with 512
+// threads and 16 x 32 with 128: 32 x 32 with 256 was fastest or within noise
+// in both.
 constexpr int kInterpTile0 = 32;
 constexpr int kInterpTileLast = 32;
 constexpr int kInterpThreads = 256;

@@ -28,9 +28,11 @@ static_assert(kThreads % kTL == 0 && kT0 % 4 == 0 && 64 % kTL == 0 && kT0 % (kTh
               "tile shape");
 constexpr int kRows = kThreads / kTL;   // tile rows (along i0) a workgroup covers per pass
 constexpr int kPerLane = kT0 / kRows;   // outputs per lane in a whole tile
-// Outputs per lane whose gathers are issued together: 16 loads in flight per
-// lane in 2D and 3D (the 3D batch of 4 would need ~250 VGPRs in the backward).
-constexpr int gather_batch(int nd) { return nd == 3 ? 2 : 4; }
+// Outputs per lane whose gathers the backward issues together (4 corner-pair
+// loads in flight per lane).  Larger batches cost occupancy: with the pairs,
+// batches of 4 (2D) and 2 (3D) ran the C3 backward 14% and the C4 backward 8%
+// slower.
+constexpr int gather_batch(int nd) { return nd == 3 ? 1 : 2; }
 static_assert(kPerLane % gather_batch(2) == 0 && kPerLane % gather_batch(3) == 0, "batches");
 constexpr int kXcds = 8;     // MI355X: accelerator complex dies, each with its own L2
 
@@ -120,34 +122,31 @@ __global__ __launch_bounds__(kThreads) void interp_fwd_kernel(Shape s,
   const bool pairs = s.in[ND - 1] >= 2;                // corners read in pairs
   if (al >= nl) return;
   if (n0 == kT0) {
-    // Whole tile along i0: a lane's outputs are independent, so the gathers of
-    // gather_batch of them are in flight before the first result is needed.
-    constexpr int NB = gather_batch(ND);
+    // Whole tile along i0, software-pipelined: the corner loads of a lane's
+    // next output are issued before the current output is blended and stored.
+    for (int ch = 0; ch < s.C; ++ch) {
+      const int64_t bc = (int64_t)b * s.C + ch;
+      const ChannelBuf d(data + bc * plane_in, plane_in);
+      float* __restrict__ o = out + bc * plane_out + (int64_t)(t0 + w) * ostride +
+                              (int64_t)im * s.olast + tl + al;
+      Axis ax[2], ay[2], az[2];
+      float c[2][1 << ND];
 #pragma unroll
-    for (int j0 = 0; j0 < kPerLane; j0 += NB) {
-      Axis ax[NB], ay[NB], az[NB];
-#pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const int a0 = w + (j0 + j) * kRows;
-        ax[j] = axis_of(crd[0][al][a0], s.in[0]);
-        ay[j] = axis_of(crd[1][al][a0], s.in[1]);
-        az[j] = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
-      }
-      for (int ch = 0; ch < s.C; ++ch) {
-        const int64_t bc = (int64_t)b * s.C + ch;
-        const ChannelBuf d(data + bc * plane_in, plane_in);
-        float* __restrict__ o = out + bc * plane_out + (int64_t)(t0 + w + j0 * kRows) * ostride +
-                                (int64_t)im * s.olast + tl + al;
-        float c[NB][1 << ND];
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-          if (pairs) gather_pairs<ND>(s.in, d, ax[j], ay[j], az[j], c[j]);
-          else gather<ND>(s.in, d, ax[j], ay[j], az[j], c[j]);
+      for (int j = -1; j < kPerLane; ++j) {
+        if (j + 1 < kPerLane) {
+          const int n = (j + 1) & 1;
+          const int a0 = w + (j + 1) * kRows;
+          ax[n] = axis_of(crd[0][al][a0], s.in[0]);
+          ay[n] = axis_of(crd[1][al][a0], s.in[1]);
+          az[n] = ND == 3 ? axis_of(crd[ND - 1][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
+          if (pairs) gather_pairs<ND>(s.in, d, ax[n], ay[n], az[n], c[n]);
+          else gather<ND>(s.in, d, ax[n], ay[n], az[n], c[n]);
         }
-        // keeps the batch's loads issued before the first blend waits for one
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < NB; ++j) o[j * kRows * ostride] = blend<ND>(c[j], ax[j], ay[j], az[j]);
+        if (j >= 0) {
+          const int k = j & 1;
+          o[j * kRows * ostride] = blend<ND>(c[k], ax[k], ay[k], az[k]);
+        }
       }
     }
     return;
@@ -159,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void interp_fwd_kernel(Shape s,
     for (int a0 = w; a0 < n0; a0 += kRows) {
       const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
       const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
-      const Axis az = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
+      const Axis az = ND == 3 ? axis_of(crd[ND - 1][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
       o[(int64_t)(t0 + a0) * ostride] = sample<ND>(s.in, d, ax, ay, az);
     }
   }
@@ -198,7 +197,7 @@ __global__ __launch_bounds__(kThreads) void interp_bwd_kernel(Shape s,
         const int a0 = w + (j0 + j) * kRows;
         ax[j] = axis_of(crd[0][al][a0], s.in[0]);
         ay[j] = axis_of(crd[1][al][a0], s.in[1]);
-        az[j] = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
+        az[j] = ND == 3 ? axis_of(crd[ND - 1][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
         dd[j][0] = dd[j][1] = dd[j][2] = 0.0f;
       }
       const int64_t o = ((int64_t)(t0 + w + j0 * kRows) * s.omid + im) * s.olast + tl + al;
@@ -242,7 +241,7 @@ __global__ __launch_bounds__(kThreads) void interp_bwd_kernel(Shape s,
     for (int a0 = w; a0 < n0; a0 += kRows) {
       const Axis ax = axis_of(crd[0][al][a0], s.in[0]);
       const Axis ay = axis_of(crd[1][al][a0], s.in[1]);
-      const Axis az = ND == 3 ? axis_of(crd[2][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
+      const Axis az = ND == 3 ? axis_of(crd[ND - 1][al][a0], s.in[2]) : Axis{0, 0, 0.0f};
       const int64_t o = ((int64_t)(t0 + a0) * s.omid + im) * s.olast + tl + al;
       float dd[3] = {0.0f, 0.0f, 0.0f};
       for (int ch = 0; ch < s.C; ++ch) {

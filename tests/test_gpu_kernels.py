@@ -425,6 +425,39 @@ def test_interp_parity(cuda, nd, ins, outs):
     assert (err <= 1e-4 * mag + 1e-12).all(), float((err / (mag + 1e-30)).max())
 
 
+@pytest.mark.parametrize("nd,tess,ins,outs", [(2, [6, 5], (150, 210), (96, 160)),
+                                              (3, [3, 3, 2], (40, 36, 44), (64, 6, 64))])
+def test_interp_smooth_warp(cuda, nd, tess, ins, outs):
+    # Resampling at a CPAB-warped meshgrid, as transform_data does: the tiles
+    # of a smooth warp read compact data regions (in 2D, full tiles stage that
+    # region in LDS; regions that are too large take the direct gathers).  The
+    # grid is scaled past [0, 1] at one end so border tiles clamp.
+    T = cpab_for(tess)
+    B, C = 2, 3
+    rng = np.random.default_rng(60 + nd)
+    theta = seeded_theta(T, B, 0.8, 61 + nd)
+    with torch.no_grad():
+        mesh = T.uniform_meshgrid(list(outs))
+        grid_t = T.transform_grid(mesh, torch.tensor(theta, device=cuda)) * 1.08 - 0.02
+    grid = grid_t.cpu().numpy().astype(np.float32)
+    data = rng.random((B, C, *ins)).astype(np.float32)
+    out = torch.empty((B, C, *outs), device=cuda)
+    native().interp_forward(nd, _dev(data, cuda), _dev(grid, cuda), outs, out)
+    np.testing.assert_array_equal(out.cpu().numpy(), orc.interp_forward(nd, data, grid, outs))
+    gout = rng.standard_normal((B, C, *outs)).astype(np.float32)
+    nP = int(np.prod(outs))
+    gg = torch.empty((B, nd, nP), device=cuda)
+    native().interp_backward(nd, _dev(data, cuda), _dev(grid, cuda), outs, _dev(gout, cuda), gg, None)
+    rg, rd = orc.interp_backward(nd, data, grid, outs, gout)
+    np.testing.assert_array_equal(gg.cpu().numpy(), rg)
+    gd = torch.empty((B, C, *ins), device=cuda)
+    native().interp_backward(nd, _dev(data, cuda), _dev(grid, cuda), outs, _dev(gout, cuda), gg, gd)
+    np.testing.assert_array_equal(gg.cpu().numpy(), rg)
+    mag = scatter_magnitude(data.shape, grid, outs, gout)
+    err = np.abs(gd.cpu().numpy().astype(np.float64) - rd)
+    assert (err <= 1e-4 * mag + 1e-12).all(), float((err / (mag + 1e-30)).max())
+
+
 def test_interp_unaligned_grid(cuda):
     # A grid view that starts 4 bytes into its buffer cannot take the 16-byte
     # vector path; results must not change.
