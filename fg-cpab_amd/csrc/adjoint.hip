@@ -504,8 +504,9 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
         }
       }
       const int c = (t == 0) ? cur : lookup<D>(p, g);
-      // Divergent branch, skipped (exec = 0) when no lane changed cell.
-      if (c != cur) A = fetch<D>(tab, c);
+      // Divergent branch, skipped (exec = 0) when no lane changed cell; marked
+      // unlikely so that the no-change case falls through.
+      if (__builtin_expect(c != cur, 0)) A = fetch<D>(tab, c);
       cur = c;
       if (t & 1) cells[t >> 1] |= (uint32_t)c << 16;
       else cells[t >> 1] = (uint32_t)c;
@@ -542,8 +543,9 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
       if (t > 0) {
         const int cn = cell_at(t - 1);
         // Divergent branch: skipped by the hardware (exec = 0) at steps where
-        // no lane of the wave changes cell.
-        if (cn != c) {
+        // no lane of the wave changes cell; marked unlikely so that this case
+        // falls through.
+        if (__builtin_expect(cn != c, 0)) {
           if (valid) {
             if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, c, m);
             else flush_lds<PP>(bins, c, m);

@@ -137,8 +137,9 @@ __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT],
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
       const int c = cell_2d(px[k], py[k], nx, ny);
-      // Divergent branch, skipped (exec = 0) when no lane changed cell.
-      if (c != cur[k]) M[k] = load_aff2(Tg, c);
+      // Divergent branch, skipped (exec = 0) when no lane changed cell; marked
+      // unlikely so that the no-change case falls through.
+      if (__builtin_expect(c != cur[k], 0)) M[k] = load_aff2(Tg, c);
       cur[k] = c;
       advance(k, c);
     }
@@ -166,8 +167,9 @@ __device__ __forceinline__ void steps_3d(float& px, float& py, float& pz,
   Aff<3> M = load_aff3(Tg, cur);
   for (int t = 0; t < T; ++t) {
     const int c = (t == 0) ? cur : cell_3d(px, py, pz, nx, ny, nz);
-    // Divergent branch, skipped (exec = 0) when no lane changed cell.
-    if (c != cur) M = load_aff3(Tg, c);
+    // Divergent branch, skipped (exec = 0) when no lane changed cell; marked
+    // unlikely so that the no-change case falls through.
+    if (__builtin_expect(c != cur, 0)) M = load_aff3(Tg, c);
     cur = c;
     float sx, sy, sz;
     apply3(M, px, py, pz, sx, sy, sz);

@@ -109,6 +109,18 @@ def _check_trace_and_interp_validation():
     bad = (ctypes.c_int64 * 2)(0, 4)
     rc = lib.cpab_interp_forward(2, 1, 1, bad, sizes, p, p, p, None)
     assert rc == 1
+    # the gathers address one data channel with 32-bit byte offsets: at most 2^30 values
+    big = (ctypes.c_int64 * 3)(1024, 1024, 1025)
+    rc = lib.cpab_interp_forward(3, 1, 1, big, sizes, p, p, p, None)
+    assert rc == 1 and "2^30" in _err(lib)
+    rc = lib.cpab_interp_backward(3, 1, 1, big, sizes, p, p, p, p, None, None)
+    assert rc == 1 and "2^30" in _err(lib)
+    huge = (ctypes.c_int64 * 3)(1 << 30, 1 << 30, 1 << 30)   # products beyond int64 if unchecked
+    rc = lib.cpab_interp_forward(3, 1, 1, sizes, huge, p, p, p, None)
+    assert rc == 1
+    rc = lib.cpab_transform_data_forward(3, 1, 1, big, sizes, 50, 2, 2, 2, 0, p, p, p, p, p, None,
+                                         None)
+    assert rc == 1 and "2^30" in _err(lib)
 
 
 def test_missing_library_raises(tmp_path):
