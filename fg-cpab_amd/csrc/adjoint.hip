@@ -88,14 +88,27 @@ template <int D, typename P> __device__ __forceinline__ Aff<D> fetch(P tab, int 
   return Fetch<D>::at(tab, c);
 }
 
-template <int D> __device__ __forceinline__ Adj<D> fetch_adj(const float* tab, int c);
-template <> __device__ __forceinline__ Adj<1> fetch_adj<1>(const float* tab, int c) { return load_adj1(tab, c); }
-template <> __device__ __forceinline__ Adj<2> fetch_adj<2>(const float* tab, int c) { return load_adj2(tab, c); }
-template <> __device__ __forceinline__ Adj<3> fetch_adj<3>(const float* tab, int c) { return load_adj3(tab, c); }
-template <int D> __device__ __forceinline__ Inv<D> fetch_inv(const float* tab, int c);
-template <> __device__ __forceinline__ Inv<1> fetch_inv<1>(const float* tab, int c) { return load_inv1(tab, c); }
-template <> __device__ __forceinline__ Inv<2> fetch_inv<2>(const float* tab, int c) { return load_inv2(tab, c); }
-template <> __device__ __forceinline__ Inv<3> fetch_inv<3>(const float* tab, int c) { return load_inv3(tab, c); }
+template <int D> struct FetchRev;
+template <> struct FetchRev<1> {
+  template <typename P> static __device__ __forceinline__ Adj<1> adj(P tab, int c) { return load_adj1(tab, c); }
+  template <typename P> static __device__ __forceinline__ Inv<1> inv(P tab, int c) { return load_inv1(tab, c); }
+};
+template <> struct FetchRev<2> {
+  template <typename P> static __device__ __forceinline__ Adj<2> adj(P tab, int c) { return load_adj2(tab, c); }
+  template <typename P> static __device__ __forceinline__ Inv<2> inv(P tab, int c) { return load_inv2(tab, c); }
+};
+template <> struct FetchRev<3> {
+  template <typename P> static __device__ __forceinline__ Adj<3> adj(P tab, int c) { return load_adj3(tab, c); }
+  template <typename P> static __device__ __forceinline__ Inv<3> inv(P tab, int c) { return load_inv3(tab, c); }
+};
+// Reverse-sweep table entries (G, the inverse one-step map) from a global or
+// an LDS table.
+template <int D, typename P> __device__ __forceinline__ Adj<D> fetch_adj(P tab, int c) {
+  return FetchRev<D>::adj(tab, c);
+}
+template <int D, typename P> __device__ __forceinline__ Inv<D> fetch_inv(P tab, int c) {
+  return FetchRev<D>::inv(tab, c);
+}
 
 __device__ __forceinline__ void velocity(const Aff<1>& A, const float (&p)[1], float (&v)[1]) {
   v[0] = fmaf(A.a, p[0], A.b);
@@ -182,7 +195,11 @@ __device__ __forceinline__ float stack_pop(float (&a)[N]) {
   return v;
 }
 
-enum Bins { kBinsFull = 1, kBinsCache = 2 };
+// Where the backward keeps its per-cell sums: full LDS bins, the hashed LDS
+// cell cache, or full bins with the reverse-sweep table (G and the inverse
+// one-step maps) staged in LDS beside them (register variant, 1D/2D).
+enum Bins { kBinsFull = 1, kBinsCache = 2, kBinsFullRev = 3 };
+constexpr bool full_bins(int b) { return b == kBinsFull || b == kBinsFullRev; }
 
 template <int P>
 __device__ __forceinline__ void flush_lds(float* bins, int c, const float (&m)[P]) {
@@ -424,7 +441,7 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
         if (s < len) {
           const int c = sc[s];
           const bool need = valid && c != prev && prev >= 0;
-          if (BINS == kBinsFull) {
+          if (full_bins(BINS)) {
             if (need) flush_lds<PP>(bins, prev, m);
           } else {
             if (need) flush_cache<PP>(keys, bins, mom_b, prev, m);
@@ -442,7 +459,7 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
     bool on;
     wave_run_sums<PP>(valid, prev, m, r, on);
     if (on) {
-      if (BINS == kBinsFull) flush_lds<PP>(bins, prev, r);
+      if (full_bins(BINS)) flush_lds<PP>(bins, prev, r);
       else flush_cache<PP>(keys, bins, mom_b, prev, r);
     }
     io.finish(pi, valid, lam);
@@ -456,8 +473,8 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
 // cell's inverse map (a few ulp per step; the positions only feed the sums
 // S, the cells stay exact).  With adaptive substeps (Heun on crossings) the
 // positions are kept in registers instead.
-template <int D, bool ADAPTIVE, int BINS, int TS, typename P, typename IO>
-__device__ __forceinline__ void register_body(P tab, const float* __restrict__ gtab, int nP,
+template <int D, bool ADAPTIVE, int BINS, int TS, typename P, typename PG, typename IO>
+__device__ __forceinline__ void register_body(P tab, PG gtab, int nP,
                                               const Cells& g, const IO& io, float* bins,
                                               int* keys, float* __restrict__ mom_b) {
   constexpr int PP = Dim<D>::P;
@@ -467,7 +484,7 @@ __device__ __forceinline__ void register_body(P tab, const float* __restrict__ g
   // registers to spare) it is kept pending instead and issued one component
   // every TS / PP steps during the next range's phase 1, alongside its VALU
   // work; the last range's flush follows the loop.
-  constexpr bool kSpread = D <= 2 && !ADAPTIVE && BINS == kBinsFull;
+  constexpr bool kSpread = D <= 2 && !ADAPTIVE && full_bins(BINS);
   const float h = 1.0f / (float)TS;
   const float hh = h * 0.5f;
   float pend[PP];
@@ -582,21 +599,31 @@ struct StageLds {
   float* ldsA;
   int* keys;
   float* bins;
+  float* ldsG;   // kBinsFullRev: the reverse-sweep table after the bins
   __device__ __forceinline__ StageLds(float* lds, int R) {
     ldsA = lds;
     float* after_a = lds + (LDS_A ? R : 0);
     keys = reinterpret_cast<int*>(after_a);
     bins = BINS == kBinsCache ? after_a + kCacheSlots : after_a;
+    ldsG = bins + ((R + 3) & ~3);   // 16-byte aligned
   }
-  // Stage the table, clear the bins / cache (and the touched-cell counter).
-  __device__ __forceinline__ void begin(const float* __restrict__ Ag, int R, int* touched_cnt) const {
+  // Stage the tables, clear the bins / cache (and the touched-cell counter).
+  __device__ __forceinline__ void begin(const float* __restrict__ Ag, const float* __restrict__ Gg,
+                                        int R, int nG, int* touched_cnt) const {
     constexpr int PP = Dim<D>::P;
     if (LDS_A) {
       const float2* s2 = reinterpret_cast<const float2*>(Ag);
       float2* d2 = reinterpret_cast<float2*>(ldsA);
       for (int i = threadIdx.x; i < R / 2; i += blockDim.x) d2[i] = s2[i];
     }
-    if (BINS == kBinsFull) {
+    if (BINS == kBinsFullRev) {
+      // nG floats, a multiple of 4 (RevStride); the table and the LDS copy are
+      // 16-byte aligned.
+      const float4* s4 = reinterpret_cast<const float4*>(Gg);
+      float4* d4 = reinterpret_cast<float4*>(ldsG);
+      for (int i = threadIdx.x; i < nG / 4; i += blockDim.x) d4[i] = s4[i];
+    }
+    if (full_bins(BINS)) {
       for (int i = threadIdx.x; i < R; i += blockDim.x) bins[i] = 0.0f;
       if (threadIdx.x == 0) *touched_cnt = 0;
     } else {
@@ -614,7 +641,7 @@ struct StageLds {
                                       float* __restrict__ mom_b, int nC, int* touched_cnt) const {
     constexpr int PP = Dim<D>::P;
     __syncthreads();
-    if (BINS == kBinsFull) {
+    if (full_bins(BINS)) {
       auto cell_touched = [&](int i) {
         bool t = false;
 #pragma unroll
@@ -685,7 +712,9 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
         return;
       }
     }
-    if (LDS_A) register_body<D, ADAPTIVE, BINS, TS>(as_lds(L.ldsA), Gg, nP, g, io, L.bins, L.keys, mom_b);
+    if constexpr (BINS == kBinsFullRev)
+      register_body<D, ADAPTIVE, BINS, TS>(Ag, as_lds(L.ldsG), nP, g, io, L.bins, L.keys, mom_b);
+    else if (LDS_A) register_body<D, ADAPTIVE, BINS, TS>(as_lds(L.ldsA), Gg, nP, g, io, L.bins, L.keys, mom_b);
     else register_body<D, ADAPTIVE, BINS, TS>(Ag, Gg, nP, g, io, L.bins, L.keys, mom_b);
   } else {
     if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(L.ldsA), Gg, nP, T, g, io, L.bins, L.keys, mom_b);
@@ -720,7 +749,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kerne
     const float* __restrict__ Gs, Recover rec, const float* __restrict__ grad_out,
     float* __restrict__ moments, float* __restrict__ partials, uint64_t* __restrict__ dense_parts,
     float* __restrict__ lam, float* __restrict__ grad_points) {
-  extern __shared__ float lds[];
+  extern __shared__ __align__(16) float lds[];
   __shared__ int touched_cnt;
   const int b = blockIdx.y;
   const int n_batch = gridDim.y;
@@ -738,7 +767,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kerne
     io.gout = k == K - 1 ? grad_out + (size_t)b * plane : lam + (size_t)b * plane;
     io.lam_out = k == 0 ? (grad_points ? grad_points + (size_t)b * plane : nullptr)
                         : lam + (size_t)b * plane;
-    L.begin(Ag, R, &touched_cnt);
+    L.begin(Ag, Gg, R, nC * RevStride<D>::S, &touched_cnt);
     run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, nP, T, g, io, moments + row * R, rec, row);
     // Every lane is done with this stage's tables before they are written out
     // (and, for the next stage, overwritten).
@@ -759,7 +788,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
     const float* __restrict__ grad_out,
     float* __restrict__ moments, float* __restrict__ partials, uint64_t* __restrict__ dense_parts,
     float* __restrict__ grad_data) {
-  extern __shared__ float lds[];
+  extern __shared__ __align__(16) float lds[];
   __shared__ int touched_cnt;
   const int b = blockIdx.y;
   const int R = nC * Dim<D>::P;
@@ -773,7 +802,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
   io.gout = grad_out + (size_t)b * s.C * s.nP;
   io.data = data + (size_t)b * s.C * s.plane_in;
   io.gdata = grad_data ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
-  L.begin(Ag, R, &touched_cnt);
+  L.begin(Ag, Gg, R, nC * RevStride<D>::S, &touched_cnt);
   run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, s.nP, T, g, io, moments + (size_t)b * R, rec,
                                           (size_t)b);
   const size_t part = (size_t)b * gridDim.x + blockIdx.x;
@@ -785,7 +814,8 @@ template <int D, bool LDS_A, int BINS>
 size_t stage_lds_bytes(int nC) {
   const size_t R = (size_t)nC * Dim<D>::P;
   size_t lds = LDS_A ? R * sizeof(float) : 0;
-  if (BINS == kBinsFull) lds += R * sizeof(float);
+  if (full_bins(BINS)) lds += R * sizeof(float);
+  if (BINS == kBinsFullRev) lds += (((R + 3) & ~(size_t)3) - R + (size_t)nC * RevStride<D>::S) * sizeof(float);
   if (BINS == kBinsCache) lds += (size_t)kCacheSlots * (Dim<D>::P + 1) * sizeof(float);
   return lds;
 }
@@ -845,6 +875,10 @@ hipError_t dispatch(const BackwardJob& j, int adaptive, const LaunchCfg& cfg, hi
   if (cfg.reg_steps == kRegSteps && j.T == kRegSteps) {
     if constexpr (D <= 2) {
       if (cfg.lds_bins) {
+        if (cfg.lds_rev) {
+          if (adaptive) CPAB_GO(true, false, kBinsFullRev, kRegSteps);
+          CPAB_GO(false, false, kBinsFullRev, kRegSteps);
+        }
         if (adaptive) CPAB_GO(true, false, kBinsFull, kRegSteps);
         CPAB_GO(false, false, kBinsFull, kRegSteps);
       }

@@ -135,6 +135,9 @@ cpab::LaunchCfg forward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta
   return c;
 }
 
+// Floats per cell of the reverse-sweep table (cpab_device.hpp RevStride).
+int adj_stride(int ndim) { return ndim == 1 ? 4 : (ndim == 2 ? 12 : 24); }
+
 // Backward: full LDS bins when a theta's nC x ppc table fits in LDS, else the
 // hashed LDS cell cache (at most 104 KiB, 3D).  Register variant for T = 50
 // (cells, and with adaptive substeps positions, in VGPRs; one 1024-lane
@@ -157,6 +160,11 @@ bool backward_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta, int T, i
   const bool reg = T == cpab::kRegSteps && g.nC <= 65535 &&
                    (g.ndim <= 2 ? c.lds_bins != 0 : !adaptive);
   c.reg_steps = reg ? cpab::kRegSteps : 0;
+  // Register variant with full bins in 1D/2D: the reverse-sweep table joins the
+  // bins in LDS when both fit, so the entry phase 2 reloads at every cell
+  // change comes from LDS (C2 backward 176 -> 170 us, C1 19.5 -> 18.6 us).
+  const int64_t rev = (int64_t)g.nC * adj_stride(g.ndim) * 4 + 16;
+  c.lds_rev = (reg && g.ndim <= 2 && c.lds_bins && table + rev <= dev.lds) ? 1 : 0;
   const int64_t used = c.lds_bins ? table : cache;
   c.lds_table = (!reg && used + table <= dev.lds) ? 1 : 0;
   const int64_t lds = used + (c.lds_table ? table : 0);
@@ -283,7 +291,6 @@ struct BackwardWorkspace {
   int64_t dense_words, partials_offset, lam_offset, g_offset, amp_offset, total;
 };
 
-int adj_stride(int ndim) { return ndim == 1 ? 4 : (ndim == 2 ? 12 : 24); }
 
 BackwardWorkspace backward_workspace(const cpab::Geometry& g, int64_t nP, int64_t n_batch, int K,
                                      const cpab::LaunchCfg& cfg) {
@@ -376,6 +383,9 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   if (K > 1) CPAB_REQUIRE(stage_points);
   cpab::LaunchCfg cfg;
   if (!backward_cfg(g, nP, n_batch, nstepsolver, adaptive, &cfg)) return CPAB_ERR_DEVICE;
+  // A chain restages each stage's table: measured slower than L2 reads (C5
+  // backward 185 -> 190 us), so chains keep the reverse-sweep table in HBM.
+  if (K > 1) cfg.lds_rev = 0;
   const BackwardWorkspace w = backward_workspace(g, nP, n_batch, K, cfg);
   if (workspace == nullptr || workspace_bytes < w.total)
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",

@@ -456,6 +456,13 @@ __device__ __forceinline__ Adj<2> load_adj2(const float* tab, int c) {
   const v4f v = *entry<v4f, 48>(tab, c);
   return {{v.x, v.y, v.z, v.w}};
 }
+__device__ __forceinline__ Adj<1> load_adj1(lds_ptr<float> tab, int c) {
+  return {tab[__umul24((uint32_t)c, 4u)]};
+}
+__device__ __forceinline__ Adj<2> load_adj2(lds_ptr<float> tab, int c) {
+  const v4f v = ((lds_ptr<v4f>)tab)[__umul24((uint32_t)c, 3u)];
+  return {{v.x, v.y, v.z, v.w}};
+}
 __device__ __forceinline__ Adj<3> load_adj3(const float* tab, int c) {
   const v4f* q = entry<v4f, 96>(tab, c);
   const v4f a = q[0], b = q[1], d = q[2];
@@ -468,6 +475,15 @@ template <int D> struct Inv { float m[D * (D + 1)]; };
 __device__ __forceinline__ Inv<1> load_inv1(const float* tab, int c) {
   const v2f v = *reinterpret_cast<const v2f*>(entry<float, 16>(tab, c) + 1);
   return {{v.x, v.y}};
+}
+__device__ __forceinline__ Inv<1> load_inv1(lds_ptr<float> tab, int c) {
+  lds_ptr<float> e = tab + __umul24((uint32_t)c, 4u);
+  return {{e[1], e[2]}};
+}
+__device__ __forceinline__ Inv<2> load_inv2(lds_ptr<float> tab, int c) {
+  lds_ptr<v4f> q = (lds_ptr<v4f>)tab + __umul24((uint32_t)c, 3u);
+  const v4f a = q[1], b = q[2];
+  return {{a.x, a.y, a.z, b.x, b.y, b.z}};
 }
 __device__ __forceinline__ Inv<2> load_inv2(const float* tab, int c) {
   const v4f* q = entry<v4f, 48>(tab, c);

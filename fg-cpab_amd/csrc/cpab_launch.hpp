@@ -32,6 +32,7 @@ struct LaunchCfg {
   int lds_bins;     // backward: accumulate moments in full LDS bins (per-workgroup partials)
   int lds_cache;    // backward: else accumulate in the hashed LDS cell cache
   int reg_steps;    // backward: compile-time step count of the register variant (0 = segmented)
+  int lds_rev;      // backward, register variant with full bins: the reverse-sweep table in LDS too
 };
 
 hipError_t launch_fill(float* dst, int64_t n, float value, hipStream_t s);
