@@ -282,11 +282,37 @@ __device__ __forceinline__ void flush_cache(int* keys, float* vals, float* __res
   for (int k = 0; k < P; ++k) unsafeAtomicAdd(mom + (size_t)P * c + k, m[k]);
 }
 
+// Logical (part, row) of a backward workgroup: `part` indexes the point
+// ranges of one row (gridDim.x of them), `row` the thetas (gridDim.y).  The
+// hardware hands workgroups to the 8 XCDs round-robin by linear id, and each
+// XCD has its own L2.  The logical grid is listed in blocks of kRowBlock rows
+// (parts in order inside a block, rows fastest) and that list is cut into 8
+// contiguous ranges, one per XCD: an XCD serves a few rows over a contiguous
+// share of their points, so each row's affine and reverse-sweep tables are
+// fetched from HBM by few L2s (at C2: by 2 of the 8 instead of all 8), and so
+// are shared input points (by 4).  The map is a bijection for any grid.
+constexpr int kRowBlock = 4;
+struct WgSlot { int part, row; };
+__device__ __forceinline__ WgSlot wg_slot() {
+  const int nx = gridDim.x, ny = gridDim.y, n = nx * ny;
+  const int lin = blockIdx.y * nx + blockIdx.x;
+  const int x = lin & 7, k = lin >> 3, q = n >> 3, r = n & 7;
+  const int L = x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
+  const int rb = ny < kRowBlock ? ny : kRowBlock;
+  const int full = (ny / rb) * rb * nx;   // entries in whole row blocks
+  if (L < full) {
+    const int blk = L / (rb * nx), rem = L - blk * rb * nx;
+    return {rem / rb, blk * rb + rem % rb};
+  }
+  const int rr = ny - (ny / rb) * rb, rem = L - full;   // the last, partial block
+  return {rem / rr, (ny / rb) * rb + rem % rr};
+}
+
 // Contiguous point range [lo, hi) of this workgroup, a whole number of blocks long.
 __device__ __forceinline__ void wg_range(int nP, int& lo, int& hi) {
   const int64_t per = ((int64_t)nP + gridDim.x - 1) / gridDim.x;
   const int64_t span = (per + blockDim.x - 1) / blockDim.x * blockDim.x;
-  const int64_t l = (int64_t)blockIdx.x * span;
+  const int64_t l = (int64_t)wg_slot().part * span;
   lo = (int)std::min<int64_t>(l, nP);
   hi = (int)std::min<int64_t>(l + span, nP);
 }
@@ -724,8 +750,7 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
 
 // TS == 0: segmented variant; TS > 0: register variant.  Both accumulate in
 // full LDS bins or the LDS cell cache.
-// One workgroup = one theta (blockIdx.y) x one contiguous point range
-// (blockIdx.x).  A chain of K stages (Cpab.transform_grid_chain) runs its
+// One workgroup = one theta x one contiguous point range (wg_slot).  A chain of K stages (Cpab.transform_grid_chain) runs its
 // stages last to first inside the kernel: stage k reads its input points from
 // `points` (k = 0) or stage_points[k-1], its seed from grad_out (k = K-1) or
 // the lam buffer the stage above wrote for the same points, and writes the
@@ -751,7 +776,8 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kerne
     float* __restrict__ lam, float* __restrict__ grad_points) {
   extern __shared__ __align__(16) float lds[];
   __shared__ int touched_cnt;
-  const int b = blockIdx.y;
+  const WgSlot w = wg_slot();
+  const int b = w.row;
   const int n_batch = gridDim.y;
   const int R = nC * Dim<D>::P;
   const size_t plane = (size_t)D * nP;  // one theta's [D, nP] block
@@ -771,8 +797,8 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kerne
     run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, nP, T, g, io, moments + row * R, rec, row);
     // Every lane is done with this stage's tables before they are written out
     // (and, for the next stage, overwritten).
-    const size_t part = row * gridDim.x + blockIdx.x;
-    L.end(partials + part * R, dense_parts + row * ((gridDim.x + 63) / 64), (int)blockIdx.x,
+    const size_t part = row * gridDim.x + w.part;
+    L.end(partials + part * R, dense_parts + row * ((gridDim.x + 63) / 64), w.part,
           moments + row * R, nC, &touched_cnt);
     if (k > 0) __syncthreads();
   }
@@ -790,7 +816,8 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
     float* __restrict__ grad_data) {
   extern __shared__ __align__(16) float lds[];
   __shared__ int touched_cnt;
-  const int b = blockIdx.y;
+  const WgSlot w = wg_slot();
+  const int b = w.row;
   const int R = nC * Dim<D>::P;
   const StageLds<D, LDS_A, BINS> L(lds, R);
   const float* __restrict__ Ag = As + (size_t)b * R;
@@ -805,8 +832,8 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
   L.begin(Ag, Gg, R, nC * RevStride<D>::S, &touched_cnt);
   run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, s.nP, T, g, io, moments + (size_t)b * R, rec,
                                           (size_t)b);
-  const size_t part = (size_t)b * gridDim.x + blockIdx.x;
-  L.end(partials + part * R, dense_parts + (size_t)b * ((gridDim.x + 63) / 64), (int)blockIdx.x,
+  const size_t part = (size_t)b * gridDim.x + w.part;
+  L.end(partials + part * R, dense_parts + (size_t)b * ((gridDim.x + 63) / 64), w.part,
         moments + (size_t)b * R, nC, &touched_cnt);
 }
 

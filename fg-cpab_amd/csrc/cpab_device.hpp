@@ -136,12 +136,17 @@ __device__ __forceinline__ int cell_from_square(int square, float lx, float ly) 
 // lanes outside (0,1)^2.
 __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   const float fx = (float)nx, fy = (float)ny;
-  // One ballot per compare keeps the masks in SGPRs (a ballot of a combined
-  // bool would first be materialised in a VGPR and compared back).
-  const uint64_t edge = __builtin_amdgcn_ballot_w64(!(px > 0.0f)) |
-                        __builtin_amdgcn_ballot_w64(!(px <= kClampHi)) |
-                        __builtin_amdgcn_ballot_w64(!(py > 0.0f)) |
-                        __builtin_amdgcn_ballot_w64(!(py <= kClampHi));
+  // x lies in (0, kClampHi] iff its bit pattern minus one, as an unsigned
+  // integer, lies below kClampHi's: +0 wraps to the top, and negative values,
+  // -0, NaN and infinities lie above (checked over all 2^32 patterns).  One
+  // compare of the larger of the two feeds the branch directly; four float
+  // compares needed three scalar ORs and a scalar compare between the vector
+  // compares and the branch, on the critical path of every step (C5 chain
+  // forward 115 -> 107 us, C2 forward 62 -> 59 us).
+  const uint32_t ux = __builtin_bit_cast(uint32_t, px) - 1u;
+  const uint32_t uy = __builtin_bit_cast(uint32_t, py) - 1u;
+  const uint64_t edge =
+      __builtin_amdgcn_ballot_w64((ux > uy ? ux : uy) >= __builtin_bit_cast(uint32_t, kClampHi));
   int base;
   float lx, ly;
   if (!edge) {

@@ -96,11 +96,14 @@ def test_forward_2d_bitexact(cuda, tess, pts_kind, adaptive):
 
 def _edge_lattice(nx, ny, seed):
     """Points on and just beyond the domain edges: each edge coordinate (0, -0,
-    1, a step outside, the float neighbours of 0 and 1) against cell-edge
+    1, a step outside, the float neighbours of 0 and 1, denormals of both signs,
+    the smallest normal, the lookup's clamp bound 1 - 2^-23) against cell-edge
     coordinates k/n and their float neighbours, plus random ones; both axes."""
     rng = np.random.default_rng(seed)
+    tiny = np.nextafter(np.float32(0), np.float32(1))          # smallest denormal
     edge = np.array([0.0, -0.0, 1.0, -1e-3, 1.0 + 1e-3, np.nextafter(np.float32(1), 0),
-                     np.nextafter(np.float32(0), 1), -0.4, 1.4], np.float32)
+                     tiny, -tiny, np.float32(2.0 ** -126) - tiny, np.float32(2.0 ** -126),
+                     np.float32(1.0 - 1e-7), -0.4, 1.4], np.float32)
 
     def across(n):
         k = np.arange(n + 1, dtype=np.float32) / np.float32(n)
