@@ -750,8 +750,9 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
 
 // TS == 0: segmented variant; TS > 0: register variant.  Both accumulate in
 // full LDS bins or the LDS cell cache.
-// One workgroup = one theta x one contiguous point range (wg_slot).  A chain of K stages (Cpab.transform_grid_chain) runs its
-// stages last to first inside the kernel: stage k reads its input points from
+// One workgroup = one theta x one contiguous point range (wg_slot).  A chain
+// of K stages (Cpab.transform_grid_chain) runs its stages last to first
+// inside the kernel: stage k reads its input points from
 // `points` (k = 0) or stage_points[k-1], its seed from grad_out (k = K-1) or
 // the lam buffer the stage above wrote for the same points, and writes the
 // adjoint of its input to lam (k > 0) or grad_points (k = 0).  The per-cell
