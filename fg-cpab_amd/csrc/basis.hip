@@ -159,58 +159,75 @@ __global__ __launch_bounds__(kTableThreads) void adjoint_table_kernel(
   }
 }
 
-// One thread per (row, cell): S = the HBM sum in `moments` plus
-// partials[row, w, cell] for every part w set in the row's dense-part mask
-// (ascending, a fixed order); then the cell's moments from S and its A
-// (cpab_device.hpp, moments_from_s), in place.
+// Moments of every (row, cell) from the sums of the reverse sweep.  One
+// workgroup covers kFinCells<D> cells of one row (blockIdx.x = row * nblk +
+// block), one thread per (cell, component): S = the HBM sum in `moments` plus
+// partials[row, w, cell] for every part w set in the row's dense-part mask,
+// added in ascending w (a fixed order), the parts' loads issued in batches;
+// then S and the cell's A go through LDS and each thread forms its component
+// of the moments (cpab_device.hpp, moments_from_s), in place.  Consecutive
+// threads read consecutive floats of each partial table.
+template <int D> constexpr int kFinCells = 256 / (D * (D + 1));
+
 template <int D>
-__global__ void finish_moments_kernel(int64_t n_cells, int nC, int nparts, float h,
-                                      const float* __restrict__ partials,
-                                      const uint64_t* __restrict__ dense_parts,
-                                      const float* __restrict__ As, float* __restrict__ moments) {
+__global__ __launch_bounds__(256) void finish_moments_kernel(int64_t rows, int nC, int nblk,
+                                                             int nparts, float h,
+                                                             const float* __restrict__ partials,
+                                                             const uint64_t* __restrict__ dense_parts,
+                                                             const float* __restrict__ As,
+                                                             float* __restrict__ moments) {
   constexpr int P = D * (D + 1);
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= n_cells) return;
-  float s[P];
+  constexpr int W = D + 1;
+  constexpr int CB = kFinCells<D>;
+  __shared__ float s_lds[CB * P], a_lds[CB * P];
+  const int64_t row = blockIdx.x / nblk;
+  const int c0 = (int)(blockIdx.x - row * nblk) * CB;
+  const int t = threadIdx.x;
+  const int cl = t / P, comp = t - cl * P;
+  const bool live = t < CB * P && c0 + cl < nC;
+  const int64_t idx = (row * nC + c0 + cl) * P + comp;   // this thread's float of the row's table
+  if (live) {
+    float s = moments[idx];
+    if (nparts > 0) {
+      const int64_t R = (int64_t)nC * P;
+      const int NW = (nparts + 63) / 64;
+      const float* src = partials + row * nparts * R + (int64_t)(c0 + cl) * P + comp;
+      constexpr int U = 16;
+      for (int q = 0; q < NW; ++q) {
+        uint64_t bits = dense_parts[row * NW + q];
+        while (bits) {
+          float x[U];
+          bool on[U];
 #pragma unroll
-  for (int k = 0; k < P; ++k) s[k] = moments[i * P + k];
-  if (nparts > 0) {
-    const int64_t R = (int64_t)nC * P;
-    const int NW = (nparts + 63) / 64;
-    const int64_t row = i / nC;
-    const float* src = partials + row * nparts * R + (i - row * nC) * P;
-    // parts whose loads are issued together, then added in order (all of a
-    // C2 row's 16 in one batch; 3D rows have no partial tables)
-    constexpr int U = D == 3 ? 4 : 16;
-    for (int q = 0; q < NW; ++q) {
-      uint64_t bits = dense_parts[row * NW + q];
-      while (bits) {
-        int w[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          w[u] = bits ? q * 64 + __builtin_ctzll(bits) : -1;
-          bits &= bits - 1;
-        }
-        float x[U][P];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-          for (int k = 0; k < P; ++k) x[u][k] = w[u] >= 0 ? src[w[u] * R + k] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          if (w[u] >= 0) {
-#pragma unroll
-            for (int k = 0; k < P; ++k) s[k] += x[u][k];
+          for (int u = 0; u < U; ++u) {
+            on[u] = bits != 0;
+            const int w = on[u] ? q * 64 + __builtin_ctzll(bits) : 0;
+            bits &= bits - 1;
+            x[u] = on[u] ? src[w * R] : 0.0f;
           }
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+            if (on[u]) s += x[u];
+        }
       }
     }
+    s_lds[t] = s;
+    a_lds[t] = As[idx];
   }
-  float a[P], m[P];
+  __syncthreads();
+  if (!live) return;
+  const float* s_ = s_lds + cl * P;
+  const float* a_ = a_lds + cl * P;
+  const int k = comp / W, q = comp - k * W;
+  const float hhh = (h * 0.5f) * h;
+  float tt = 0.0f;
+  if (q < D) {
 #pragma unroll
-  for (int k = 0; k < P; ++k) a[k] = As[i * P + k];
-  moments_from_s<D>(a, s, h, (h * 0.5f) * h, m);
+    for (int r = 0; r < W; ++r) tt = fmaf(s_[k * W + r], a_[q * W + r], tt);
+  }
 #pragma unroll
-  for (int k = 0; k < P; ++k) moments[i * P + k] = m[k];
+  for (int j = 0; j < D; ++j) tt = fmaf(a_[j * W + k], s_[j * W + q], tt);
+  moments[idx] = fmaf(h, s_[comp], hhh * tt);
 }
 
 // dst[i] = sum_b src[b, i], b ascending.
@@ -532,19 +549,16 @@ hipError_t launch_adjoint_table(int ndim, int64_t rows, int nC, int T, const flo
 hipError_t launch_finish_moments(int ndim, int64_t rows, int nC, int nparts, int T,
                                  const float* partials, const uint64_t* dense_parts,
                                  const float* As, float* moments, hipStream_t s) {
-  const int64_t n = rows * nC;
-  if (n <= 0) return hipSuccess;
+  if (rows <= 0 || nC <= 0) return hipSuccess;
   const float h = 1.0f / (float)T;
-  const dim3 g(grid_for(n, 256)), b(256);
-  if (ndim == 1)
-    hipLaunchKernelGGL(finish_moments_kernel<1>, g, b, 0, s, n, nC, nparts, h, partials, dense_parts,
-                       As, moments);
-  else if (ndim == 2)
-    hipLaunchKernelGGL(finish_moments_kernel<2>, g, b, 0, s, n, nC, nparts, h, partials, dense_parts,
-                       As, moments);
-  else
-    hipLaunchKernelGGL(finish_moments_kernel<3>, g, b, 0, s, n, nC, nparts, h, partials, dense_parts,
-                       As, moments);
+  auto go = [&](auto kernel, int cb) {
+    const int nblk = (nC + cb - 1) / cb;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)(rows * nblk)), dim3(256), 0, s, rows, nC, nblk,
+                       nparts, h, partials, dense_parts, As, moments);
+  };
+  if (ndim == 1) go(finish_moments_kernel<1>, kFinCells<1>);
+  else if (ndim == 2) go(finish_moments_kernel<2>, kFinCells<2>);
+  else go(finish_moments_kernel<3>, kFinCells<3>);
   return hipGetLastError();
 }
 
