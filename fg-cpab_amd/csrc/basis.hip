@@ -78,24 +78,39 @@ __global__ __launch_bounds__(kProjThreads) void project_kernel(
   float acc = 0.0f;
   for (int r = 0; r < rounds; ++r) {
     const int base = k0 + r * kProjCap;
-    int idx[PER];
-    float v[PER];
+    if (base < k1) {
+      // Every load is issued from an in-range index (entries past the column
+      // end re-read its last entry) and masked afterwards, so a lane's loads
+      // are independent of each other.
+      int idx[PER];
+      float v[PER], mv[PER];
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const int k = base + lane + u * kProjSeg;
-      const bool ok = k < k1;
-      idx[u] = ok ? row_idx[k] : 0;
-      v[u] = ok ? vals[k] : 0.0f;
-    }
+      for (int u = 0; u < PER; ++u) {
+        const int k = min(base + lane + u * kProjSeg, k1 - 1);
+        idx[u] = row_idx[k];
+        v[u] = vals[k];
+      }
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const bool ok = base + lane + u * kProjSeg < k1;
-      stage[seg][lane + u * kProjSeg] = make_float2(v[u], ok ? m[idx[u]] : 0.0f);
+      for (int u = 0; u < PER; ++u) mv[u] = m[idx[u]];
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const bool ok = base + lane + u * kProjSeg < k1;
+        stage[seg][lane + u * kProjSeg] = make_float2(ok ? v[u] : 0.0f, ok ? mv[u] : 0.0f);
+      }
     }
     __syncthreads();
-    if (lane == 0) {
+    if (lane == 0 && base < k1) {
       const int n = min(kProjCap, k1 - base);
-      for (int k = 0; k < n; ++k) acc = fmaf(stage[seg][k].x, stage[seg][k].y, acc);
+      int k = 0;
+      for (; k + 4 <= n; k += 4) {
+        const float2 e0 = stage[seg][k], e1 = stage[seg][k + 1];
+        const float2 e2 = stage[seg][k + 2], e3 = stage[seg][k + 3];
+        acc = fmaf(e0.x, e0.y, acc);
+        acc = fmaf(e1.x, e1.y, acc);
+        acc = fmaf(e2.x, e2.y, acc);
+        acc = fmaf(e3.x, e3.y, acc);
+      }
+      for (; k < n; ++k) acc = fmaf(stage[seg][k].x, stage[seg][k].y, acc);
     }
     __syncthreads();
   }
