@@ -308,6 +308,46 @@ __global__ __launch_bounds__(1024) void image_forward_kernel(
   const float* __restrict__ dat = data + (size_t)b * s.C * s.plane_in;
   float* __restrict__ o = out + (size_t)b * s.C * s.nP;
   float* __restrict__ fin = final_points ? final_points + (size_t)b * ND * s.nP : nullptr;
+  if constexpr (ND == 2 && !ADAPTIVE) {
+    // Two output positions per lane, m and m + stride (the second clamped to
+    // the last position and not written when past it).
+    const int stride = gridDim.x * blockDim.x;
+    for (int m0 = blockIdx.x * blockDim.x + threadIdx.x; m0 < s.nP; m0 += 2 * stride) {
+      int qs[2];
+      float px[2], py[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int m = min(m0 + k * stride, s.nP - 1);
+        int ix[3], q = m;
+        if (s.walk_tiles) {
+          tile_index<2>(s, m, ix);
+          q = image_pos<2>(s, ix);
+        } else {
+          image_index<2>(s, m, ix);
+        }
+        float x[3];
+        grid_point<2>(s, axes, ix, x);
+        qs[k] = q;
+        px[k] = x[0];
+        py[k] = x[1];
+      }
+      steps_2d<false, 2>(px, py, Tg, Ag, T, nx, ny, hh);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        if (m0 + k * stride >= s.nP) continue;
+        const int q = qs[k];
+        if (fin) {
+          fin[q] = px[k];
+          fin[q + (size_t)s.nP] = py[k];
+        }
+        const Axis ax = axis_of(px[k], s.in[0]);
+        const Axis ay = axis_of(py[k], s.in[1]);
+        for (int c = 0; c < s.C; ++c)
+          o[(size_t)c * s.nP + q] = sample<2>(s.in, dat + c * s.plane_in, ax, ay, Axis{0, 0, 0.0f});
+      }
+    }
+    return;
+  }
   for (int m = blockIdx.x * blockDim.x + threadIdx.x; m < s.nP; m += gridDim.x * blockDim.x) {
     int ix[3], q = m;
     if (ND >= 2 && s.walk_tiles) {
@@ -470,7 +510,8 @@ hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_
                                 const float* As, const float* data, float* out,
                                 float* final_points, const LaunchCfg& cfg, hipStream_t s) {
   if (img.nP <= 0 || n_batch <= 0) return hipSuccess;
-  const int64_t need = (img.nP + (int64_t)cfg.block - 1) / cfg.block;
+  const int per_lane = (g.ndim == 2 && !adaptive) ? 2 : 1;
+  const int64_t need = (img.nP + (int64_t)per_lane * cfg.block - 1) / ((int64_t)per_lane * cfg.block);
   const dim3 blocks((unsigned)std::max<int64_t>(1, std::min<int64_t>(cfg.chunks, need)),
                     (unsigned)n_batch);
   const dim3 threads((unsigned)cfg.block);
