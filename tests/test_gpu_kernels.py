@@ -374,6 +374,23 @@ def test_backward_mixed_dense_sparse(cuda, chain):
     assert_adjoint_close(gp.cpu().numpy(), lam)
 
 
+@pytest.mark.parametrize("tess,n_theta", [([20, 20], 1), ([50], 2)])
+def test_backward_dense_parts_many_words(cuda, tess, n_theta):
+    # One or two theta rows over 200,000 uniform points: about 196 (98) point
+    # ranges per row, every workgroup dense, so each row's dense-part mask
+    # spans several 64-bit words and finish_moments_kernel adds that many
+    # partial tables per cell.
+    T = cpab_for(tess)
+    nd = len(tess)
+    theta = seeded_theta(T, n_theta, 0.5, 66)
+    pts = uniform_points(nd, 200000, 67)
+    g = np.random.default_rng(68).standard_normal((n_theta, nd, pts.shape[-1])).astype(np.float32)
+    As, mom, gp = _backward_case(T, theta, pts, g, cuda)
+    ref_m, ref_gp = orc.backward(pts, As, g, tess, 50)
+    assert_adjoint_close(gp, ref_gp)
+    assert_grad_close(mom, ref_m, rtol=2e-5)
+
+
 def test_backward_no_points_grad(cuda):
     T = cpab_for([20, 20])
     theta = seeded_theta(T, 2, 0.5, 3)
