@@ -589,14 +589,17 @@ __device__ __forceinline__ void register_body(P tab, PG gtab, int nP,
         // no lane of the wave changes cell; marked unlikely so that this case
         // falls through.
         if (__builtin_expect(cn != c, 0)) {
+          // The next cell's entry is read before the finished cell's sums are
+          // added: LDS operations retire in order, so a read issued after the
+          // adds would wait for them before the next step can use it.
+          G = fetch_adj<D>(gtab, cn);
+          if (!ADAPTIVE) E = fetch_inv<D>(gtab, cn);
           if (valid) {
             if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, c, m);
             else flush_lds<PP>(bins, c, m);
           }
 #pragma unroll
           for (int k = 0; k < PP; ++k) m[k] = 0.0f;
-          G = fetch_adj<D>(gtab, cn);
-          if (!ADAPTIVE) E = fetch_inv<D>(gtab, cn);
         }
         c = cn;
       }

@@ -135,8 +135,10 @@ __global__ __launch_bounds__(kTableThreads) void adjoint_table_kernel(
     int64_t n_words) {
   constexpr int P = D * (D + 1);
   constexpr int S = RevStride<D>::S;
-  constexpr int GS = D == 1 ? 1 : (D == 2 ? 4 : 12);   // floats of the G part
-  constexpr int IW = D == 1 ? 2 : 4;                   // row stride of the inverse map
+  // Entry layout (cpab_device.hpp, RevStride): G at G0, the inverse map's
+  // rows (D + 1 floats each) from I0.
+  constexpr int G0 = D == 3 ? 12 : 0;
+  constexpr int I0 = D == 3 ? 0 : D * D;
   __shared__ float wave_max[kTableThreads / 64];
   const int64_t lin = blockIdx.x * (int64_t)kTableThreads + threadIdx.x;
   if (lin < n_words) dense_parts[lin] = 0;
@@ -150,13 +152,11 @@ __global__ __launch_bounds__(kTableThreads) void adjoint_table_kernel(
     for (int k = 0; k < S; ++k) e[k] = 0.0f;
 #pragma unroll
     for (int k = 0; k < P; ++k) a[k] = As[i * P + k];
-    adjoint_increment<D>(a, h, (h * 0.5f) * h, e);
+    adjoint_increment<D>(a, h, (h * 0.5f) * h, e + G0);
     inverse_step_map<D>(a, h, inv);
     norm = inverse_map_norm<D>(inv);
 #pragma unroll
-    for (int r = 0; r < D; ++r)
-#pragma unroll
-      for (int j = 0; j <= D; ++j) e[GS + r * IW + j] = inv[r * (D + 1) + j];
+    for (int k = 0; k < P; ++k) e[I0 + k] = inv[k];
 #pragma unroll
     for (int k = 0; k < S; ++k) G[i * S + k] = e[k];
 #pragma unroll

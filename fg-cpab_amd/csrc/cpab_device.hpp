@@ -441,11 +441,15 @@ __device__ __forceinline__ void adjoint3(const Aff<3>& A, float px, float py, fl
 // ---------------------------------------------------------------------------
 
 // Per-cell table of the reverse sweep (16-byte aligned entries of
-// RevStride<D>::S floats): G first, then the inverse of the cell's one-step
-// midpoint map p' = E [p; 1], as rows [M | m] with p = M p' + m.
+// RevStride<D>::S floats): G and the inverse of the cell's one-step midpoint
+// map p' = E [p; 1], as rows [M | m] with p = M p' + m.
 //   1D  [g, M, m, 0]                                              4 floats
-//   2D  [g00 g01 g10 g11] [M00 M01 m0 0] [M10 M11 m1 0]             12 floats
-//   3D  3 rows of G (4th column 0), then 3 rows [M_r0 M_r1 M_r2 m_r] 24 floats
+//   2D  [g00 g01 g10 g11] [M00 M01 m0 M10] [M11 m1 0 0]             12 floats
+//       (the inverse map packed, so that its reads, one of 16 bytes and one
+//       of 8, fill no register that goes unused)
+//   3D  3 rows [M_r0 M_r1 M_r2 m_r], then G (9 floats), then 0 0 0  24 floats
+//       (every float a read fetches is used: a fetched register left unused is
+//       reallocated at once, which makes the wave wait for the load there)
 template <int D> struct RevStride;
 template <> struct RevStride<1> { static constexpr int S = 4; };
 template <> struct RevStride<2> { static constexpr int S = 12; };
@@ -470,8 +474,9 @@ __device__ __forceinline__ Adj<2> load_adj2(lds_ptr<float> tab, int c) {
 }
 __device__ __forceinline__ Adj<3> load_adj3(const float* tab, int c) {
   const v4f* q = entry<v4f, 96>(tab, c);
-  const v4f a = q[0], b = q[1], d = q[2];
-  return {{a.x, a.y, a.z, b.x, b.y, b.z, d.x, d.y, d.z}};
+  const v4f a = q[3], b = q[4];
+  const float g8 = reinterpret_cast<const float*>(q)[20];
+  return {{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, g8}};
 }
 
 // Inverse one-step map of a cell, row-major [D, D+1].
@@ -487,17 +492,19 @@ __device__ __forceinline__ Inv<1> load_inv1(lds_ptr<float> tab, int c) {
 }
 __device__ __forceinline__ Inv<2> load_inv2(lds_ptr<float> tab, int c) {
   lds_ptr<v4f> q = (lds_ptr<v4f>)tab + __umul24((uint32_t)c, 3u);
-  const v4f a = q[1], b = q[2];
-  return {{a.x, a.y, a.z, b.x, b.y, b.z}};
+  const v4f a = q[1];
+  const v2f b = *(lds_ptr<v2f>)(q + 2);
+  return {{a.x, a.y, a.z, a.w, b.x, b.y}};
 }
 __device__ __forceinline__ Inv<2> load_inv2(const float* tab, int c) {
   const v4f* q = entry<v4f, 48>(tab, c);
-  const v4f a = q[1], b = q[2];
-  return {{a.x, a.y, a.z, b.x, b.y, b.z}};
+  const v4f a = q[1];
+  const v2f b = *reinterpret_cast<const v2f*>(q + 2);
+  return {{a.x, a.y, a.z, a.w, b.x, b.y}};
 }
 __device__ __forceinline__ Inv<3> load_inv3(const float* tab, int c) {
   const v4f* q = entry<v4f, 96>(tab, c);
-  const v4f a = q[3], b = q[4], d = q[5];
+  const v4f a = q[0], b = q[1], d = q[2];
   return {{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w}};
 }
 
@@ -565,7 +572,7 @@ __device__ __forceinline__ void adjoint_s3(const Adj<3>& G, float px, float py, 
 template <int D>
 __device__ __forceinline__ void adjoint_increment(const float* a, float h, float hhh, float* g) {
   constexpr int W = D + 1;
-  constexpr int RS = D == 3 ? 4 : D;  // row stride inside the table entry
+  constexpr int RS = D;  // row stride inside the table entry
 #pragma unroll
   for (int i = 0; i < D; ++i) {
 #pragma unroll
