@@ -51,12 +51,12 @@ _SIGNATURES = {
                                      _c_vp]),
     "cpab_transform_data_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int,
                                              _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
-                                             _c_vp, _c_vp, _c_vp]),
+                                             _c_vp, _c_vp, _c_vp, _c_vp]),
     "cpab_transform_data_backward_workspace_size": (_c_i64, [_c_int, _c_i64, _c_vp, _c_int]),
     "cpab_transform_data_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int,
                                               _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
-                                              _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                                              _c_vp, _c_vp, _c_i64, _c_vp]),
+                                              _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
+                                              _c_vp, _c_vp, _c_vp, _c_i64, _c_vp]),
     "cpab_project": (_c_int, [_c_i64, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "cpab_sum_batch": (_c_int, [_c_i64, _c_i64, _c_vp, _c_vp, _c_vp]),
     "cpab_interp_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
@@ -220,12 +220,13 @@ class Native:
             _ptr(workspace), wbytes, _stream(points.device)), "cpab_chain_backward")
 
     def transform_data_forward(self, ndim, data, axes, outsize, T, nc, adaptive, Trels, As, out,
-                               final_points):
+                               final_points, seed_grad=None):
         ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
         _check(self.lib.cpab_transform_data_forward(
             ndim, data.shape[0], data.shape[1], _lengths(data.shape[2:]), _lengths(outsize),
             int(T), ncx, ncy, ncz, int(adaptive), _ptr(axes), _ptr(Trels), _ptr(As), _ptr(data),
-            _ptr(out), _ptr(final_points), _stream(data.device)), "cpab_transform_data_forward")
+            _ptr(out), _ptr(final_points), _ptr(seed_grad), _stream(data.device)),
+            "cpab_transform_data_forward")
 
     def transform_data_backward_workspace_size(self, ndim, n_batch, outsize, nC):
         return int(self.lib.cpab_transform_data_backward_workspace_size(
@@ -233,16 +234,16 @@ class Native:
 
     def transform_data_backward(self, ndim, data, axes, outsize, T, nc, adaptive, final_points,
                                 As, grad_out, moments, grad_data, workspace, tab=None,
-                                grad_theta=None):
+                                grad_theta=None, seed_grad=None):
         """tab (basis_tables) and grad_theta [n_batch, d]: also project the
-        moments onto the basis."""
+        moments onto the basis.  seed_grad: the forward's (one channel)."""
         ncx, ncy, ncz = (list(nc) + [1, 1])[:3]
         wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
         proj = tab is not None and grad_theta is not None
         _check(self.lib.cpab_transform_data_backward(
             ndim, data.shape[0], data.shape[1], _lengths(data.shape[2:]), _lengths(outsize),
-            int(T), ncx, ncy, ncz, int(adaptive), _ptr(axes), _ptr(final_points), _ptr(As),
-            _ptr(data), _ptr(grad_out), tab["d"] if proj else 0,
+            int(T), ncx, ncy, ncz, int(adaptive), _ptr(axes), _ptr(final_points), _ptr(seed_grad),
+            _ptr(As), _ptr(data), _ptr(grad_out), tab["d"] if proj else 0,
             _ptr(tab["col_ptr"]) if proj else None, _ptr(tab["row_idx"]) if proj else None,
             _ptr(tab["vals_t"]) if proj else None, _ptr(moments),
             _ptr(grad_theta) if proj else None, _ptr(grad_data), _ptr(workspace), wbytes,

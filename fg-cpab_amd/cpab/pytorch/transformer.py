@@ -313,24 +313,30 @@ class _CPABImageFunction(torch.autograd.Function):
                             1.0 / T, As, Trels)
         else:
             lib.affine(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"], As)
-        grad_wanted = ctx.needs_input_grad[0] or ctx.needs_input_grad[1]
+        # For the backward: with one channel the sample's spatial gradient at
+        # each final point (the seed then needs no data reads); the final
+        # points themselves when grad_data's scatter or several channels need
+        # them.
+        one = data.shape[1] == 1
+        seed_grad = (torch.empty((n, ndim, nP), device=dev, dtype=torch.float32)
+                     if ctx.needs_input_grad[1] and one else None)
         final = (torch.empty((n, ndim, nP), device=dev, dtype=torch.float32)
-                 if grad_wanted else None)
+                 if ctx.needs_input_grad[0] or (ctx.needs_input_grad[1] and not one) else None)
         out = torch.empty((n, data.shape[1], *outsize), device=dev, dtype=torch.float32)
         lib.transform_data_forward(ndim, data_c, axes_c, outsize, T, nc, adaptive, Trels, As, out,
-                                   final)
+                                   final, seed_grad)
         ctx.outsize = list(outsize)
         ctx.T = T
         ctx.nc = nc
         ctx.adaptive = adaptive
         ctx.params = params
-        ctx.save_for_backward(data_c, axes_c, final, As)
+        ctx.save_for_backward(data_c, axes_c, final, seed_grad, As)
         return out
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, grad):
-        data, axes, final, As = ctx.saved_tensors
+        data, axes, final, seed_grad, As = ctx.saved_tensors
         params = ctx.params
         lib = native()
         dev = As.device
@@ -346,5 +352,5 @@ class _CPABImageFunction(torch.autograd.Function):
             grad_theta = torch.empty((n, tab["d"]), device=dev, dtype=torch.float32)
         lib.transform_data_backward(ndim, data, axes, ctx.outsize, ctx.T, ctx.nc, ctx.adaptive,
                                     final, As, grad, moments, grad_data, ws, tab=tab,
-                                    grad_theta=grad_theta)
+                                    grad_theta=grad_theta, seed_grad=seed_grad)
         return grad_data, grad_theta, None, None, None

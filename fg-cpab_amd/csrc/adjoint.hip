@@ -359,6 +359,8 @@ struct ImageIO {
   ImageShape s;
   const float* __restrict__ axes;   // per-axis coordinates of the uniform grid (shared by all thetas)
   const float* __restrict__ fin;    // [D, nP] integrated points of this theta, image order
+  const float* __restrict__ sgrad;  // [D, nP] the sample's spatial gradient there (one channel, no
+                                    // grad_data), or null
   const float* __restrict__ gout;   // [C, nP] image gradient of this theta
   const float* __restrict__ data;   // [C, plane_in]
   float* __restrict__ gdata;        // [C, plane_in] or null
@@ -381,6 +383,14 @@ struct ImageIO {
       int ix[3];
       walk_index(i, ix);
       q = image_pos<D>(s, ix);
+    }
+    if (sgrad) {
+      // The forward's spatial gradient at the final point: three coalesced
+      // reads and no corner reads behind them.
+      const float g = gout[q];
+#pragma unroll
+      for (int k = 0; k < D; ++k) lam[k] = (g * sgrad[q + (size_t)k * s.nP]) * (float)(s.in[k] - 1);
+      return;
     }
     const Axis ax = axis_of(fin[q], s.in[0]);
     const Axis ay = D >= 2 ? axis_of(fin[q + (size_t)s.nP], s.in[1]) : Axis{0, 0, 0.0f};
@@ -813,7 +823,8 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kerne
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward_kernel(
     ImageShape s, int T, Cells g, int nC, const float* __restrict__ axes,
-    const float* __restrict__ final_points, const float* __restrict__ As,
+    const float* __restrict__ final_points, const float* __restrict__ seed_grad,
+    const float* __restrict__ As,
     const float* __restrict__ Gs, Recover rec, const float* __restrict__ data,
     const float* __restrict__ grad_out,
     float* __restrict__ moments, float* __restrict__ partials, uint64_t* __restrict__ dense_parts,
@@ -829,7 +840,8 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
   ImageIO<D> io;
   io.s = s;
   io.axes = axes;
-  io.fin = final_points + (size_t)b * D * s.nP;
+  io.fin = final_points ? final_points + (size_t)b * D * s.nP : nullptr;
+  io.sgrad = seed_grad ? seed_grad + (size_t)b * D * s.nP : nullptr;
   io.gout = grad_out + (size_t)b * s.C * s.nP;
   io.data = data + (size_t)b * s.C * s.plane_in;
   io.gdata = grad_data ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
@@ -868,7 +880,7 @@ struct BackwardJob {
   float *moments, *partials, *lam, *grad_points;
   uint64_t* dense_parts;
   const ImageShape* image;
-  const float *axes, *final_points, *data;
+  const float *axes, *final_points, *seed_grad, *data;
   float* grad_data;
 };
 
@@ -884,8 +896,8 @@ hipError_t go(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
     hipError_t e = allow_lds(kernel, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, grid, block, lds, s, *j.image, j.T, g, j.geo.nC, j.axes,
-                       j.final_points, j.As, j.G, rec, j.data, j.grad_out, j.moments, j.partials,
-                       j.dense_parts, j.grad_data);
+                       j.final_points, j.seed_grad, j.As, j.G, rec, j.data, j.grad_out, j.moments,
+                       j.partials, j.dense_parts, j.grad_data);
   } else {
     auto kernel = backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
     hipError_t e = allow_lds(kernel, lds);
@@ -974,6 +986,7 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
 
 hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
                                  int adaptive, const float* axes, const float* final_points,
+                                 const float* seed_grad,
                                  const float* As, const float* G, const float* amp, const float* data,
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
@@ -994,6 +1007,7 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
   j.image = &img;
   j.axes = axes;
   j.final_points = final_points;
+  j.seed_grad = seed_grad;
   j.data = data;
   j.grad_data = grad_data;
   return dispatch_any(j, adaptive, cfg, s);

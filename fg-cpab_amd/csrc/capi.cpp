@@ -490,7 +490,7 @@ const char* cpab_last_error_string(void) { return g_last_error.c_str(); }
 // (cpab_backward_project; projection arguments of the chain and
 // transform_data backwards).  200: the fused transform_data entry points take
 // the uniform grid's per-axis coordinates instead of the meshgrid.
-int cpab_abi_version(void) { return 300; }
+int cpab_abi_version(void) { return 400; }
 
 int cpab_affine(int ndim, int64_t n_theta, int nC, int d, const float* theta,
                 const int32_t* row_ptr, const int32_t* col_idx, const float* vals, float* As,
@@ -657,7 +657,7 @@ int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
                                 const int64_t* in_size, const int64_t* out_size, int nstepsolver,
                                 int ncx, int ncy, int ncz, int adaptive, const float* axes,
                                 const float* Trels, const float* As, const float* data,
-                                float* out, float* final_points, void* stream) {
+                                float* out, float* final_points, float* seed_grad, void* stream) {
   cpab::Geometry g{};
   int rc = check_geometry(ndim, ncx, ncy, ncz, &g);
   if (rc) return rc;
@@ -669,12 +669,14 @@ int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
   CPAB_REQUIRE(axes); CPAB_REQUIRE(As); CPAB_REQUIRE(data); CPAB_REQUIRE(out);
   if (ndim > 1) CPAB_REQUIRE(Trels);
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(Trels, 16);
+  if (seed_grad && n_channels != 1)
+    return fail(CPAB_ERR_INVALID, "seed_grad needs n_channels == 1, got %lld", (long long)n_channels);
   hipStream_t s = as_stream(stream);
   const cpab::LaunchCfg cfg = forward_cfg(g, img.nP, n_batch);
   hipEvent_t ev = nullptr;
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_image_forward(g, img, n_batch, nstepsolver, adaptive, axes, Trels,
-                                            As, data, out, final_points, cfg, s),
+                                            As, data, out, final_points, seed_grad, cfg, s),
                  "cpab_transform_data_forward");
   prof_end(timed, ev, "image_forward", s);
   return rc;
@@ -691,7 +693,8 @@ int64_t cpab_transform_data_backward_workspace_size(int ndim, int64_t n_batch,
 int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
                                  const int64_t* in_size, const int64_t* out_size, int nstepsolver,
                                  int ncx, int ncy, int ncz, int adaptive, const float* axes,
-                                 const float* final_points, const float* As, const float* data,
+                                 const float* final_points, const float* seed_grad,
+                                 const float* As, const float* data,
                                  const float* grad_out, int d, const int32_t* col_ptr,
                                  const int32_t* row_idx, const float* vals, float* moments,
                                  float* grad_theta, float* grad_data, void* workspace,
@@ -711,7 +714,13 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   pr.grad_theta = grad_theta;
   if ((rc = check_projection(pr))) return rc;
   if (n_batch == 0) return CPAB_OK;
-  CPAB_REQUIRE(axes); CPAB_REQUIRE(final_points); CPAB_REQUIRE(As); CPAB_REQUIRE(data);
+  CPAB_REQUIRE(axes); CPAB_REQUIRE(As); CPAB_REQUIRE(data);
+  // The seed comes from seed_grad (one channel) when given; grad_data's
+  // scatter and the general seed need the final points.
+  if (seed_grad && n_channels != 1)
+    return fail(CPAB_ERR_INVALID, "seed_grad needs n_channels == 1, got %lld", (long long)n_channels);
+  if (!seed_grad || grad_data) CPAB_REQUIRE(final_points);
+  if (grad_data) seed_grad = nullptr;
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(workspace, 16);
   CPAB_REQUIRE(grad_out); CPAB_REQUIRE(moments);
   hipStream_t s = as_stream(stream);
@@ -738,8 +747,8 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   hipEvent_t ev = nullptr;
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, axes,
-                                             final_points, As, G, amp, data, grad_out, moments,
-                                             partials, dense, grad_data, cfg, s),
+                                             final_points, seed_grad, As, G, amp, data, grad_out,
+                                             moments, partials, dense, grad_data, cfg, s),
                  "cpab_transform_data_backward");
   prof_end(timed, ev, "image_backward", s);
   if (rc) return rc;

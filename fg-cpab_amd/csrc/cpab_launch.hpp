@@ -96,9 +96,11 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
 hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
                                 int adaptive, const float* axes, const float* Trels,
                                 const float* As, const float* data, float* out,
-                                float* final_points, const LaunchCfg& cfg, hipStream_t s);
+                                float* final_points, float* seed_grad, const LaunchCfg& cfg,
+                                hipStream_t s);
 hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
                                  int adaptive, const float* axes, const float* final_points,
+                                 const float* seed_grad,
                                  const float* As, const float* G, const float* amp, const float* data,
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,

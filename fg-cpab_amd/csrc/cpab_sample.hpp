@@ -172,6 +172,47 @@ __device__ __forceinline__ float sample(const int* in, const float* __restrict__
   return blend<ND>(c, ax, ay, az);
 }
 
+// The sample at (ax, ay, az) (blend's value, bit for bit) and its spatial
+// gradient d out / d (x, y, z) before the (size-1) chain factor: blend_grad's
+// terms without the upstream gradient, which the fused transform_data forward
+// stores so that its backward seeds a pixel's adjoint from two or three
+// coalesced reads instead of the corner reads.  In 1D/3D g times these equals
+// blend_grad's result bit for bit; in 2D the x term is g (uy dx0 + ty dx1)
+// where blend_grad rounds (g uy) dx0 + (g ty) dx1.
+template <int ND>
+__device__ __forceinline__ float sample_spatial_grad(const int* in, const float* __restrict__ d,
+                                                     const Axis& ax, const Axis& ay,
+                                                     const Axis& az, float* grad) {
+  float c[1 << ND];
+  gather<ND>(in, ChannelPtr{d}, ax, ay, az, c);
+  if (ND == 1) {
+    grad[0] = c[1] - c[0];
+    return lerp_ref(c[0], c[1], ax.t);
+  }
+  const float uy = 1.0f - ay.t;
+  if (ND == 2) {
+    const float c0 = lerp_ref(c[0], c[2], ax.t), c1 = lerp_ref(c[1], c[3], ax.t);
+    grad[0] = uy * (c[2] - c[0]) + ay.t * (c[3] - c[1]);
+    grad[1] = c1 - c0;
+    return lerp_ref(c0, c1, ay.t);
+  }
+  const float uz = 1.0f - az.t;
+  const float wyz[2][2] = {{uy * uz, uy * az.t}, {ay.t * uz, ay.t * az.t}};
+  float gx = 0.0f;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) gx += wyz[b][e] * (c[4 | (b << 1) | e] - c[(b << 1) | e]);
+  const float c00 = lerp_ref(c[0], c[4], ax.t);
+  const float c01 = lerp_ref(c[1], c[5], ax.t);
+  const float c10 = lerp_ref(c[2], c[6], ax.t);
+  const float c11 = lerp_ref(c[3], c[7], ax.t);
+  grad[0] = gx;
+  grad[1] = uz * (c10 - c00) + az.t * (c11 - c01);
+  grad[2] = lerp_ref(c01, c11, ay.t) - lerp_ref(c00, c10, ay.t);
+  return lerp_ref(lerp_ref(c00, c10, ay.t), lerp_ref(c01, c11, ay.t), az.t);
+}
+
 // d out / d (x, y, z) for one channel with upstream gradient g (before the
 // (size-1) chain factor) from the corners of gather(), added into dxyz.
 template <int ND>

@@ -298,7 +298,8 @@ template <int ND, bool ADAPTIVE>
 __global__ __launch_bounds__(1024) void image_forward_kernel(
     ImageShape s, int T, int nx, int ny, int nz, const float* __restrict__ axes,
     const float* __restrict__ Trels, const float* __restrict__ As,
-    const float* __restrict__ data, float* __restrict__ out, float* __restrict__ final_points) {
+    const float* __restrict__ data, float* __restrict__ out, float* __restrict__ final_points,
+    float* __restrict__ seed_grad) {
   const int b = blockIdx.y;
   constexpr int P = ND * (ND + 1);
   const int nC = ND == 1 ? nx : (ND == 2 ? 4 * nx * ny : 5 * nx * ny * nz);
@@ -308,6 +309,19 @@ __global__ __launch_bounds__(1024) void image_forward_kernel(
   const float* __restrict__ dat = data + (size_t)b * s.C * s.plane_in;
   float* __restrict__ o = out + (size_t)b * s.C * s.nP;
   float* __restrict__ fin = final_points ? final_points + (size_t)b * ND * s.nP : nullptr;
+  // One channel: the sample's spatial gradient too, for the backward's seed.
+  float* __restrict__ sg = seed_grad ? seed_grad + (size_t)b * ND * s.nP : nullptr;
+  auto emit = [&](int q, const Axis& ax, const Axis& ay, const Axis& az) {
+    if (sg) {
+      float gr[3];
+      o[q] = sample_spatial_grad<ND>(s.in, dat, ax, ay, az, gr);
+#pragma unroll
+      for (int k = 0; k < ND; ++k) sg[q + (size_t)k * s.nP] = gr[k];
+      return;
+    }
+    for (int c = 0; c < s.C; ++c)
+      o[(size_t)c * s.nP + q] = sample<ND>(s.in, dat + c * s.plane_in, ax, ay, az);
+  };
   if constexpr (ND == 2 && !ADAPTIVE) {
     // Two output positions per lane, m and m + stride (the second clamped to
     // the last position and not written when past it).
@@ -340,10 +354,7 @@ __global__ __launch_bounds__(1024) void image_forward_kernel(
           fin[q] = px[k];
           fin[q + (size_t)s.nP] = py[k];
         }
-        const Axis ax = axis_of(px[k], s.in[0]);
-        const Axis ay = axis_of(py[k], s.in[1]);
-        for (int c = 0; c < s.C; ++c)
-          o[(size_t)c * s.nP + q] = sample<2>(s.in, dat + c * s.plane_in, ax, ay, Axis{0, 0, 0.0f});
+        emit(q, axis_of(px[k], s.in[0]), axis_of(py[k], s.in[1]), Axis{0, 0, 0.0f});
       }
     }
     return;
@@ -375,8 +386,7 @@ __global__ __launch_bounds__(1024) void image_forward_kernel(
     const Axis ax = axis_of(x[0], s.in[0]);
     const Axis ay = ND >= 2 ? axis_of(x[1], s.in[1]) : Axis{0, 0, 0.0f};
     const Axis az = ND == 3 ? axis_of(x[2], s.in[2]) : Axis{0, 0, 0.0f};
-    for (int c = 0; c < s.C; ++c)
-      o[(size_t)c * s.nP + q] = sample<ND>(s.in, dat + c * s.plane_in, ax, ay, az);
+    emit(q, ax, ay, az);
   }
 }
 
@@ -508,7 +518,8 @@ hipError_t launch_forward(const Geometry& g, int64_t nP, int64_t n_batch, int ba
 hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
                                 int adaptive, const float* axes, const float* Trels,
                                 const float* As, const float* data, float* out,
-                                float* final_points, const LaunchCfg& cfg, hipStream_t s) {
+                                float* final_points, float* seed_grad, const LaunchCfg& cfg,
+                                hipStream_t s) {
   if (img.nP <= 0 || n_batch <= 0) return hipSuccess;
   const int per_lane = (g.ndim == 2 && !adaptive) ? 2 : 1;
   const int64_t need = (img.nP + (int64_t)per_lane * cfg.block - 1) / ((int64_t)per_lane * cfg.block);
@@ -517,7 +528,7 @@ hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_
   const dim3 threads((unsigned)cfg.block);
   auto go = [&](auto kernel) -> hipError_t {
     hipLaunchKernelGGL(kernel, blocks, threads, 0, s, img, T, g.nx, g.ny, g.nz, axes, Trels, As,
-                       data, out, final_points);
+                       data, out, final_points, seed_grad);
     return hipGetLastError();
   };
   switch (g.ndim * 2 + (adaptive ? 1 : 0)) {

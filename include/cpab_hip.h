@@ -45,7 +45,8 @@ extern "C" {
 /* Message for the calling thread's last failed call ("" if none). */
 const char* cpab_last_error_string(void);
 
-/* ABI version (major*100 + minor). */
+/* ABI version (major*100 + minor).  400: the transform_data entry points take
+ * seed_grad. */
 int cpab_abi_version(void);
 
 /* A = B theta per theta: As[b, r] = sum_k vals[k] * theta[b, col_idx[k]] over
@@ -206,13 +207,17 @@ int cpab_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, voi
  * data there with cpab_interp_forward's, so out equals the unfused pair bit
  * for bit.  final_points (may be NULL): the integrated points
  * [n_batch, ndim, prod(out_size)] in IMAGE order (last output axis fastest),
- * which cpab_transform_data_backward takes.  No counterpart entry point in
- * the reference, whose transform_data is three separate steps. */
+ * which cpab_transform_data_backward takes.  seed_grad (may be NULL; only
+ * with n_channels == 1): the sample's spatial gradient d out / d x_k at each
+ * integrated point, before the (in_size[k] - 1) chain factor, same layout,
+ * from which the backward seeds each pixel's adjoint without re-reading data.
+ * No counterpart entry point in the reference, whose transform_data is three
+ * separate steps. */
 int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
                                 const int64_t* in_size, const int64_t* out_size, int nstepsolver,
                                 int ncx, int ncy, int ncz, int adaptive, const float* axes,
                                 const float* Trels, const float* As, const float* data,
-                                float* out, float* final_points, void* stream);
+                                float* out, float* final_points, float* seed_grad, void* stream);
 
 /* Bytes of device workspace cpab_transform_data_backward needs. */
 int64_t cpab_transform_data_backward_workspace_size(int ndim, int64_t n_batch,
@@ -227,11 +232,16 @@ int64_t cpab_transform_data_backward_workspace_size(int ndim, int64_t n_batch,
  * (overwritten); grad_theta (may be NULL) [n_batch, d] through B's CSC tables
  * as in cpab_chain_backward; grad_data [n_batch, C, *in_size] (may be NULL;
  * overwritten).  grad_out is the image gradient [n_batch, C, *out_size]; axes
- * as for the forward. */
+ * as for the forward.  The seed comes from seed_grad when it is given (as the
+ * forward wrote it; n_channels == 1), else from final_points and data;
+ * final_points is required unless seed_grad is given and grad_data is NULL.
+ * With seed_grad the seed's x term (2D) rounds differently from the
+ * resampling backward's, within the backward's tolerance. */
 int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
                                  const int64_t* in_size, const int64_t* out_size, int nstepsolver,
                                  int ncx, int ncy, int ncz, int adaptive, const float* axes,
-                                 const float* final_points, const float* As, const float* data,
+                                 const float* final_points, const float* seed_grad,
+                                 const float* As, const float* data,
                                  const float* grad_out, int d, const int32_t* col_ptr,
                                  const int32_t* row_idx, const float* vals, float* moments,
                                  float* grad_theta, float* grad_data, void* workspace,

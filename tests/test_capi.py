@@ -119,8 +119,30 @@ def _check_trace_and_interp_validation():
     rc = lib.cpab_interp_forward(3, 1, 1, sizes, huge, p, p, p, None)
     assert rc == 1
     rc = lib.cpab_transform_data_forward(3, 1, 1, big, sizes, 50, 2, 2, 2, 0, p, p, p, p, p, None,
-                                         None)
+                                         None, None)
     assert rc == 1 and "2^30" in _err(lib)
+
+
+def test_transform_data_seed_grad_checks():
+    # seed_grad only with one channel; the backward needs final_points unless
+    # seed_grad is given and grad_data is not.  Validation fails before any
+    # launch (the pointers are never dereferenced).
+    lib = _native.load_library()
+    p = ctypes.c_void_p(64)
+    ins = (ctypes.c_int64 * 2)(8, 8)
+    outs = (ctypes.c_int64 * 2)(8, 8)
+    rc = lib.cpab_transform_data_forward(2, 1, 2, ins, outs, 50, 2, 2, 1, 0, p, p, p, p, p, None,
+                                         p, None)
+    assert rc == 1 and "seed_grad" in _err(lib)
+    rc = lib.cpab_transform_data_backward(2, 1, 2, ins, outs, 50, 2, 2, 1, 0, p, None, p, p, p, p,
+                                          0, None, None, None, p, None, None, p, 1 << 30, None)
+    assert rc == 1 and "seed_grad" in _err(lib)
+    rc = lib.cpab_transform_data_backward(2, 1, 1, ins, outs, 50, 2, 2, 1, 0, p, None, None, p, p,
+                                          p, 0, None, None, None, p, None, None, p, 1 << 30, None)
+    assert rc == 1 and "final_points" in _err(lib)
+    rc = lib.cpab_transform_data_backward(2, 1, 1, ins, outs, 50, 2, 2, 1, 0, p, None, p, p, p, p,
+                                          0, None, None, None, p, None, p, p, 1 << 30, None)
+    assert rc == 1 and "final_points" in _err(lib)
 
 
 def test_missing_library_raises(tmp_path):

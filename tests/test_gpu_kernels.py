@@ -640,6 +640,62 @@ def test_transform_data_fused_parity(cuda, tess, ins, outs, adaptive, scale):
     assert (err <= 1e-4 * mag + 1e-12).all(), float((err / (mag + 1e-30)).max())
 
 
+@pytest.mark.parametrize("tess,ins,outs,scale", [([10], (50,), (70,), 0.5),
+                                                 ([6, 5], (40, 48), (36, 48), 0.5),
+                                                 ([6, 5], (37, 23), (29, 31), 0.5),
+                                                 ([3, 3, 3], (10, 12, 9), (6, 8, 32), 0.5),
+                                                 ([6, 5], (40, 48), (36, 48), 5.0)])
+def test_transform_data_seed_grad(cuda, tess, ins, outs, scale):
+    # One channel: the forward also writes the sample's spatial gradient at each
+    # final point, and the backward seeds from it (no final points, no data
+    # reads).  The image is bit-exact; the stored gradient times (size - 1) is
+    # the resampling backward's grad_grid at unit image gradient, bit for bit
+    # (blend_grad with g = 1 multiplies by 1); the moments match the oracle and
+    # the final-point path within the backward's tolerance.
+    T = cpab_for(tess)
+    p = T.params
+    nd = len(tess)
+    B = 2
+    theta = seeded_theta(T, B, scale, 95)
+    rng = np.random.default_rng(96)
+    data = rng.random((B, 1, *ins)).astype(np.float32)
+    grid_np = T.uniform_meshgrid(list(outs)).cpu().numpy()
+    axes = T._uniform_axes(list(outs))
+    As = _As_gpu(T, theta, cuda)
+    Tr = torch.empty_like(As)
+    native().expm(nd, As, 1.0 / 50, Tr)
+    nP = int(np.prod(outs))
+    out = torch.empty((B, 1, *outs), device=cuda)
+    fin = torch.empty((B, nd, nP), device=cuda)
+    sg = torch.empty((B, nd, nP), device=cuda)
+    native().transform_data_forward(nd, _dev(data, cuda), axes, list(outs), 50, p.nc, 0, Tr, As,
+                                    out, fin, seed_grad=sg)
+    A = As.cpu().numpy()
+    if nd == 1:
+        xT = orc.forward_closed_1d(grid_np, A, p.nc)
+    else:
+        xT = orc.forward_trels(grid_np, Tr.cpu().numpy(), A, p.nc, 50)
+    np.testing.assert_array_equal(fin.cpu().numpy(), _image_order(xT, outs))
+    np.testing.assert_array_equal(out.cpu().numpy(), orc.interp_forward(nd, data, xT, outs))
+    unit, _ = orc.interp_backward(nd, data, xT, outs, np.ones((B, 1, *outs), np.float32))
+    scale_k = np.array([s_ - 1 for s_ in ins], np.float32).reshape(1, nd, 1)
+    np.testing.assert_array_equal(sg.cpu().numpy() * scale_k, _image_order(unit, outs))
+
+    gout = rng.standard_normal((B, 1, *outs)).astype(np.float32)
+    nbytes = native().transform_data_backward_workspace_size(nd, B, list(outs), p.nC)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=cuda) if nbytes else None
+    mom = torch.empty((B, p.nC, nd * (nd + 1)), device=cuda)
+    native().transform_data_backward(nd, _dev(data, cuda), axes, list(outs), 50, p.nc, 0, None,
+                                     As, _dev(gout, cuda), mom, None, ws, seed_grad=sg)
+    rg, _ = orc.interp_backward(nd, data, xT, outs, gout)
+    ref_m, _ = orc.backward(grid_np, A, rg, p.nc, 50)
+    assert_grad_close(mom.cpu().numpy(), ref_m, rtol=2e-5)
+    mom_fin = torch.empty_like(mom)
+    native().transform_data_backward(nd, _dev(data, cuda), axes, list(outs), 50, p.nc, 0, fin,
+                                     As, _dev(gout, cuda), mom_fin, None, ws)
+    assert_grad_close(mom.cpu().numpy(), mom_fin.cpu().numpy(), rtol=2e-5)
+
+
 @pytest.mark.parametrize("case", ["dense", "sparse", "cache3d", "chain", "image"])
 def test_fused_projection_matches_project(cuda, case):
     # The backward launch forms each row's moments and projects them onto the
