@@ -71,57 +71,17 @@ __device__ __forceinline__ int cell_1d(float px, int nx) {
   return (int)__builtin_floorf(clamp_lookup(px) * (float)nx);
 }
 
-// Triangle within a square from the local coordinates (lx, ly) in [0,1):
-//   bit1 = lx < ly (above the main diagonal), bit0 = (1 - lx) < ly (above the
-//   anti-diagonal); raw 0,1,2,3 -> triangle 0,1,3,2 (cpab_ops_2d.cu:119-127).
-__device__ __forceinline__ int tri_2d(float lx, float ly) {
-  const int t1 = ((1.0f - lx) < ly) ? 1 : 0;
-  const int t3 = (lx < ly) ? 3 : 0;
-  return t3 ^ t1;
-}
-
-// Out-of-domain rules (cpab_ops_2d.cu:97-117): the boundary triangle of the
-// nearest square; beyond a corner the diagonal through the corner decides.
-// Falls through to the inside rule exactly as the reference does (NaN input).
-// Written as selects: a wave with points on the domain boundary (every row of
-// a meshgrid has two) takes this path at every step, and the nested branches
-// of the rule tree cost far more than evaluating all of it.  The products are
-// the reference's, term for term.
-__device__ __forceinline__ int cell_2d_outside(float px, float py, float fx, float fy,
-                                                         int base, float lx, float ly) {
-  const bool xl = px <= 0.0f, xh = px >= 1.0f, yl = py <= 0.0f, yh = py >= 1.0f;
-  const float pyfy = py * fy, pxfx = px * fx;
-  const float nyfy = (-py) * fy, nxfx = (-px) * fx;
-  const float yhi = fmaf(py, fy, -fy), xhi = fmaf(px, fx, -fx);
-  // px <= 0: below-left corner -> 0, above-left corner -> 2, else 3
-  const int tl = (yl & (pyfy < pxfx)) ? 0 : ((yh & (yhi > nxfx)) ? 2 : 3);
-  // px >= 1: below-right corner -> 0, above-right corner -> 2, else 1
-  const int th = (yl & (nyfy > xhi)) ? 0 : ((yh & (yhi > xhi)) ? 2 : 1);
-  // 0 < px < 1 (or NaN): bottom -> 0, top -> 2, else the inside rule
-  const int tm = yl ? 0 : (yh ? 2 : tri_2d(lx, ly));
-  return base + (xl ? tl : (xh ? th : tm));
-}
-
-// Inside rule from the clamped coordinates: square base id (4 * square) in
-// `base`, local coordinates in (lx, ly), and the triangle within the square.
-__device__ __forceinline__ int tri_2d_inside(float xc, float yc, float fx, float fy, int& base,
-                                             float& lx, float& ly) {
-  const float sx = __builtin_floorf(xc * fx), sy = __builtin_floorf(yc * fy);
-  lx = fmaf(xc, fx, -sx);
-  ly = fmaf(yc, fy, -sy);
-  base = (int)fmaf(sy, fx, sx) << 2;  // exact: cx + cy*nx < 2^22
-  return tri_2d(lx, ly);
-}
-
-// 4 * square + tri_2d(lx, ly) in two adds with a carry-in.  With
-// b3 = lx < ly and b1 = (1 - lx) < ly, tri_2d = 3*b3 ^ b1 = 2*b3 + (b3 ^ b1),
-// so the cell is 2 * (2 * square + b3) + (b3 ^ b1).  Each "x + x + bit" is one
-// v_addc_co_u32 whose carry-in is the bit's lane mask (the compare's own
-// result; the xor of two masks is a scalar op), where the select form takes a
-// shift, two selects and an or.
-__device__ __forceinline__ int cell_from_square(int square, float lx, float ly) {
-  const uint64_t m3 = __builtin_amdgcn_ballot_w64(lx < ly);
-  const uint64_t m0 = m3 ^ __builtin_amdgcn_ballot_w64((1.0f - lx) < ly);
+// 4 * square + triangle in two adds with a carry-in.  The triangle within a
+// square comes from its local coordinates (lx, ly): b3 = lx < ly (above the
+// main diagonal), b1 = (1 - lx) < ly (above the anti-diagonal), and raw
+// 0,1,2,3 -> triangle 0,1,3,2 (cpab_ops_2d.cu:119-127), i.e. tri = 3*b3 ^ b1
+// = 2*b3 + (b3 ^ b1).  So the cell is 2 * (2 * square + b3) + (b3 ^ b1): each
+// "x + x + bit" is one v_addc_co_u32 whose carry-in is the bit's lane mask
+// (a compare's own result; the xor of two masks is a scalar op), where the
+// select form takes a shift, two selects and an or.  The masks come in as
+// arguments so that the out-of-domain rules can replace lanes' bits first.
+__device__ __forceinline__ int cell_from_bits(int square, uint64_t m3, uint64_t m1) {
+  const uint64_t m0 = m3 ^ m1;
   int u, c;
   uint64_t co;
   asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(u), "=s"(co) : "v"(square), "s"(m3));
@@ -129,11 +89,27 @@ __device__ __forceinline__ int cell_from_square(int square, float lx, float ly) 
   return c;
 }
 
-// Square (cx, cy) holds triangles 4*(cx + cy*nx) + {0 top, 1 right, 2 bottom, 3 left}.
+// Square (cx, cy) holds triangles 4*(cx + cy*nx) + {0 bottom, 1 right, 2 top, 3 left}.
+//
 // A wave whose lanes all lie in (0, kClampHi]^2, where the lookup clamp is the
-// identity, takes the inside rule on the raw coordinates (cell_from_square).
-// Otherwise a wave-uniform branch clamps, and applies the boundary rules to
-// lanes outside (0,1)^2.
+// identity, takes the inside rule on the raw coordinates.  Otherwise (a
+// wave-uniform branch) the inside rule runs on the clamped coordinates and
+// the out-of-domain rules of cpab_ops_2d.cu:97-117 replace the triangle bits
+// of lanes on or beyond a side, as lane masks:
+//   px <= 0 -> left (3), else px >= 1 -> right (1), else py <= 0 -> bottom
+//   (0), else py >= 1 -> top (2); the square is the clamped point's either way;
+//   beyond a corner (an x rule and a y rule both apply) the diagonal through
+//   the corner picks the y side's triangle or the x side's, with the
+//   reference's products term for term.
+// Lanes with no rule (inside, or NaN coordinates, which fail every compare as
+// in the reference) keep the inside rule's bits.  Meshgrid inputs put a point
+// on the domain's left and right edges in every row, so half the waves or
+// more of such a workload take this path at most steps.  Computed first, the
+// inside rule's compares and the side compares are independent; the side
+// masks enter as a few scalar operations ahead of the adds, and the corner
+// rule behind a scalar branch.  (Per-lane selects of the side's triangle, a
+// side-versus-inside-rule check and a nested branch made these waves take a
+// third longer per step than this; C5 chain forward 107 -> 97 us.)
 __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   const float fx = (float)nx, fy = (float)ny;
   // x lies in (0, kClampHi] iff its bit pattern minus one, as an unsigned
@@ -147,26 +123,40 @@ __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   const uint32_t uy = __builtin_bit_cast(uint32_t, py) - 1u;
   const uint64_t edge =
       __builtin_amdgcn_ballot_w64((ux > uy ? ux : uy) >= __builtin_bit_cast(uint32_t, kClampHi));
-  int base;
-  float lx, ly;
   if (!edge) {
     const float sx = __builtin_floorf(px * fx), sy = __builtin_floorf(py * fy);
-    return cell_from_square((int)fmaf(sy, fx, sx), fmaf(px, fx, -sx), fmaf(py, fy, -sy));
+    const float lx = fmaf(px, fx, -sx), ly = fmaf(py, fy, -sy);
+    return cell_from_bits((int)fmaf(sy, fx, sx), __builtin_amdgcn_ballot_w64(lx < ly),
+                          __builtin_amdgcn_ballot_w64((1.0f - lx) < ly));
   }
-  const int t = tri_2d_inside(clamp_lookup(px), clamp_lookup(py), fx, fy, base, lx, ly);
-  int c = base + t;
-  // Away from the domain's corners the boundary rules return a fixed triangle
-  // per side (left 3, right 1, bottom 0, top 2) and fall through to the inside
-  // rule otherwise (inside lanes, NaN).  Points on a domain edge (every
-  // meshgrid row has two) mostly get that same triangle from the inside rule
-  // already, so the full rules run only when some lane is at a corner or the
-  // inside rule disagrees with its side's triangle.
-  const bool xl = px <= 0.0f, xh = px >= 1.0f, yl = py <= 0.0f, yh = py >= 1.0f;
-  const int side = xl ? 3 : (xh ? 1 : (yl ? 0 : (yh ? 2 : t)));
-  const bool corner = (xl | xh) & (yl | yh);
-  if (__builtin_amdgcn_ballot_w64(corner | (side != t)))
-    c = cell_2d_outside(px, py, fx, fy, base, lx, ly);
-  return c;
+  const float xc = clamp_lookup(px), yc = clamp_lookup(py);
+  const float sx = __builtin_floorf(xc * fx), sy = __builtin_floorf(yc * fy);
+  const float lx = fmaf(xc, fx, -sx), ly = fmaf(yc, fy, -sy);
+  const int square = (int)fmaf(sy, fx, sx);  // exact: cx + cy*nx < 2^22
+  const uint64_t b3 = __builtin_amdgcn_ballot_w64(lx < ly);
+  const uint64_t b1 = __builtin_amdgcn_ballot_w64((1.0f - lx) < ly);
+  const bool xl_lane = px <= 0.0f, yl_lane = py <= 0.0f;
+  const uint64_t xl = __builtin_amdgcn_ballot_w64(xl_lane);
+  const uint64_t xh = __builtin_amdgcn_ballot_w64(px >= 1.0f);
+  const uint64_t yl = __builtin_amdgcn_ballot_w64(yl_lane);
+  const uint64_t yh = __builtin_amdgcn_ballot_w64(py >= 1.0f);
+  const uint64_t xs = xl | xh, ys = yl | yh, side = xs | ys, corner = xs & ys;
+  // Side triangles as (b3, b1): left (1,0), right (0,1), bottom (0,0), top (1,1).
+  uint64_t m3 = (b3 & ~side) | xl | (yh & ~xs);
+  uint64_t m1 = (b1 & ~side) | xh | (yh & ~xs);
+  if (corner) {
+    // cpab_ops_2d.cu:98-113: below-left pyfy < pxfx, above-left yhi > -pxfx,
+    // below-right -pyfy > xhi (as -xhi > pyfy), above-right yhi > xhi; where
+    // it holds the y side's triangle, else the x side's.
+    const float pxfx = px * fx, pyfy = py * fy;
+    const float xhi = fmaf(px, fx, -fx), yhi = fmaf(py, fy, -fy);
+    const float lhs = yl_lane ? (xl_lane ? pxfx : -xhi) : yhi;
+    const float rhs = yl_lane ? pyfy : (xl_lane ? -pxfx : xhi);
+    const uint64_t y_wins = __builtin_amdgcn_ballot_w64(lhs > rhs) & corner;
+    m3 = (m3 & ~y_wins) | (y_wins & yh);
+    m1 = (m1 & ~y_wins) | (y_wins & yh);
+  }
+  return cell_from_bits(square, m3, m1);
 }
 
 // Tetrahedron of the clamped point (xc, yc, zc) in [0,1]^3.  The cube
@@ -208,19 +198,28 @@ __device__ __forceinline__ int tet_3d(float xc, float yc, float zc, float fx, fl
 // A wave whose lanes all lie in [0,1]^3 (the meshgrid and most trajectories)
 // needs neither the corner rule nor the clamps: as unsigned integers the bit
 // patterns of +0 ... 1.0 are exactly 0 ... 0x3f800000, and negative values,
-// -0, NaN and infinities compare above.
+// -0, NaN and infinities compare above.  Meshgrid points on the x = 0 and
+// x = 1 faces drift to either side of them, so most waves of a volume warp
+// take the clamping path at most steps; there the corner rule's overshoots
+// are computed only when some lane lies outside [0,1] on all three axes (the
+// reference's overshoot (|p - 1/2| - 1/2) * n is positive only outside
+// [0,1]), which costs three compares instead of the nine operations of the
+// overshoots and their three compares.
 __device__ __forceinline__ int cell_3d(float px, float py, float pz, int nx, int ny, int nz) {
   const float fx = (float)nx, fy = (float)ny, fz = (float)nz;
   const float fxy = (float)(nx * ny);
   const uint32_t bmax = max(max(__float_as_uint(px), __float_as_uint(py)), __float_as_uint(pz));
   if (!__builtin_amdgcn_ballot_w64(bmax > 0x3f800000u)) return tet_3d(px, py, pz, fx, fy, fz, fxy);
-  const float ox = (fabsf(px - 0.5f) - 0.5f) * fx;
-  const float oy = (fabsf(py - 0.5f) - 0.5f) * fy;
-  const float oz = (fabsf(pz - 0.5f) - 0.5f) * fz;
-  // Beyond a corner (rare): move the axis with the smallest overshoot half a
-  // cell inside.  Wave-uniform branch, so the common case pays one ballot.
-  const bool corner = (ox > 0.0f) & (oy > 0.0f) & (oz > 0.0f);
-  if (__builtin_amdgcn_ballot_w64(corner)) {
+  const uint64_t out3 = __builtin_amdgcn_ballot_w64(__float_as_uint(px) > 0x3f800000u) &
+                        __builtin_amdgcn_ballot_w64(__float_as_uint(py) > 0x3f800000u) &
+                        __builtin_amdgcn_ballot_w64(__float_as_uint(pz) > 0x3f800000u);
+  if (out3) {
+    const float ox = (fabsf(px - 0.5f) - 0.5f) * fx;
+    const float oy = (fabsf(py - 0.5f) - 0.5f) * fy;
+    const float oz = (fabsf(pz - 0.5f) - 0.5f) * fz;
+    // Beyond a corner (rare): move the axis with the smallest overshoot half
+    // a cell inside (cpab_ops_3d.cu:79-88).
+    const bool corner = (ox > 0.0f) & (oy > 0.0f) & (oz > 0.0f);
     if (corner) {
       if (ox <= oy && ox <= oz) {
         px = (px < 0.5f) ? 0.5f / fx : 1.0f - 0.5f / fx;

@@ -28,6 +28,37 @@ def meshgrid(sizes):
     return np.stack([m.reshape(-1) for m in mesh[::-1]]).astype(np.float32)
 
 
+def edge_lattice(tess, seed):
+    """Points on and just beyond the domain's faces, edges and corners.
+
+    Each axis takes, in turn, an "edge" coordinate (0, -0, 1, a step outside,
+    the float neighbours of 0 and 1, denormals of both signs, the smallest
+    normal, the 2D lookup's clamp bound 1 - 2^-23, far outside) while the
+    others take cell-face coordinates k/n, their float neighbours and random
+    values; then every pair of axes, and (3D) all three, take edge coordinates
+    together.  Returns [ndim, n] float32."""
+    rng = np.random.default_rng(seed)
+    tiny = np.nextafter(np.float32(0), np.float32(1))          # smallest denormal
+    edge = np.array([0.0, -0.0, 1.0, -1e-3, 1.0 + 1e-3, np.nextafter(np.float32(1), 0),
+                     np.nextafter(np.float32(1), 2), tiny, -tiny,
+                     np.float32(2.0 ** -126) - tiny, np.float32(2.0 ** -126),
+                     np.float32(1.0 - 1e-7), -0.4, 1.4], np.float32)
+    nd = len(tess)
+
+    def across(n):
+        k = np.arange(n + 1, dtype=np.float32) / np.float32(n)
+        m = 64 if nd == 2 else 8
+        return np.concatenate([k, np.nextafter(k, np.float32(2)), np.nextafter(k, np.float32(-1)),
+                               rng.random(m).astype(np.float32)]).astype(np.float32)
+
+    parts = []
+    for mask in range(1, 1 << nd):          # bit a set: axis a takes edge coordinates
+        axes = [edge if (mask >> a) & 1 else across(tess[a]) for a in range(nd)]
+        mesh = np.meshgrid(*axes, indexing="ij")
+        parts.append(np.stack([m.ravel() for m in mesh]))
+    return np.concatenate(parts, axis=1).astype(np.float32)
+
+
 def rel_err(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)

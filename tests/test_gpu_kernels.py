@@ -11,8 +11,8 @@ from cpab.pytorch._native import native
 from cpab.pytorch.transformer import basis_tables
 from oracle import oracle as orc
 
-from helpers import (assert_adjoint_close, assert_grad_close, cpab_for, meshgrid, recover_growth,
-                     scatter_magnitude, seeded_theta, uniform_points)
+from helpers import (assert_adjoint_close, assert_grad_close, cpab_for, edge_lattice, meshgrid,
+                     recover_growth, scatter_magnitude, seeded_theta, uniform_points)
 
 pytestmark = pytest.mark.gpu
 
@@ -94,30 +94,6 @@ def test_forward_2d_bitexact(cuda, tess, pts_kind, adaptive):
     np.testing.assert_array_equal(out, ref)
 
 
-def _edge_lattice(nx, ny, seed):
-    """Points on and just beyond the domain edges: each edge coordinate (0, -0,
-    1, a step outside, the float neighbours of 0 and 1, denormals of both signs,
-    the smallest normal, the lookup's clamp bound 1 - 2^-23) against cell-edge
-    coordinates k/n and their float neighbours, plus random ones; both axes."""
-    rng = np.random.default_rng(seed)
-    tiny = np.nextafter(np.float32(0), np.float32(1))          # smallest denormal
-    edge = np.array([0.0, -0.0, 1.0, -1e-3, 1.0 + 1e-3, np.nextafter(np.float32(1), 0),
-                     tiny, -tiny, np.float32(2.0 ** -126) - tiny, np.float32(2.0 ** -126),
-                     np.float32(1.0 - 1e-7), -0.4, 1.4], np.float32)
-
-    def across(n):
-        k = np.arange(n + 1, dtype=np.float32) / np.float32(n)
-        return np.concatenate([k, np.nextafter(k, np.float32(2)), np.nextafter(k, np.float32(-1)),
-                               rng.random(64).astype(np.float32)]).astype(np.float32)
-
-    ex, ay = np.meshgrid(edge, across(ny), indexing="ij")
-    ax, ey = np.meshgrid(across(nx), edge, indexing="ij")
-    cx, cy = np.meshgrid(edge, edge, indexing="ij")
-    x = np.concatenate([ex.ravel(), ax.ravel(), cx.ravel()])
-    y = np.concatenate([ay.ravel(), ey.ravel(), cy.ravel()])
-    return np.stack([x, y]).astype(np.float32)
-
-
 @pytest.mark.parametrize("adaptive", [0, 1])
 @pytest.mark.parametrize("tess", [[20, 20], [30, 30], [3, 5]])
 def test_forward_2d_edge_ties(cuda, tess, adaptive):
@@ -126,13 +102,34 @@ def test_forward_2d_edge_ties(cuda, tess, adaptive):
     # on the domain boundary must still come out as the reference's rules say.
     T = cpab_for(tess)
     theta = seeded_theta(T, 2, 0.5, 24)
-    pts = _edge_lattice(tess[0], tess[1], 25)
+    pts = edge_lattice(tess, 25)
     As, Tr, out, cells = _forward_case(T, theta, pts, cuda, adaptive=adaptive)
     ref, ref_cells = orc.forward_trels(pts, Tr, As, tess, 50, adaptive=bool(adaptive),
                                        return_cells=True)
     np.testing.assert_array_equal(cells, ref_cells)
     np.testing.assert_array_equal(out, ref)
     g = np.random.default_rng(26).standard_normal((2, 2, pts.shape[1])).astype(np.float32)
+    _, mom, gp = _backward_case(T, theta, pts, g, cuda, adaptive=adaptive)
+    ref_m, ref_gp = orc.backward(pts, As, g, tess, 50, adaptive=bool(adaptive))
+    assert_adjoint_close(gp, ref_gp)
+    assert_grad_close(mom, ref_m, rtol=2e-5)
+
+
+@pytest.mark.parametrize("adaptive", [0, 1])
+@pytest.mark.parametrize("tess", [[4, 3, 5], [10, 10, 10]])
+def test_forward_3d_edge_lattice(cuda, tess, adaptive):
+    # Points on and beyond faces, edges and corners: the clamping path, the
+    # corner rule behind its prefilter, and the visited cells as the
+    # reference's rules give them.
+    T = cpab_for(tess)
+    theta = seeded_theta(T, 2, 0.5, 47)
+    pts = edge_lattice(tess, 27)
+    As, Tr, out, cells = _forward_case(T, theta, pts, cuda, adaptive=adaptive)
+    ref, ref_cells = orc.forward_trels(pts, Tr, As, tess, 50, adaptive=bool(adaptive),
+                                       return_cells=True)
+    np.testing.assert_array_equal(cells, ref_cells)
+    np.testing.assert_array_equal(out, ref)
+    g = np.random.default_rng(28).standard_normal((2, 3, pts.shape[1])).astype(np.float32)
     _, mom, gp = _backward_case(T, theta, pts, g, cuda, adaptive=adaptive)
     ref_m, ref_gp = orc.backward(pts, As, g, tess, 50, adaptive=bool(adaptive))
     assert_adjoint_close(gp, ref_gp)
