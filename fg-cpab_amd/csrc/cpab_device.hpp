@@ -159,6 +159,28 @@ __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   return cell_from_bits(square, m3, m1);
 }
 
+// Issue priority of a wave from its lanes' positions at the start of a
+// trajectory: lanes on or beyond the domain's edge take the lookup's clamping
+// path, and beyond a corner the corner rule too, at most steps, so their
+// waves run the longest.  Where each wave's trajectories are the only work it
+// has left to hide latency with (the chain forward: 262,144 points, 4 waves
+// per SIMD), the kernel ends with its slowest waves; raising their priority
+// lets them issue first when several waves are ready (C5 chain forward 95 ->
+// 86 us).  Waves with no such lane are set back to the default priority 0.
+template <int N>
+__device__ __forceinline__ void edge_priority(const float (&x)[N], const float (&y)[N]) {
+  bool side = false, corner = false;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const bool xo = !(x[k] > 0.0f && x[k] < 1.0f), yo = !(y[k] > 0.0f && y[k] < 1.0f);
+    side |= xo | yo;
+    corner |= xo & yo;
+  }
+  if (__builtin_amdgcn_ballot_w64(corner)) __builtin_amdgcn_s_setprio(3);
+  else if (__builtin_amdgcn_ballot_w64(side)) __builtin_amdgcn_s_setprio(2);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // Tetrahedron of the clamped point (xc, yc, zc) in [0,1]^3.  The cube
 // coordinates are kept as floats (integers below 2^24, so every sum and
 // product here is exact): floor(xc * n) capped at n - 1 as the reference's

@@ -223,6 +223,7 @@ __global__ __launch_bounds__(1024) void fwd2d_kernel(int nP, int batched, int T,
       px[k] = pts[p];
       py[k] = pts[p + nP];
     }
+    edge_priority(px, py);
     for (int st = 0; st < K; ++st) {
       const size_t row = (size_t)st * n_batch + b;
       const float* __restrict__ Tg = Trels + row * nC * 6;
