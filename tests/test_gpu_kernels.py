@@ -115,6 +115,25 @@ def test_forward_2d_edge_ties(cuda, tess, adaptive):
     assert_grad_close(mom, ref_m, rtol=2e-5)
 
 
+@pytest.mark.parametrize("tess", [[20, 20], [3, 5], [4, 3, 5]])
+def test_forward_nan_inf_points(cuda, tess):
+    # NaN and infinite coordinates, alone or beside ordinary ones: the lookup
+    # clamps NaN to 0 (fminf(fmaxf(NaN, 0), hi) in the reference; the device's
+    # v_med3_f32 returns its smallest operand when one is NaN) and fails every
+    # outside test with it, and clamps infinities to the domain.  Visited cells
+    # exact, coordinates equal (NaN where the reference's are).
+    T = cpab_for(tess)
+    theta = seeded_theta(T, 2, 0.5, 48)
+    nd = len(tess)
+    special = np.array([np.nan, -np.nan, np.inf, -np.inf, 0.3, 0.0, 1.0, -0.2, 1.2], np.float32)
+    axes = np.meshgrid(*([special] * nd), indexing="ij")
+    pts = np.stack([a.ravel() for a in axes]).astype(np.float32)
+    As, Tr, out, cells = _forward_case(T, theta, pts, cuda)
+    ref, ref_cells = orc.forward_trels(pts, Tr, As, tess, 50, return_cells=True)
+    np.testing.assert_array_equal(cells, ref_cells)
+    np.testing.assert_array_equal(out, ref)
+
+
 @pytest.mark.parametrize("adaptive", [0, 1])
 @pytest.mark.parametrize("tess", [[4, 3, 5], [10, 10, 10]])
 def test_forward_3d_edge_lattice(cuda, tess, adaptive):
