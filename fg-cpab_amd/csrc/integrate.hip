@@ -107,18 +107,19 @@ __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT],
                                          const float* __restrict__ Tg,
                                          const float* __restrict__ Ag, int T, int nx, int ny,
                                          float hh) {
-  int cur[PPT];
+  CellKey cur[PPT];
   Aff<2> M[PPT];
 #pragma unroll
   for (int k = 0; k < PPT; ++k) {
-    cur[k] = cell_2d(px[k], py[k], nx, ny);
-    M[k] = load_aff2(Tg, cur[k]);
+    cur[k] = cell_key_2d(px[k], py[k], nx, ny);
+    M[k] = load_aff2(Tg, key_cell(cur[k]));
   }
   // One step of point k from its cell c (M[k] already holds c's map).
-  auto advance = [&](int k, int c) {
+  auto advance = [&](int k, const CellKey& ck) {
     float sx, sy;
     apply2(M[k], px[k], py[k], sx, sy);
     if (ADAPTIVE) {
+      const int c = key_cell(ck);
       const int ce = cell_2d(sx, sy, nx, ny);
       if (ce != c) {
         float v0x, v0y, v1x, v1y;
@@ -136,12 +137,13 @@ __device__ __forceinline__ void steps_2d(float (&px)[PPT], float (&py)[PPT],
   auto step = [&]() {
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
-      const int c = cell_2d(px[k], py[k], nx, ny);
-      // Divergent branch, skipped (exec = 0) when no lane changed cell; marked
-      // unlikely so that the no-change case falls through.
-      if (__builtin_expect(c != cur[k], 0)) M[k] = load_aff2(Tg, c);
-      cur[k] = c;
-      advance(k, c);
+      const CellKey ck = cell_key_2d(px[k], py[k], nx, ny);
+      // Divergent branch on the changed lanes' mask, skipped (exec = 0) when
+      // no lane changed cell; marked unlikely so that this case falls through.
+      if (__builtin_expect(__builtin_amdgcn_inverse_ballot_w64(key_changed(ck, cur[k])), 0))
+        M[k] = load_aff2(Tg, key_cell(ck));
+      cur[k] = ck;
+      advance(k, ck);
     }
   };
   // Steps 1 .. T-1, two per iteration (written out: the lookup's ballots keep
