@@ -46,7 +46,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "all"])
+    ap.add_argument("--config", default="c2",
+                    choices=["c1", "c2", "c3", "c4", "c5", "c2_t16", "c2_t30", "all"])
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -101,7 +102,7 @@ def setup(cfg, nstep, dev):
     import torch
     from cpab import Cpab
 
-    if cfg in ("c1", "c2"):
+    if cfg in ("c1", "c2", "c2_t16", "c2_t30"):
         if cfg == "c1":
             T = Cpab([50])
             pts = np.linspace(0, 1, 10_000, dtype=np.float32)[None]
@@ -109,10 +110,12 @@ def setup(cfg, nstep, dev):
             desc = ("C1: 1D CPAB transform_grid fwd+MSE+backward, tess [50], zero_boundary, "
                     "10000 grid points, batch 16, nstepsolver %d" % nstep)
         else:
-            T = Cpab([20, 20])
+            n = {"c2": 20, "c2_t16": 16, "c2_t30": 30}[cfg]
+            T = Cpab([n, n])
             pts, theta, theta_t = make_c2_inputs(T)
-            desc = ("C2: 2D CPAB transform_grid fwd+MSE+backward, tess [20,20], zero_boundary, "
-                    "125000 uniform points, batch 16, nstepsolver %d" % nstep)
+            label = "C2" if cfg == "c2" else f"C2 shape at N_tess {n}"
+            desc = (f"{label}: 2D CPAB transform_grid fwd+MSE+backward, tess [{n},{n}], "
+                    "zero_boundary, 125000 uniform points, batch 16, nstepsolver %d" % nstep)
         T.set_solver_params(nstepsolver=nstep)
         x = torch.tensor(pts, device=dev)
         th0 = torch.tensor(theta, device=dev)
@@ -126,8 +129,11 @@ def setup(cfg, nstep, dev):
             return th.grad
 
         traj = pts.shape[1] * theta.shape[0]
-        return step, {"ndim": T.params.ndim, "traj": traj, "desc": desc,
-                      "global_batch": theta.shape[0], "points": pts.shape[1]}
+        info = {"ndim": T.params.ndim, "traj": traj, "desc": desc,
+                "global_batch": theta.shape[0], "points": pts.shape[1]}
+        if cfg != "c1":
+            info["ref_latency"] = lambda: reference_latency(T, x, th0)
+        return step, info
 
     if cfg in ("c3", "c4"):
         if cfg == "c3":
@@ -200,6 +206,68 @@ def setup(cfg, nstep, dev):
                   "global_batch": 1, "points": nP}
 
 
+def reference_latency(T, x, th0, n_warmup=10, n_iter=100):
+    """Forward and backward latency measured the way the reference's benchmark
+    does (benchmarks/benchmark_transformer.py:71-128): the forward is timed from
+    one synchronisation to the next around ``transform_grid``; the backward is
+    ``output.sum().backward()`` alone, the forward run untimed before it.  Mean
+    milliseconds over ``n_iter`` runs, comparable with the published figure's
+    N_tess points (docs/assets/fgcpab-scaling-2d.svg:518,734)."""
+    import numpy as np
+    import torch
+
+    def fwd():
+        return T.transform_grid(x, th0.detach().requires_grad_(True))
+
+    for _ in range(n_warmup):
+        fwd().sum().backward()
+    torch.cuda.synchronize()
+    tf, tb = [], []
+    for _ in range(n_iter):
+        torch.cuda.synchronize()
+        a = time.perf_counter()
+        out = fwd()
+        torch.cuda.synchronize()
+        tf.append(time.perf_counter() - a)
+    for _ in range(n_iter):
+        loss = fwd().sum()
+        torch.cuda.synchronize()
+        a = time.perf_counter()
+        loss.backward()
+        torch.cuda.synchronize()
+        tb.append(time.perf_counter() - a)
+    del out
+    # Peak device memory of that backward above what is allocated just before it
+    # (the output, the saved tensors and the inputs already resident).
+    loss = fwd().sum()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    loss.backward()
+    torch.cuda.synchronize()
+    bwd_mib = (torch.cuda.max_memory_allocated() - base) / 2**20
+    return {"forward_ms": round(float(np.mean(tf)) * 1e3, 4),
+            "backward_ms": round(float(np.mean(tb)) * 1e3, 4),
+            "backward_peak_MiB": round(bwd_mib, 2),
+            "method": "benchmarks/benchmark_transformer.py:71-128 (sync-to-sync mean of 100, "
+                      "backward = sum().backward() alone; backward_peak_MiB = allocator peak during "
+                      "that backward above the memory allocated before it)"}
+
+
+def step_memory(step):
+    """Device memory of one step beyond what is resident before it (inputs, target,
+    parameters): the peak of torch's caching allocator during the step, in MiB."""
+    import torch
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated()
+    return {"step_peak_MiB": round((peak - base) / 2**20, 2),
+            "resident_before_step_MiB": round(base / 2**20, 2)}
+
+
 NAMES = ["forward", "backward", "image_forward", "image_backward", "interp_forward",
          "interp_backward"]
 # fused transform_data kernels carry the integrator's work
@@ -208,24 +276,33 @@ FLOP_KIND = {"forward": "forward", "backward": "backward", "image_forward": "for
 
 
 def timed_steps(step, steps, warmup):
-    """(seconds for `steps` steps after `warmup`, {kernel: (total ms, launches)})."""
+    """(seconds for `steps` steps after `warmup`, {kernel: (total ms, launches)}).
+
+    The wall time comes from steps run without instrumentation.  The kernel
+    durations come from the same number of steps run right after, with the
+    library's HIP-event timing on: each event the library records on the launch
+    stream leaves the GPU idle for a few microseconds between kernels (about
+    5.5 us per timed kernel on MI355X), which would otherwise count against the
+    step's throughput."""
     import torch
     from cpab.pytorch import _native
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    for n in NAMES:
-        _native.profile_read(n)
-    _native.profile_enable(True)
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         g = step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    _native.profile_enable(False)
     assert torch.isfinite(g).all()
+    for n in NAMES:
+        _native.profile_read(n)
+    _native.profile_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    _native.profile_enable(False)
     return t1 - t0, {n: _native.profile_read(n) for n in NAMES}
 
 
@@ -261,6 +338,9 @@ def gpu_bench(cfg, args):
                            v["unit"]: round(v["rate"], 3)} for k, v in kern.items()}}
     total = sum(v["work"] * v["per_step"] for v in kern.values())
     out["integrator_tflops_per_step"] = round(total / (ms_step * 1e-3) / 1e12, 3)
+    out["memory"] = step_memory(step)
+    if "ref_latency" in info:
+        out["reference_style_latency"] = info["ref_latency"]()
     if "interp_step" in info:
         # HBM roofline of the standalone resampling kernels on this workload's shapes
         _, itiming = timed_steps(info["interp_step"], args.steps, args.warmup)
@@ -296,6 +376,19 @@ def profiled_traffic(cfg, kernel):
         if name.startswith(KERNEL_PREFIX.get(kernel, ())):
             return v["bytes"]
     return None
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
 
 
 def cpu_baseline(args):
@@ -335,7 +428,12 @@ def cpu_baseline(args):
         if reps >= 20:
             break
     per = tot / reps
-    return {"value": round(n * B / per, 1), "unit": "points/s", "cores": cores, "kind": "port",
+    pps = n * B / per
+    return {"value": round(pps, 1), "unit": "points/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
+            "gflops": round(pps * (FLOPS[2]["forward"] + FLOPS[2]["backward"]) * nstep / 1e9, 3),
+            "gflops_note": "algorithmic fp32 FLOPs of fwd+grad, 98 per trajectory-step (the count "
+                           "the GPU roofline uses)",
             "sample": f"{n} of the 125000 points x 16 thetas, fwd+MSE+grad, mean of "
                       f"{reps} runs ({per:.3f} s each), C/OpenMP restatement of the reference "
                       f"kernels (oracle/)"}
@@ -362,7 +460,10 @@ def line_for(cfg, r, args, cpu):
         "cpu_baseline": cpu,
         "kernels": r["kernels"],
         "integrator_tflops_per_step": r["integrator_tflops_per_step"],
+        "memory": r["memory"],
     }
+    if "reference_style_latency" in r:
+        line["reference_style_latency"] = r["reference_style_latency"]
     if "interp_roofline" in r:
         line["interp_roofline"] = r["interp_roofline"]
     if cfg == "c2":
@@ -380,7 +481,8 @@ def main():
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
               "(the CPAB path has no multi-GPU component here)", file=sys.stderr)
         sys.exit(2)
-    cfgs = ["c1", "c2", "c3", "c4", "c5"] if args.config == "all" else [args.config]
+    cfgs = (["c1", "c2", "c3", "c4", "c5", "c2_t16", "c2_t30"] if args.config == "all"
+            else [args.config])
     for cfg in cfgs:
         r = gpu_bench(cfg, args)
         cpu = None if (args.no_cpu or cfg != "c2") else cpu_baseline(args)

@@ -94,8 +94,8 @@ __device__ __forceinline__ int cell_from_bits(int square, uint64_t m3, uint64_t 
 // A wave whose lanes all lie in (0, kClampHi]^2, where the lookup clamp is the
 // identity, takes the inside rule on the raw coordinates.  Otherwise (a
 // wave-uniform branch) the inside rule runs on the clamped coordinates and
-// the out-of-domain rules of cpab_ops_2d.cu:97-117 replace the triangle bits
-// of lanes on or beyond a side, as lane masks:
+// the out-of-domain rules of cpab_ops_2d.cu:97-117 decide the triangle of
+// lanes on or beyond a side:
 //   px <= 0 -> left (3), else px >= 1 -> right (1), else py <= 0 -> bottom
 //   (0), else py >= 1 -> top (2); the square is the clamped point's either way;
 //   beyond a corner (an x rule and a y rule both apply) the diagonal through
@@ -104,12 +104,10 @@ __device__ __forceinline__ int cell_from_bits(int square, uint64_t m3, uint64_t 
 // Lanes with no rule (inside, or NaN coordinates, which fail every compare as
 // in the reference) keep the inside rule's bits.  Meshgrid inputs put a point
 // on the domain's left and right edges in every row, so half the waves or
-// more of such a workload take this path at most steps.  Computed first, the
-// inside rule's compares and the side compares are independent; the side
-// masks enter as a few scalar operations ahead of the adds, and the corner
-// rule behind a scalar branch.  (Per-lane selects of the side's triangle, a
-// side-versus-inside-rule check and a nested branch made these waves take a
-// third longer per step than this; C5 chain forward 107 -> 97 us.)
+// more of such a workload take this path at most steps, and in a chain those
+// waves run longest.  The side rules enter as substituted local coordinates
+// (below), the corner rule behind a scalar branch on the lanes beyond a
+// corner.
 //
 // The lookup yields the cell as a key: the square's index as a float (an
 // integer below 2^22, exact) and the lane masks of the two triangle bits.
@@ -151,18 +149,25 @@ __device__ __forceinline__ CellKey cell_key_2d(float px, float py, int nx, int n
   const float sx = __builtin_floorf(xc * fx), sy = __builtin_floorf(yc * fy);
   const float lx = fmaf(xc, fx, -sx), ly = fmaf(yc, fy, -sy);
   const float square = fmaf(sy, fx, sx);  // exact: cx + cy*nx < 2^22
-  const uint64_t b3 = __builtin_amdgcn_ballot_w64(lx < ly);
-  const uint64_t b1 = __builtin_amdgcn_ballot_w64((1.0f - lx) < ly);
+  // The side rules as substituted local coordinates: the inside rule's two
+  // compares, b3 = lx < ly and b1 = (1 - lx) < ly, give left (1,0) for
+  // lx = -4, right (0,1) for lx = 4, bottom (0,0) for ly = -2 and top (1,1)
+  // for ly = 2, against any ly in [0, 1) or lx in [0, 1) respectively; with
+  // both substituted the x side wins (lx = -4 or 4 decides both bits against
+  // ly = -2 or 2), as the reference tests x first.  Four selects replace the
+  // ~13 dependent scalar mask operations of the side rules (C5 chain forward
+  // 87.7 -> 79.4 us).
   const bool xl_lane = px <= 0.0f, yl_lane = py <= 0.0f;
-  const uint64_t xl = __builtin_amdgcn_ballot_w64(xl_lane);
-  const uint64_t xh = __builtin_amdgcn_ballot_w64(px >= 1.0f);
-  const uint64_t yl = __builtin_amdgcn_ballot_w64(yl_lane);
-  const uint64_t yh = __builtin_amdgcn_ballot_w64(py >= 1.0f);
-  const uint64_t xs = xl | xh, ys = yl | yh, side = xs | ys, corner = xs & ys;
-  // Side triangles as (b3, b1): left (1,0), right (0,1), bottom (0,0), top (1,1).
-  uint64_t m3 = (b3 & ~side) | xl | (yh & ~xs);
-  uint64_t m1 = (b1 & ~side) | xh | (yh & ~xs);
+  const bool xh_lane = px >= 1.0f, yh_lane = py >= 1.0f;
+  const float lxs = xl_lane ? -4.0f : (xh_lane ? 4.0f : lx);
+  const float lys = yl_lane ? -2.0f : (yh_lane ? 2.0f : ly);
+  uint64_t m3 = __builtin_amdgcn_ballot_w64(lxs < lys);
+  uint64_t m1 = __builtin_amdgcn_ballot_w64((1.0f - lxs) < lys);
+  const uint64_t corner =
+      (__builtin_amdgcn_ballot_w64(xl_lane) | __builtin_amdgcn_ballot_w64(xh_lane)) &
+      (__builtin_amdgcn_ballot_w64(yl_lane) | __builtin_amdgcn_ballot_w64(yh_lane));
   if (corner) {
+    const uint64_t yh = __builtin_amdgcn_ballot_w64(yh_lane);
     // cpab_ops_2d.cu:98-113: below-left pyfy < pxfx, above-left yhi > -pxfx,
     // below-right -pyfy > xhi (as -xhi > pyfy), above-right yhi > xhi; where
     // it holds the y side's triangle, else the x side's.

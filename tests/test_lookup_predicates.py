@@ -7,9 +7,10 @@
   could disagree (zeros, denormals, the clamp bound and 1, the top of the
   finite range, infinities and NaNs of both signs) and a random sample of the
   rest.
-- The 2D edge path's lane-mask form of the reference's out-of-domain rules,
-  restated per lane, against the oracle's if-chain on the edge lattice,
-  NaN / infinity combinations and points around the domain.
+- The 2D edge path's form of the reference's out-of-domain rules (side rules
+  as substituted local coordinates, the corner rule on lane masks), restated
+  per lane, against the oracle's if-chain on the edge lattice, NaN / infinity
+  combinations, points around the domain and points far outside it.
 - The 3D corner prefilter: a positive corner overshoot only outside [+0, 1].
 """
 import numpy as np
@@ -47,11 +48,11 @@ def test_edge_predicate_matches_float_compares():
 
 
 # ---------------------------------------------------------------------------
-# The 2D lookup's edge path as lane masks (cpab_device.hpp, cell_2d): the inside
-# rule on the clamped coordinates, whose two triangle bits are replaced for
-# lanes on or beyond a side, and for lanes beyond a corner by the corner rule.
-# Restated per lane in numpy (a lane's bit of each mask), against the oracle's
-# if-chain of the reference rules.
+# The 2D lookup's edge path (cpab_device.hpp, cell_2d): the inside rule on the
+# clamped coordinates, with the side rules entered as substituted local
+# coordinates (lx = -4 left, 4 right; ly = -2 bottom, 2 top) and lanes beyond
+# a corner decided by the corner rule.  Restated per lane in numpy (a lane's
+# bit of each mask), against the oracle's if-chain of the reference rules.
 # ---------------------------------------------------------------------------
 
 def _fma32(a, b, c):
@@ -59,7 +60,7 @@ def _fma32(a, b, c):
     return (np.float64(a) * np.float64(b) + np.float64(c)).astype(np.float32)
 
 
-def _mask_rule_2d(px, py, nx, ny):
+def _edge_rule_2d(px, py, nx, ny):
     fx, fy = np.float32(nx), np.float32(ny)
 
     def clamp(v):   # v_med3_f32(v, 0, K): NaN -> min3 -> 0
@@ -70,13 +71,12 @@ def _mask_rule_2d(px, py, nx, ny):
         sx, sy = np.floor(xc * fx), np.floor(yc * fy)
         lx, ly = _fma32(xc, fx, -sx), _fma32(yc, fy, -sy)
         square = (sy * fx + sx).astype(np.int64)
-        b3 = lx < ly
-        b1 = (np.float32(1) - lx) < ly
         xl, xh, yl, yh = px <= 0, px >= 1, py <= 0, py >= 1
-        xs, ys = xl | xh, yl | yh
-        side, corner = xs | ys, xs & ys
-        m3 = (b3 & ~side) | xl | (yh & ~xs)
-        m1 = (b1 & ~side) | xh | (yh & ~xs)
+        lxs = np.where(xl, np.float32(-4), np.where(xh, np.float32(4), lx)).astype(np.float32)
+        lys = np.where(yl, np.float32(-2), np.where(yh, np.float32(2), ly)).astype(np.float32)
+        m3 = lxs < lys
+        m1 = (np.float32(1) - lxs) < lys
+        corner = (xl | xh) & (yl | yh)
         pxfx, pyfy = px * fx, py * fy
         xhi = _fma32(px, fx, np.full_like(px, -fx))
         yhi = _fma32(py, fy, np.full_like(py, -fy))
@@ -89,7 +89,7 @@ def _mask_rule_2d(px, py, nx, ny):
 
 
 @pytest.mark.parametrize("tess", [[20, 20], [30, 30], [3, 5], [16, 16], [1, 1], [1000, 7]])
-def test_edge_masks_match_reference_rules(tess):
+def test_edge_rule_matches_reference_rules(tess):
     from oracle import oracle as orc
     from helpers import edge_lattice
     rng = np.random.default_rng(3)
@@ -98,8 +98,9 @@ def test_edge_masks_match_reference_rules(tess):
     sp = np.stack(np.meshgrid(np.concatenate([special, lat[0, :40]]),
                               np.concatenate([special, lat[1, :40]]), indexing="ij")).reshape(2, -1)
     wide = (rng.random((2, 200000)) * 1.6 - 0.3).astype(np.float32)
-    for pts in (lat, sp.astype(np.float32), wide):
-        got = _mask_rule_2d(pts[0], pts[1], *tess)
+    far = (rng.standard_normal((2, 100000)) * 1e3).astype(np.float32)
+    for pts in (lat, sp.astype(np.float32), wide, far):
+        got = _edge_rule_2d(pts[0], pts[1], *tess)
         ref = orc.cells(2, pts, tess)
         bad = np.flatnonzero(got != ref)
         assert bad.size == 0, (pts[:, bad[:5]].T.tolist(), got[bad[:5]], ref[bad[:5]])
