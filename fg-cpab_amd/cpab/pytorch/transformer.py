@@ -313,13 +313,13 @@ class _CPABImageFunction(torch.autograd.Function):
                             1.0 / T, As, Trels)
         else:
             lib.affine(ndim, theta_c, nC, tab["row_ptr"], tab["col_idx"], tab["vals"], As)
-        # For the backward: with one channel the sample's spatial gradient at
-        # each final point (the seed then needs no data reads); the final
-        # points themselves when grad_data's scatter or several channels need
-        # them.
+        # For the backward: with one channel and no grad_data the sample's
+        # spatial gradient at each final point (the seed then needs no data
+        # reads); the final points themselves when grad_data's scatter or
+        # several channels need them.
         one = data.shape[1] == 1
         seed_grad = (torch.empty((n, ndim, nP), device=dev, dtype=torch.float32)
-                     if ctx.needs_input_grad[1] and one else None)
+                     if ctx.needs_input_grad[1] and one and not ctx.needs_input_grad[0] else None)
         final = (torch.empty((n, ndim, nP), device=dev, dtype=torch.float32)
                  if ctx.needs_input_grad[0] or (ctx.needs_input_grad[1] and not one) else None)
         out = torch.empty((n, data.shape[1], *outsize), device=dev, dtype=torch.float32)
