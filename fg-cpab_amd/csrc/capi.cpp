@@ -96,9 +96,15 @@ int check_steps(int T) {
   return CPAB_OK;
 }
 
+// Points (and image output positions) per row.  The kernels index a row's
+// points with 32-bit ints and walk them as p0 + k * stride with k <= 2 and a
+// grid stride of at most CUs * 4096 lanes, so nP + 2 * stride must stay below
+// 2^31; below 2^31 / 3 it does with more than 2^30 to spare.
+constexpr int64_t kMaxPoints = (1LL << 31) / 3;
+
 int check_points(int64_t nP, int64_t n_theta, int ndim) {
   if (nP < 0 || n_theta < 0) return fail(CPAB_ERR_INVALID, "negative size (nP=%lld, n_theta=%lld)", (long long)nP, (long long)n_theta);
-  if (nP >= (1LL << 31) / 3) return fail(CPAB_ERR_INVALID, "nP=%lld exceeds the 32-bit point index", (long long)nP);
+  if (nP >= kMaxPoints) return fail(CPAB_ERR_INVALID, "nP=%lld exceeds the 32-bit point index", (long long)nP);
   if (n_theta >= 65536) return fail(CPAB_ERR_INVALID, "n_theta=%lld exceeds the grid limit 65535", (long long)n_theta);
   (void)ndim;
   return CPAB_OK;
@@ -462,7 +468,8 @@ int image_shape(int ndim, int64_t n_batch, int64_t C, const int64_t* in_size,
     if (in_size[k] < 1 || out_size[k] < 1) return fail(CPAB_ERR_INVALID, "sizes must be >= 1 (axis %d)", k);
     nP *= out_size[k];
     plane *= in_size[k];
-    if (nP >= (1LL << 31)) return fail(CPAB_ERR_INVALID, "image too large");
+    if (nP >= kMaxPoints)
+      return fail(CPAB_ERR_INVALID, "output of %lld positions exceeds the 32-bit point index", (long long)nP);
     // the gathers address one channel with 32-bit byte offsets
     if (plane > (1LL << 30)) return fail(CPAB_ERR_INVALID, "one data channel must hold at most 2^30 values");
   }

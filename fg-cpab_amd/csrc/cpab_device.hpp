@@ -34,9 +34,10 @@ constexpr int kRegSteps = 50;
 // position by up to ||M_c||_2 per step.  It does so only for rows (thetas)
 // whose bound (max_c ||M_c||_2)^T is at most kRecoverGrowth; other rows replay
 // the trajectory from checkpoints, which reproduces the replayed positions
-// exactly.  Measured on a CPU emulation of the recovery: the largest position
-// error is about 3.5e-6 at a bound near 2 (theta ~ N(0, 0.5^2), the benchmark
-// scale) and grows like 3e-7 x the bound beyond, so 16 keeps it near 5e-6.
+// exactly.  Measured on a CPU emulation of the recovery (1D/2D/3D rows): the
+// largest position error is about 4e-6 below a bound of 2 (theta ~ N(0, 0.5^2),
+// the benchmark scale), 7e-6 below 8 and 1.5e-5 below 16; rows at 1e2 .. 1e3
+// reach 3e-5 .. 2.7e-4.
 constexpr float kRecoverGrowth = 16.0f;
 // Hashed LDS cell cache of the backward when the full moment table does not
 // fit in LDS: slots (a power of two) and linear-probe length.  3D: 2048 x 13

@@ -134,9 +134,12 @@ int cpab_backward_project(int ndim, int64_t nP, int64_t n_theta, int batched, in
  * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
  * results and kernels as cpab_backward without the workspace: the workspace
  * is a library-owned device array of CPAB_NOALLOC_SCRATCH_BYTES on each GPU
- * (held until the process ends), and the call allocates nothing.  Problems
- * whose cpab_backward_workspace_size(...) exceeds it are rejected with
- * CPAB_ERR_INVALID before anything is enqueued.  Every call on one GPU uses
+ * (held until the process ends), and the call allocates nothing.  A problem
+ * is rejected with CPAB_ERR_INVALID, before anything is enqueued, when the
+ * workspace of the backward variant that will run for it exceeds that size;
+ * that workspace is at most cpab_backward_workspace_size(...), which also
+ * covers the other variant, so a problem within the limit by that size is
+ * always accepted and some above it are too.  Every call on one GPU uses
  * that GPU's one array: calls that overlap on a GPU (other streams, other
  * host threads) race and must be serialised by the caller.  Kernel timing
  * (cpab_profile_enable) does not cover these calls. */

@@ -157,10 +157,11 @@ static void FN(adjoint)(int ndim, const R* A, const R* p, R h, R hh, R hhh, R* m
 }
 
 /* ---- forward with Trels (cpab_ops_2d.cu:164-230, cpab_ops_3d.cu:169-241) ----
- * cells (nullable): [n_theta, nP, T] cell index used at each step. */
+ * cells (nullable): [n_theta, nP, T] cell index used at each step.
+ * path (nullable): [n_theta, T, ndim, nP] the position each step looks up. */
 void FN(orc_forward_trels)(int ndim, int64_t nP, int64_t n_theta, int batched, int T, int nx,
                            int ny, int nz, int adaptive, const R* points, const R* Trels,
-                           const R* As, R* out, int32_t* cells) {
+                           const R* As, R* out, int32_t* cells, R* path) {
   const int P = ndim * (ndim + 1);
   const int nC = ndim == 2 ? 4 * nx * ny : 5 * nx * ny * nz;
   const R h = (R)1 / (R)T, hh = (R)0.5 * h;
@@ -177,6 +178,8 @@ void FN(orc_forward_trels)(int ndim, int64_t nP, int64_t n_theta, int batched, i
       for (t = 0; t < T; ++t) {
         int c = FN(cell)(ndim, p, nx, ny, nz);
         if (cells) cells[(b * nP + i) * T + t] = c;
+        if (path)
+          for (k = 0; k < ndim; ++k) path[((b * T + t) * ndim + k) * nP + i] = p[k];
         FN(apply)(ndim, Tb + P * c, p, s);
         if (adaptive) {
           int ce = FN(cell)(ndim, s, nx, ny, nz);
@@ -194,10 +197,11 @@ void FN(orc_forward_trels)(int ndim, int64_t nP, int64_t n_theta, int batched, i
 }
 
 /* ---- midpoint trajectory endpoint: the map the backward differentiates ----
- * (phase 1 of cpab_ops_2d.cu:426-440).  cells (nullable): [n_theta, nP, T]. */
+ * (phase 1 of cpab_ops_2d.cu:426-440).  cells (nullable): [n_theta, nP, T];
+ * path (nullable): [n_theta, T, ndim, nP] the position each step looks up. */
 void FN(orc_forward_midpoint)(int ndim, int64_t nP, int64_t n_theta, int batched, int T, int nx,
                               int ny, int nz, int adaptive, const R* points, const R* As, R* out,
-                              int32_t* cells) {
+                              int32_t* cells, R* path) {
   const int P = ndim * (ndim + 1);
   const int nC = ndim == 1 ? nx : ndim == 2 ? 4 * nx * ny : 5 * nx * ny * nz;
   const R h = (R)1 / (R)T, hh = h * (R)0.5;
@@ -213,6 +217,8 @@ void FN(orc_forward_midpoint)(int ndim, int64_t nP, int64_t n_theta, int batched
       for (t = 0; t < T; ++t) {
         int c = FN(cell)(ndim, p, nx, ny, nz);
         if (cells) cells[(b * nP + i) * T + t] = c;
+        if (path)
+          for (k = 0; k < ndim; ++k) path[((b * T + t) * ndim + k) * nP + i] = p[k];
         FN(replay_step)(ndim, Ab, c, p, h, hh, adaptive, nx, ny, nz);
       }
       for (k = 0; k < ndim; ++k) out[(b * ndim + k) * nP + i] = p[k];

@@ -63,8 +63,8 @@ def lib():
             "orc_expm_f32": [_i, _l, _f, _p, _p],
             "orc_affine": [_l, _i, _i, _p, _p, _p, _p, _p],
             "orc_project": [_l, _i, _i, _p, _p, _p, _p, _p],
-            "orc_forward_trels": [_i, _l, _l, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p],
-            "orc_forward_midpoint": [_i, _l, _l, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p],
+            "orc_forward_trels": [_i, _l, _l, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p],
+            "orc_forward_midpoint": [_i, _l, _l, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p],
             "orc_backward": [_i, _l, _l, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p],
             "orc_forward_closed_1d": [_l, _l, _i, _i, _p, _p, _p],
             "orc_interp_forward": [_i, _l, _l, _p, _p, _p, _p, _p],
@@ -149,32 +149,39 @@ def _pts(points, n_theta, dtype):
 
 
 def forward_trels(points, Trels, As, nc, T, adaptive=False, n_theta=None, return_cells=False,
-                  dtype=np.float32):
-    """Trels stepping (2D/3D forward).  Trels/As [n_theta, nC, ndim, ndim+1]."""
+                  dtype=np.float32, return_path=False):
+    """Trels stepping (2D/3D forward).  Trels/As [n_theta, nC, ndim, ndim+1].
+    return_path: also the position each step looks up, [n_theta, T, ndim, nP]."""
     Tr, A = _c(Trels, dtype), _c(As, dtype)
     n_theta = Tr.shape[0]
     pts, batched, nP, ndim = _pts(points, n_theta, dtype)
     out = np.empty((n_theta, ndim, nP), dtype)
     cl = np.empty((n_theta, nP, T), np.int32) if return_cells else None
+    path = np.empty((n_theta, T, ndim, nP), dtype) if return_path else None
     nx, ny, nz = _geo(nc)
     getattr(lib(), "orc_forward_trels" + _suffix(dtype))(
         ndim, nP, n_theta, batched, T, nx, ny, nz, int(adaptive), _ptr(pts), _ptr(Tr), _ptr(A),
-        _ptr(out), _ptr(cl))
-    return (out, cl) if return_cells else out
+        _ptr(out), _ptr(cl), _ptr(path))
+    res = (out,) + ((cl,) if return_cells else ()) + ((path,) if return_path else ())
+    return res if len(res) > 1 else out
 
 
-def forward_midpoint(points, As, nc, T, adaptive=False, return_cells=False, dtype=np.float32):
-    """Explicit-midpoint trajectory endpoint: the map the backward differentiates."""
+def forward_midpoint(points, As, nc, T, adaptive=False, return_cells=False, dtype=np.float32,
+                     return_path=False):
+    """Explicit-midpoint trajectory endpoint: the map the backward differentiates.
+    return_path: also the position each step looks up, [n_theta, T, ndim, nP]."""
     A = _c(As, dtype)
     n_theta = A.shape[0]
     pts, batched, nP, ndim = _pts(points, n_theta, dtype)
     out = np.empty((n_theta, ndim, nP), dtype)
     cl = np.empty((n_theta, nP, T), np.int32) if return_cells else None
+    path = np.empty((n_theta, T, ndim, nP), dtype) if return_path else None
     nx, ny, nz = _geo(nc)
     getattr(lib(), "orc_forward_midpoint" + _suffix(dtype))(
         ndim, nP, n_theta, batched, T, nx, ny, nz, int(adaptive), _ptr(pts), _ptr(A), _ptr(out),
-        _ptr(cl))
-    return (out, cl) if return_cells else out
+        _ptr(cl), _ptr(path))
+    res = (out,) + ((cl,) if return_cells else ()) + ((path,) if return_path else ())
+    return res if len(res) > 1 else out
 
 
 def backward(points, As, grad_out, nc, T, adaptive=False, dtype=np.float32):

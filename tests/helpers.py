@@ -112,6 +112,49 @@ def recover_growth(As, T=50):
     return s.max(axis=-1) ** T
 
 
+def recover_error(points, As, nc, T=50):
+    """Per theta row, the largest distance between the positions the register
+    backward recovers and the replayed ones (CPU emulation, float32 data).
+
+    Phase 1 replays the explicit-midpoint trajectory (the oracle's replay,
+    which the kernels match bit for bit) and keeps its cells; phase 2 starts
+    from the final position and steps back through each cell's inverse
+    one-step map, p <- M_c p + m_c, with M_c and m_c formed in float64 from E_c
+    = I + hA + (h^2/2)A^2 and e_c = hb + (h^2/2)Ab and rounded to float32, and
+    each component accumulated from m_c by fmaf in the kernels' order (last
+    coordinate first).  fmaf is emulated in float64: the product of two
+    floats is exact there, the sum is rounded once to float64 and once to
+    float32.  As: [rows, nC, nd, nd + 1]; points [nd, nP]."""
+    from oracle import oracle as orc
+    A64 = np.asarray(As, np.float64)
+    nd = A64.shape[-2]
+    h = np.float32(1.0) / np.float32(T)
+    hd, h2 = float(h), float(h) * float(h * np.float32(0.5))
+    L, b = A64[..., :nd], A64[..., nd]
+    E = np.eye(nd) + hd * L + h2 * (L @ L)
+    e = hd * b + h2 * (L @ b[..., None])[..., 0]
+    M = np.linalg.inv(E)
+    m = -(M @ e[..., None])[..., 0]
+    M, m = M.astype(np.float32), m.astype(np.float32)
+    final, cells, path = orc.forward_midpoint(points, As, nc, T, return_cells=True,
+                                              return_path=True)
+    err = np.zeros(A64.shape[0])
+    for r in range(A64.shape[0]):
+        p = final[r].astype(np.float64)
+        for t in range(T - 1, -1, -1):
+            c = cells[r, :, t]
+            q = np.empty_like(p)
+            for i in range(nd):
+                acc = m[r, c, i].astype(np.float64)
+                for j in range(nd - 1, -1, -1):
+                    acc = (M[r, c, i, j].astype(np.float64) * p[j] + acc).astype(np.float32)
+                    acc = acc.astype(np.float64)
+                q[i] = acc
+            p = q
+            err[r] = max(err[r], float(np.abs(p - path[r, t]).max()))
+    return err
+
+
 def scatter_magnitude(data_shape, grid, outs, gout):
     """Per data pixel, the sum over its grad_data contributions of |g * w|
     (float64), w being the corner weight of the point's resampling.

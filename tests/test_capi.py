@@ -121,6 +121,21 @@ def _check_trace_and_interp_validation():
     rc = lib.cpab_transform_data_forward(3, 1, 1, big, sizes, 50, 2, 2, 2, 0, p, p, p, p, p, None,
                                          None, None)
     assert rc == 1 and "2^30" in _err(lib)
+    # The fused image calls index output positions with 32-bit ints and walk
+    # them in grid strides (two positions per lane in 2D): the output must
+    # stay below (2^31 - 1) / 3 positions, the point limit of cpab_forward.
+    small = (ctypes.c_int64 * 2)(8, 8)
+    for out in ((1 << 16, (1 << 15) - 2), (715827883, 1), ((1 << 31) - 1, 1)):
+        outs = (ctypes.c_int64 * 2)(*out)
+        rc = lib.cpab_transform_data_forward(2, 1, 1, small, outs, 50, 2, 2, 1, 0, p, p, p, p, p,
+                                             None, None, None)
+        assert rc == 1 and "32-bit point index" in _err(lib), out
+        rc = lib.cpab_transform_data_backward(2, 1, 1, small, outs, 50, 2, 2, 1, 0, p, p, None, p,
+                                              p, p, 0, None, None, None, p, None, None, p, 1 << 30,
+                                              None)
+        assert rc == 1 and "32-bit point index" in _err(lib), out
+    rc = lib.cpab_forward(2, 715827882, 1, 0, 50, 2, 2, 1, 0, p, p, p, p, None)
+    assert rc == 1 and "32-bit point index" in _err(lib)
 
 
 def test_transform_data_seed_grad_checks():

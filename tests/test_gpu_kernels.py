@@ -714,10 +714,11 @@ def test_transform_data_seed_grad(cuda, tess, ins, outs, scale):
 
 @pytest.mark.parametrize("case", ["dense", "sparse", "cache3d", "chain", "image"])
 def test_fused_projection_matches_project(cuda, case):
-    # The backward launch forms each row's moments and projects them onto the
-    # basis in its last workgroup; the projection must equal cpab_project of
-    # the same moments bit for bit (same summation order), and the moments the
-    # oracle's within the backward's tolerance.
+    # The backward entry points with a basis table finish each row's moments
+    # and then project them onto the basis (two launches after the sweep); the
+    # projection must equal cpab_project of the same moments bit for bit (same
+    # summation order), and the moments the oracle's within the backward's
+    # tolerance.
     tess = {"dense": [20, 20], "sparse": [16, 16], "cache3d": [10, 10, 10], "chain": [16, 16],
             "image": [6, 5]}[case]
     T = cpab_for(tess)

@@ -91,3 +91,45 @@ def test_noalloc_rejects_beyond_limit(cuda):
     # and a problem that fits still runs after the rejection
     p, pts, As, g = _case(cuda, [4, 4], 2, 500, False, 306)
     _both(cuda, p, pts, As, g, False)
+
+
+def test_noalloc_under_graph_capture(cuda):
+    # The callers the entry point is for include code under HIP graph capture:
+    # record it into a torch CUDA graph in global capture mode (an allocation,
+    # a synchronisation or another capture-unsafe call in any thread then
+    # fails the capture), replay it with the inputs changed in place and eager
+    # work and synchronisations between the replays, and check every replay
+    # against cpab_backward with a workspace.  Every tensor is allocated before
+    # the capture, and the first (eager) call sets up the scratch address and
+    # kernel attributes outside it.
+    p, pts, As, g = _case(cuda, [20, 20], 4, 8000, False, 307)
+    nd, ppc = p.ndim, p.ndim * (p.ndim + 1)
+    n_theta, nP = As.shape[0], pts.shape[-1]
+    g0 = g.clone()
+    ref_m = torch.empty((n_theta, p.nC, ppc), device=cuda)
+    ref_gp = torch.empty((n_theta, nd, nP), device=cuda)
+    ws = torch.empty(native().backward_workspace_size(nd, nP, n_theta, p.nC), dtype=torch.uint8,
+                     device=cuda)
+    native().backward(nd, pts, False, n_theta, nP, 50, p.nc, 0, As, g0, ref_m, ref_gp, ws)
+    m = torch.empty((n_theta, p.nC, ppc), device=cuda)
+    gp = torch.empty((n_theta, nd, nP), device=cuda)
+    native().backward_noalloc(nd, pts, False, n_theta, nP, 50, p.nc, 0, As, g, m, gp)
+    torch.cuda.synchronize()
+    assert_grad_close(m.cpu().numpy(), ref_m.cpu().numpy(), rtol=2e-5)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, capture_error_mode="global"):
+        native().backward_noalloc(nd, pts, False, n_theta, nP, 50, p.nc, 0, As, g, m, gp)
+    torch.cuda.synchronize()
+    ref_m, ref_gp = ref_m.cpu().numpy(), ref_gp.cpu().numpy()
+    for k in (1.0, 2.0, 0.5, 1.0):
+        # the backward is linear in grad_out, and scaling by a power of two is
+        # exact: the replay must follow the new input
+        g.copy_(g0 * k)
+        m.fill_(7.0)
+        gp.fill_(-3.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_grad_close(m.cpu().numpy(), ref_m * k, rtol=2e-5)
+        assert_adjoint_close(gp.cpu().numpy(), ref_gp * k)
+    del graph
