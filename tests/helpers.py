@@ -65,14 +65,15 @@ def rel_err(a, b):
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
 
 
-def assert_grad_close(got, ref, rtol=1e-4, atol_frac=5e-5):
-    """Gradient parity: per element |got - ref| <= rtol*|ref| + atol_frac*max|ref|.
+def assert_grad_close(got, ref, rtol=2e-5, atol_frac=5e-6):
+    """Moment parity: per element |got - ref| <= rtol*|ref| + atol_frac*max|ref|.
 
     The moments are sums of many per-trajectory contributions accumulated with
     float atomics in no fixed order, so elements whose contributions cancel
     carry an absolute (not relative) error of a few fp32 ulps of the summed
-    magnitudes; atol_frac*max|ref| bounds that (normwise, half the 1e-4
-    relative tolerance the gradients are held to).
+    magnitudes; atol_frac*max|ref| bounds that.  Measured on MI355X over the
+    GPU suite: at rtol 2e-5 the largest absolute part needed is 1.2e-6 of
+    max|ref| (the stage-wise chain cases), a quarter of the bound.
     """
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
@@ -89,11 +90,45 @@ def assert_adjoint_close(got, ref):
     per-cell G = h A + (h^2/2) A^2, the reference's two half-steps
     (cpab_ops_2d.cu:374-381) multiplied out: the same number, rounded
     differently, so after T steps the two differ by a few fp32 ulps of the
-    trajectory's adjoint.  Held per element to 1e-5 relative plus 2e-6 of the
-    largest adjoint (a CPU emulation of the factored arithmetic stays within
-    3e-6 normwise on the kernel-test cases).
+    trajectory's adjoint.  Held per element to 1e-5 relative plus 1e-6 of the
+    largest adjoint (measured on MI355X over the GPU suite: at most 4.1e-7 of
+    it needed beyond the relative part).
     """
-    assert_grad_close(got, ref, rtol=1e-5, atol_frac=2e-6)
+    assert_grad_close(got, ref, rtol=1e-5, atol_frac=1e-6)
+
+
+def theta_grad_bound(got, mom, basis, scale=1.0, rtol=2e-5, atol_frac=5e-6):
+    """(|got - ref|, bound) for a theta gradient; see assert_theta_grad_close."""
+    import scipy.sparse as sp
+    got = np.asarray(got, np.float64)
+    m = np.asarray(mom, np.float64).reshape(got.shape[0], -1)
+    Bc = sp.csc_matrix(basis, dtype=np.float64)
+    Ba = abs(Bc)
+    nnz = int(np.diff(Bc.indptr).max()) if Bc.nnz else 0
+    ref = (Bc.T @ m.T).T * scale
+    tol_m = rtol * np.abs(m) + atol_frac * np.abs(m).max()
+    rounding = (nnz + 1) * 2.0 ** -24 * (Ba.T @ np.abs(m).T).T
+    bound = ((Ba.T @ tol_m.T).T + rounding) * abs(scale)
+    return np.abs(got - ref), bound
+
+
+def assert_theta_grad_close(got, mom, basis, scale=1.0, rtol=2e-5, atol_frac=5e-6):
+    """Theta-gradient parity, propagated from the moments' tolerance.
+
+    got [rows, d] is the library's gradient; the reference is scale * B^T m
+    per row, m [rows, D] being the oracle's moments and B the basis [D, d].
+    The library's moments are held to rtol*|m| + atol_frac*max|m| (the moment
+    bound of assert_grad_close); the projection carries that to each
+    theta-gradient element as |B|^T of it, plus the projection's own fp32
+    rounding (B rounded to float32 and at most nnz terms summed:
+    (nnz + 1) 2^-24 |B|^T |m|).  A bound on the gradient alone, relative to
+    its own largest element, would have to be ~30x looser than the moments':
+    each element sums moment contributions of both signs that cancel, so it
+    is small next to the moments it sums, and their rounding is not."""
+    err, bound = theta_grad_bound(got, mom, basis, scale, rtol, atol_frac)
+    bad = err > bound
+    assert not bad.any(), (f"{bad.sum()} of {bad.size} elements off; worst err/bound "
+                           f"{(err / np.maximum(bound, 1e-300)).max():.3f}")
 
 
 def recover_growth(As, T=50):

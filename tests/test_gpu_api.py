@@ -7,13 +7,15 @@ import torch
 
 from oracle import oracle as orc
 
-from helpers import assert_grad_close, cpab_for, meshgrid, scatter_magnitude, seeded_theta, uniform_points
+from helpers import (assert_theta_grad_close, cpab_for, meshgrid, scatter_magnitude, seeded_theta,
+                     uniform_points)
 
 pytestmark = pytest.mark.gpu
 
 
 def _oracle_grid(T, theta, pts, g_out, nstep=50):
-    """Oracle forward + theta / points gradient of <out, g_out>."""
+    """Oracle forward, moments [n_theta, D] (theta gradient B^T m) and points
+    gradient of <out, g_out>."""
     p = T.params
     nd = p.ndim
     As = orc.affine(theta, p.basis).reshape(theta.shape[0], p.nC, nd, nd + 1)
@@ -22,10 +24,9 @@ def _oracle_grid(T, theta, pts, g_out, nstep=50):
     else:
         out = orc.forward_trels(pts, orc.expm(nd, As, 1.0 / nstep), As, p.nc, nstep)
     mom, gp = orc.backward(pts, As, g_out, p.nc, nstep)
-    gth = orc.project(mom.reshape(theta.shape[0], -1), p.basis, dtype=np.float64)
     if pts.ndim == 2:
         gp = gp.astype(np.float64).sum(0)
-    return out, gth, gp
+    return out, mom.reshape(theta.shape[0], -1), gp
 
 
 @pytest.mark.parametrize("tess,n,B", [([50], 10000, 16), ([20, 20], 20000, 4),
@@ -40,9 +41,9 @@ def test_transform_grid_fwd_bwd(cuda, tess, n, B):
     x = torch.tensor(pts, device=cuda, requires_grad=True)
     out = T.transform_grid(x, th)
     out.backward(torch.tensor(g, device=cuda))
-    ref_out, ref_gth, ref_gp = _oracle_grid(T, theta, pts, g)
+    ref_out, ref_m, ref_gp = _oracle_grid(T, theta, pts, g)
     np.testing.assert_allclose(out.detach().cpu().numpy(), ref_out, atol=1e-5, rtol=0)
-    assert_grad_close(th.grad.cpu().numpy(), ref_gth)
+    assert_theta_grad_close(th.grad.cpu().numpy(), ref_m, T.params.basis)
     np.testing.assert_allclose(x.grad.cpu().numpy(), ref_gp, rtol=1e-5,
                                atol=1e-6 * np.abs(ref_gp).max())
 
@@ -61,9 +62,9 @@ def test_transform_grid_mse_loss_c2_shape(cuda):
     loss = ((out - target) ** 2).mean()
     loss.backward()
     g = (2.0 / out.numel()) * (out - target).detach().cpu().numpy().astype(np.float32)
-    ref_out, ref_gth, _ = _oracle_grid(T, theta, pts, g)
+    ref_out, ref_m, _ = _oracle_grid(T, theta, pts, g)
     np.testing.assert_allclose(out.detach().cpu().numpy(), ref_out, atol=1e-5, rtol=0)
-    assert_grad_close(th.grad.cpu().numpy(), ref_gth)
+    assert_theta_grad_close(th.grad.cpu().numpy(), ref_m, T.params.basis)
 
 
 @pytest.mark.parametrize("tess,ins", [([30, 30], (64, 48)), ([10, 10, 10], (20, 18, 16))])
@@ -88,8 +89,7 @@ def test_transform_data(cuda, tess, ins):
     np.testing.assert_allclose(out.detach().cpu().numpy(), ref, atol=1e-5, rtol=0)
     gg, _ = orc.interp_backward(nd, data, grid_t, ins, gout, want_data=False)
     mom, _ = orc.backward(grid, As, gg, p.nc, 50)
-    ref_gth = orc.project(mom.reshape(B, -1), p.basis, dtype=np.float64)
-    assert_grad_close(th.grad.cpu().numpy(), ref_gth)
+    assert_theta_grad_close(th.grad.cpu().numpy(), mom, p.basis)
 
 
 def test_transform_data_data_gradient(cuda):
@@ -139,12 +139,11 @@ def test_transform_grid_chain(cuda):
         xs.append(orc.forward_trels(xs[-1], orc.expm(2, As, 1 / 50), As, p.nc, 50))
     np.testing.assert_allclose(out.detach().cpu().numpy(), xs[-1], atol=1e-5, rtol=0)
     lam = g
-    grads = [None] * K
+    gth = th.grad.cpu().numpy()
     for i in reversed(range(K)):
         mom, gp = orc.backward(xs[i], As_all[i], lam, p.nc, 50)
-        grads[i] = orc.project(mom.reshape(1, -1), p.basis, dtype=np.float64)[0] / K
+        assert_theta_grad_close(gth[i:i + 1], mom, p.basis, scale=1.0 / K)
         lam = gp
-    assert_grad_close(th.grad.cpu().numpy(), np.stack(grads))
 
 
 def _corner_heavy_points(nd, n, seed):
@@ -191,9 +190,9 @@ def test_general_basis_end_to_end(cuda, tess, zb, vp, scale, n):
         assert outside.mean() > 0.01, outside.mean()
         if nd == 3 and not vp:  # some trajectories end beyond a corner of the cube
             assert ((res < 0) | (res > 1)).all(axis=1).sum() > 10
-    ref_out, ref_gth, ref_gp = _oracle_grid(T, theta, pts, g)
+    ref_out, ref_m, ref_gp = _oracle_grid(T, theta, pts, g)
     np.testing.assert_allclose(res, ref_out, atol=1e-5, rtol=0)
-    assert_grad_close(th.grad.cpu().numpy(), ref_gth)
+    assert_theta_grad_close(th.grad.cpu().numpy(), ref_m, T.params.basis)
     np.testing.assert_allclose(x.grad.cpu().numpy(), ref_gp, rtol=1e-5,
                                atol=1e-6 * np.abs(ref_gp).max())
 
@@ -237,8 +236,8 @@ def test_stn_cpabwarp_style_composition(cuda):
     lam = (2 * g[:, ::-1]).astype(np.float32)  # d out / d x2 through the flip and scale
     m1, lam1 = orc.backward(x1, A1, lam, p.nc, 50)
     m2, _ = orc.backward(x0, A2, lam1, p.nc, 50)
-    assert_grad_close(th1.grad.cpu().numpy(), orc.project(m1.reshape(B, -1), p.basis, dtype=np.float64))
-    assert_grad_close(th2.grad.cpu().numpy(), orc.project(m2.reshape(B, -1), p.basis, dtype=np.float64))
+    assert_theta_grad_close(th1.grad.cpu().numpy(), m1, p.basis)
+    assert_theta_grad_close(th2.grad.cpu().numpy(), m2, p.basis)
 
 
 def test_runs_on_current_stream(cuda):

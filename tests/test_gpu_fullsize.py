@@ -10,7 +10,7 @@ from scipy.ndimage import gaussian_filter
 
 from oracle import oracle as orc
 
-from helpers import assert_grad_close, cpab_for, seeded_theta
+from helpers import assert_theta_grad_close, cpab_for, seeded_theta
 
 pytestmark = pytest.mark.gpu
 
@@ -58,8 +58,7 @@ def test_transform_grid_full_size(cuda, cfg):
     np.testing.assert_array_equal(out_np, ref)
     g = _mse_grad(out_np, target.cpu().numpy())
     mom, _ = orc.backward(pts, As, g, p.nc, 50)
-    ref_gth = orc.project(mom.reshape(16, -1), p.basis, dtype=np.float64)
-    assert_grad_close(th.grad.cpu().numpy(), ref_gth)
+    assert_theta_grad_close(th.grad.cpu().numpy(), mom, p.basis)
 
 
 @pytest.mark.parametrize("cfg", ["c3", "c4"])
@@ -86,8 +85,7 @@ def test_transform_data_full_size(cuda, cfg):
     gimg = _mse_grad(out_np, target)
     gg, _ = orc.interp_backward(nd, data, grid_t, size, gimg, want_data=False)
     mom, _ = orc.backward(grid, As, gg, p.nc, 50)
-    ref_gth = orc.project(mom.reshape(B, -1), p.basis, dtype=np.float64)
-    assert_grad_close(th.grad.cpu().numpy(), ref_gth)
+    assert_theta_grad_close(th.grad.cpu().numpy(), mom, p.basis)
 
 
 def test_transform_grid_chain_full_size(cuda):
@@ -113,8 +111,7 @@ def test_transform_grid_chain_full_size(cuda):
     out_np = out.detach().cpu().numpy()
     np.testing.assert_array_equal(out_np, xs[-1])
     lam = _mse_grad(out_np, target.cpu().numpy())
-    grads = [None] * K
+    gch = ch.grad.cpu().numpy()
     for i in reversed(range(K)):
         mom, lam = orc.backward(xs[i], As_all[i], lam, p.nc, 50)
-        grads[i] = orc.project(mom.reshape(1, -1), p.basis, dtype=np.float64)[0] / K
-    assert_grad_close(ch.grad.cpu().numpy(), np.stack(grads))
+        assert_theta_grad_close(gch[i:i + 1], mom, p.basis, scale=1.0 / K)
