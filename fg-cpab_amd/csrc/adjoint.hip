@@ -73,6 +73,13 @@ template <> __device__ __forceinline__ int lookup<2>(const float (&p)[2], const 
 template <> __device__ __forceinline__ int lookup<3>(const float (&p)[3], const Cells& g) {
   return cell_3d(p[0], p[1], p[2], g.nx, g.ny, g.nz);
 }
+// 2D: the inside rule only, for waves whose trajectories stay in
+// (0, kClampHi]^2 (other dimensions: the full lookup).
+template <int D>
+__device__ __forceinline__ int lookup_inside(const float (&p)[D], const Cells& g) {
+  if constexpr (D == 2) return key_cell(cell_key_2d_inside(p[0], p[1], g.nx, g.ny));
+  else return lookup<D>(p, g);
+}
 
 template <int D> struct Fetch;
 template <> struct Fetch<1> {
@@ -508,11 +515,14 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
 // the cells and phase 2 recovers each position from the next through the
 // cell's inverse map (a few ulp per step; the positions only feed the sums
 // S, the cells stay exact).  With adaptive substeps (Heun on crossings) the
-// positions are kept in registers instead.
+// positions are kept in registers instead.  delta (2D without adaptive
+// substeps, else +inf): the row's domain-edge bound for TS replay steps; a wave
+// whose lanes all start at least that far from every edge replays without the
+// lookup's per-step edge test (the same cells).
 template <int D, bool ADAPTIVE, int BINS, int TS, typename P, typename PG, typename IO>
 __device__ __forceinline__ void register_body(P tab, PG gtab, int nP,
                                               const Cells& g, const IO& io, float* bins,
-                                              int* keys, float* __restrict__ mom_b) {
+                                              int* keys, float* __restrict__ mom_b, float delta) {
   constexpr int PP = Dim<D>::P;
   // A trajectory's last flush has all 64 lanes of every wave adding to
   // scattered bins at the same moment, a burst the LDS atomic pipe drains at
@@ -544,30 +554,44 @@ __device__ __forceinline__ void register_body(P tab, PG gtab, int nP,
     // at steps where some lane of the wave changed cell.
     float traj[TS][D];
     uint32_t cells[(TS + 1) / 2];
-    int cur = lookup<D>(p, g);
-    Aff<D> A = fetch<D>(tab, cur);
+    auto phase1 = [&](auto inside) {
+      constexpr bool kInside = decltype(inside)::value;
+      auto look = [&]() {
+        if constexpr (kInside) return lookup_inside<D>(p, g);
+        else return lookup<D>(p, g);
+      };
+      int cur = look();
+      Aff<D> A = fetch<D>(tab, cur);
 #pragma unroll
-    for (int t = 0; t < TS; ++t) {
-      if constexpr (kSpread) {
+      for (int t = 0; t < TS; ++t) {
+        if constexpr (kSpread) {
 #pragma unroll
-        for (int k = 0; k < PP; ++k) {
-          if (t == (k * TS) / PP && pend_on)
-            __hip_atomic_fetch_add(bins + PP * pend_c + k, pend[k], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+          for (int k = 0; k < PP; ++k) {
+            if (t == (k * TS) / PP && pend_on)
+              __hip_atomic_fetch_add(bins + PP * pend_c + k, pend[k], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
         }
-      }
-      const int c = (t == 0) ? cur : lookup<D>(p, g);
-      // Divergent branch, skipped (exec = 0) when no lane changed cell; marked
-      // unlikely so that the no-change case falls through.
-      if (__builtin_expect(c != cur, 0)) A = fetch<D>(tab, c);
-      cur = c;
-      if (t & 1) cells[t >> 1] |= (uint32_t)c << 16;
-      else cells[t >> 1] = (uint32_t)c;
-      if (ADAPTIVE) {
+        const int c = (t == 0) ? cur : look();
+        // Divergent branch, skipped (exec = 0) when no lane changed cell; marked
+        // unlikely so that the no-change case falls through.
+        if (__builtin_expect(c != cur, 0)) A = fetch<D>(tab, c);
+        cur = c;
+        if (t & 1) cells[t >> 1] |= (uint32_t)c << 16;
+        else cells[t >> 1] = (uint32_t)c;
+        if (ADAPTIVE) {
 #pragma unroll
-        for (int k = 0; k < D; ++k) traj[t][k] = p[k];
+          for (int k = 0; k < D; ++k) traj[t][k] = p[k];
+        }
+        replay_step_with<D, ADAPTIVE>(tab, A, c, p, h, hh, g);
       }
-      replay_step_with<D, ADAPTIVE>(tab, A, c, p, h, hh, g);
+    };
+    if constexpr (D == 2 && !ADAPTIVE) {
+      const float x0[1] = {p[0]}, y0[1] = {p[1]};
+      if (edge_safe(x0, y0, delta)) phase1(std::integral_constant<bool, true>{});
+      else phase1(std::integral_constant<bool, false>{});
+    } else {
+      phase1(std::integral_constant<bool, false>{});
     }
 
     // Phase 2: reverse sweep.  A cell change is handled at the end of the
@@ -733,13 +757,39 @@ struct Recover {
   const float* __restrict__ amp;  // [rows, namp]
   int namp;
   float amp_max;
+  // 2D, may be null: [rows, namp] parts of the rows' domain-edge bounds of the
+  // replay maps (adjoint_table_kernel).
+  const EdgeAcc* __restrict__ edge;
 };
+
+// delta_T of a row from its namp bound parts (cpab_device.hpp, edge_delta_2d),
+// the same value in every lane of the wave.
+__device__ __forceinline__ float row_edge_delta(const EdgeAcc* __restrict__ parts, int namp, int T,
+                                                int nx, int ny) {
+  EdgeAcc acc;
+  acc.init();
+  for (int i = __lane_id(); i < namp; i += 64) acc.merge(parts[i]);
+  acc.wave_merge();
+  const float d = edge_delta_2d(acc, T, nx, ny);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, d)));
+}
+
+// The row's domain-edge bound for the register variant's replay (2D without
+// adaptive substeps and with bound parts), else +inf.  Called before the
+// stage's tables are staged, so that its loads overlap theirs.
+template <int D, bool ADAPTIVE, int TS>
+__device__ __forceinline__ float stage_delta(const Recover& rec, size_t row, const Cells& g) {
+  if constexpr (D == 2 && !ADAPTIVE && TS > 0) {
+    if (rec.edge) return row_edge_delta(rec.edge + row * rec.namp, rec.namp, TS, g.nx, g.ny);
+  }
+  return INFINITY;
+}
 
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS, typename IO>
 __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, const float* Ag,
                                           const float* Gg, int nP, int T, const Cells& g,
                                           const IO& io, float* __restrict__ mom_b,
-                                          const Recover& rec, size_t row) {
+                                          const Recover& rec, size_t row, float delta) {
   if constexpr (TS > 0) {
     if constexpr (!ADAPTIVE) {
       // Rows whose inverse maps could amplify the recovered positions' rounding
@@ -752,9 +802,9 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
       }
     }
     if constexpr (BINS == kBinsFullRev)
-      register_body<D, ADAPTIVE, BINS, TS>(Ag, as_lds(L.ldsG), nP, g, io, L.bins, L.keys, mom_b);
-    else if (LDS_A) register_body<D, ADAPTIVE, BINS, TS>(as_lds(L.ldsA), Gg, nP, g, io, L.bins, L.keys, mom_b);
-    else register_body<D, ADAPTIVE, BINS, TS>(Ag, Gg, nP, g, io, L.bins, L.keys, mom_b);
+      register_body<D, ADAPTIVE, BINS, TS>(Ag, as_lds(L.ldsG), nP, g, io, L.bins, L.keys, mom_b, delta);
+    else if (LDS_A) register_body<D, ADAPTIVE, BINS, TS>(as_lds(L.ldsA), Gg, nP, g, io, L.bins, L.keys, mom_b, delta);
+    else register_body<D, ADAPTIVE, BINS, TS>(Ag, Gg, nP, g, io, L.bins, L.keys, mom_b, delta);
   } else {
     if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(L.ldsA), Gg, nP, T, g, io, L.bins, L.keys, mom_b);
     else segmented_body<D, ADAPTIVE, BINS>(Ag, Gg, nP, T, g, io, L.bins, L.keys, mom_b);
@@ -807,8 +857,10 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void backward_kerne
     io.gout = k == K - 1 ? grad_out + (size_t)b * plane : lam + (size_t)b * plane;
     io.lam_out = k == 0 ? (grad_points ? grad_points + (size_t)b * plane : nullptr)
                         : lam + (size_t)b * plane;
+    const float delta = stage_delta<D, ADAPTIVE, TS>(rec, row, g);
     L.begin(Ag, Gg, R, nC * RevStride<D>::S, &touched_cnt);
-    run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, nP, T, g, io, moments + row * R, rec, row);
+    run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, nP, T, g, io, moments + row * R, rec, row,
+                                            delta);
     // Every lane is done with this stage's tables before they are written out
     // (and, for the next stage, overwritten).
     const size_t part = row * gridDim.x + w.part;
@@ -845,9 +897,10 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
   io.gout = grad_out + (size_t)b * s.C * s.nP;
   io.data = data + (size_t)b * s.C * s.plane_in;
   io.gdata = grad_data ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
+  const float delta = stage_delta<D, ADAPTIVE, TS>(rec, (size_t)b, g);
   L.begin(Ag, Gg, R, nC * RevStride<D>::S, &touched_cnt);
   run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, s.nP, T, g, io, moments + (size_t)b * R, rec,
-                                          (size_t)b);
+                                          (size_t)b, delta);
   const size_t part = (size_t)b * gridDim.x + w.part;
   L.end(partials + part * R, dense_parts + (size_t)b * ((gridDim.x + 63) / 64), w.part,
         moments + (size_t)b * R, nC, &touched_cnt);
@@ -877,6 +930,7 @@ struct BackwardJob {
   int64_t nP, n_batch;
   int batched, T, K;
   const float *points, *stage_points, *As, *G, *amp, *grad_out;
+  const EdgeAcc* edge;
   float *moments, *partials, *lam, *grad_points;
   uint64_t* dense_parts;
   const ImageShape* image;
@@ -889,7 +943,7 @@ hipError_t go(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
   const size_t lds = stage_lds_bytes<D, LDS_A, BINS>(j.geo.nC);
   const Cells g{j.geo.nx, j.geo.ny, j.geo.nz};
   const Recover rec{j.amp, adjoint_table_blocks(j.geo.nC),
-                    (float)std::pow((double)kRecoverGrowth, 1.0 / (double)j.T)};
+                    (float)std::pow((double)kRecoverGrowth, 1.0 / (double)j.T), j.edge};
   const dim3 grid((unsigned)cfg.chunks, (unsigned)j.n_batch), block((unsigned)cfg.block);
   if (j.image) {
     auto kernel = image_backward_kernel<D, ADAPTIVE, LDS_A, BINS, TS>;
@@ -960,10 +1014,11 @@ hipError_t dispatch_any(const BackwardJob& j, int adaptive, const LaunchCfg& cfg
 hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
                            int K, int adaptive, const float* points, const float* stage_points,
                            const float* As, const float* G, const float* amp,
-                           const float* grad_out, float* moments,
+                           const EdgeAcc* edge, const float* grad_out, float* moments,
                            float* partials, uint64_t* dense_parts, float* lam, float* grad_points,
                            const LaunchCfg& cfg, hipStream_t s) {
   BackwardJob j{};
+  j.edge = edge;
   j.geo = g;
   j.nP = nP;
   j.n_batch = n_batch;
@@ -987,11 +1042,13 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
 hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
                                  int adaptive, const float* axes, const float* final_points,
                                  const float* seed_grad,
-                                 const float* As, const float* G, const float* amp, const float* data,
+                                 const float* As, const float* G, const float* amp,
+                                 const EdgeAcc* edge, const float* data,
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
                                  hipStream_t s) {
   BackwardJob j{};
+  j.edge = edge;
   j.geo = g;
   j.nP = img.nP;
   j.n_batch = n_batch;

@@ -125,14 +125,17 @@ __global__ __launch_bounds__(kProjThreads) void project_kernel(
 // ||M_c||_2 of the inverse maps (inverse_map_norm) goes to amp[blockIdx.x]:
 // the backward reads a row's nblk entries to bound how much the recovered
 // positions' rounding can grow.  Thread i of the grid also clears
-// dense_parts[i] for i < n_words.
+// dense_parts[i] for i < n_words.  2D, ebound not null: the block's part of
+// the domain-edge bound of the replay's explicit-midpoint maps
+// (cpab_device.hpp, edge_bound_cell_2d) goes to ebound[blockIdx.x] (alpha,
+// beta, reach, err); the backward merges a row's nblk parts into its delta_T.
 constexpr int kTableThreads = 256;
 
 template <int D>
 __global__ __launch_bounds__(kTableThreads) void adjoint_table_kernel(
-    int64_t rows, int nC, int nblk, float h, const float* __restrict__ As, float* __restrict__ G,
-    float* __restrict__ moments, float* __restrict__ amp, uint64_t* __restrict__ dense_parts,
-    int64_t n_words) {
+    int64_t rows, int nC, int nblk, float h, int nx, int ny, const float* __restrict__ As,
+    float* __restrict__ G, float* __restrict__ moments, float* __restrict__ amp,
+    EdgeAcc* __restrict__ ebound, uint64_t* __restrict__ dense_parts, int64_t n_words) {
   constexpr int P = D * (D + 1);
   constexpr int S = RevStride<D>::S;
   // Entry layout (cpab_device.hpp, RevStride): G at G0, the inverse map's
@@ -140,6 +143,10 @@ __global__ __launch_bounds__(kTableThreads) void adjoint_table_kernel(
   constexpr int G0 = D == 3 ? 12 : 0;
   constexpr int I0 = D == 3 ? 0 : D * D;
   __shared__ float wave_max[kTableThreads / 64];
+  __shared__ EdgeAcc wave_edge[kTableThreads / 64];
+  const bool edges = D == 2 && ebound != nullptr;
+  EdgeAcc edge;
+  edge.init();
   const int64_t lin = blockIdx.x * (int64_t)kTableThreads + threadIdx.x;
   if (lin < n_words) dense_parts[lin] = 0;
   const int64_t row = blockIdx.x / nblk;
@@ -153,6 +160,11 @@ __global__ __launch_bounds__(kTableThreads) void adjoint_table_kernel(
 #pragma unroll
     for (int k = 0; k < P; ++k) a[k] = As[i * P + k];
     adjoint_increment<D>(a, h, (h * 0.5f) * h, e + G0);
+    if (D == 2 && edges) {
+      double mm[2][3];
+      midpoint_map_2d(a, h, mm);
+      edge_bound_cell_2d(mm, c, nx, ny, midpoint_step_err(a, h, h * 0.5f), edge);
+    }
     inverse_step_map<D>(a, h, inv);
     norm = inverse_map_norm<D>(inv);
 #pragma unroll
@@ -164,13 +176,23 @@ __global__ __launch_bounds__(kTableThreads) void adjoint_table_kernel(
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) norm = fmaxf(norm, __shfl_xor(norm, off));
-  if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = norm;
+  if (edges) edge.wave_merge();
+  if ((threadIdx.x & 63) == 0) {
+    wave_max[threadIdx.x >> 6] = norm;
+    if (edges) wave_edge[threadIdx.x >> 6] = edge;
+  }
   __syncthreads();
   if (threadIdx.x == 0 && row < rows) {
     float m = wave_max[0];
 #pragma unroll
     for (int w = 1; w < kTableThreads / 64; ++w) m = fmaxf(m, wave_max[w]);
     amp[blockIdx.x] = m;
+    if (edges) {
+      EdgeAcc acc = wave_edge[0];
+#pragma unroll
+      for (int w = 1; w < kTableThreads / 64; ++w) acc.merge(wave_edge[w]);
+      ebound[blockIdx.x] = acc;
+    }
   }
 }
 
@@ -542,8 +564,9 @@ hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
 
 int adjoint_table_blocks(int nC) { return (nC + kTableThreads - 1) / kTableThreads; }
 
-hipError_t launch_adjoint_table(int ndim, int64_t rows, int nC, int T, const float* As, float* G,
-                                float* moments, float* amp, uint64_t* dense_parts, int64_t n_words,
+hipError_t launch_adjoint_table(int ndim, int64_t rows, int nx, int ny, int nC, int T,
+                                const float* As, float* G, float* moments, float* amp,
+                                EdgeAcc* ebound, uint64_t* dense_parts, int64_t n_words,
                                 hipStream_t s) {
   if (rows <= 0 || nC <= 0) return hipSuccess;
   const float h = 1.0f / (float)T;
@@ -552,8 +575,8 @@ hipError_t launch_adjoint_table(int ndim, int64_t rows, int nC, int T, const flo
   const int64_t blocks = std::max<int64_t>(rows * nblk, (n_words + kTableThreads - 1) / kTableThreads);
   const dim3 g((unsigned)blocks), b(kTableThreads);
   auto go = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, g, b, 0, s, rows, nC, nblk, h, As, G, moments, amp, dense_parts,
-                       n_words);
+    hipLaunchKernelGGL(kernel, g, b, 0, s, rows, nC, nblk, h, nx, ny, As, G, moments, amp,
+                       ndim == 2 ? ebound : nullptr, dense_parts, n_words);
   };
   if (ndim == 1) go(adjoint_table_kernel<1>);
   else if (ndim == 2) go(adjoint_table_kernel<2>);

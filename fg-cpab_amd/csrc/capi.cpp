@@ -291,10 +291,11 @@ int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 // dense-part masks [rows, ceil(chunks/64)] and the partial tables
 // [rows, chunks, nC, ppc]; then the inter-stage adjoint [n_batch, ndim, nP]
 // (K > 1), the reverse-sweep table [rows, nC, 4|12|24] (G and the inverse
-// one-step map per cell, cpab_device.hpp RevStride) and the per-block norms of
-// the inverse maps [rows, adjoint_table_blocks(nC)].
+// one-step map per cell, cpab_device.hpp RevStride), the per-block norms of
+// the inverse maps [rows, adjoint_table_blocks(nC)] and (2D) the per-block
+// parts of the rows' domain-edge bounds [rows, adjoint_table_blocks(nC)].
 struct BackwardWorkspace {
-  int64_t dense_words, partials_offset, lam_offset, g_offset, amp_offset, total;
+  int64_t dense_words, partials_offset, lam_offset, g_offset, amp_offset, edge_offset, total;
 };
 
 
@@ -307,7 +308,9 @@ BackwardWorkspace backward_workspace(const cpab::Geometry& g, int64_t nP, int64_
   w.lam_offset = align_up(w.partials_offset + parts * g.nC * g.ppc() * 4);
   w.g_offset = K > 1 ? align_up(w.lam_offset + n_batch * g.ndim * nP * 4) : w.lam_offset;
   w.amp_offset = align_up(w.g_offset + (int64_t)K * n_batch * g.nC * adj_stride(g.ndim) * 4);
-  w.total = w.amp_offset + (int64_t)K * n_batch * cpab::adjoint_table_blocks(g.nC) * 4;
+  const int64_t blocks = (int64_t)K * n_batch * cpab::adjoint_table_blocks(g.nC);
+  w.edge_offset = align_up(w.amp_offset + blocks * 4);
+  w.total = w.edge_offset + (g.ndim == 2 ? blocks * cpab::kEdgeAccBytes : 0);
   return w;
 }
 
@@ -402,15 +405,22 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   float* lam = K > 1 ? reinterpret_cast<float*>(ws + w.lam_offset) : nullptr;
   float* G = reinterpret_cast<float*>(ws + w.g_offset);
   float* amp = reinterpret_cast<float*>(ws + w.amp_offset);
-  // G table and inverse-map norms; the HBM sums and dense-part masks cleared.
-  rc = check_hip(cpab::launch_adjoint_table(ndim, rows, g.nC, nstepsolver, As, G, moments, amp,
-                                            dense, w.dense_words, s),
+  // The domain-edge bound lets the replay of waves that stay inside the domain
+  // skip the lookup's edge test.  Not for chains: each stage would pay the
+  // bound's reduction, and a chain's slowest waves (those on the domain's
+  // edge, which never qualify) set its time (C5 backward 174 -> 185 us).
+  cpab::EdgeAcc* edge =
+      ndim == 2 && K == 1 ? reinterpret_cast<cpab::EdgeAcc*>(ws + w.edge_offset) : nullptr;
+  // G table, inverse-map norms and domain-edge bound parts; the HBM sums and
+  // dense-part masks cleared.
+  rc = check_hip(cpab::launch_adjoint_table(ndim, rows, g.nx, g.ny, g.nC, nstepsolver, As, G,
+                                            moments, amp, edge, dense, w.dense_words, s),
                  who);
   if (rc) return rc;
   hipEvent_t ev = nullptr;
   const bool timed = timing && prof_begin(s, &ev);
   rc = check_hip(cpab::launch_backward(g, nP, n_batch, batched ? 1 : 0, nstepsolver, K, adaptive,
-                                       points, stage_points, As, G, amp, grad_out, moments,
+                                       points, stage_points, As, G, amp, edge, grad_out, moments,
                                        partials, dense, lam, grad_points, cfg, s),
                  who);
   prof_end(timed, ev, "backward", s);
@@ -742,8 +752,9 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   float* partials = reinterpret_cast<float*>(ws + w.partials_offset);
   float* G = reinterpret_cast<float*>(ws + w.g_offset);
   float* amp = reinterpret_cast<float*>(ws + w.amp_offset);
-  rc = check_hip(cpab::launch_adjoint_table(ndim, n_batch, g.nC, nstepsolver, As, G, moments, amp,
-                                            dense, w.dense_words, s),
+  cpab::EdgeAcc* edge = ndim == 2 ? reinterpret_cast<cpab::EdgeAcc*>(ws + w.edge_offset) : nullptr;
+  rc = check_hip(cpab::launch_adjoint_table(ndim, n_batch, g.nx, g.ny, g.nC, nstepsolver, As, G,
+                                            moments, amp, edge, dense, w.dense_words, s),
                  "cpab_transform_data_backward");
   if (rc) return rc;
   if (grad_data) {
@@ -754,8 +765,8 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   hipEvent_t ev = nullptr;
   const bool timed = prof_begin(s, &ev);
   rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, axes,
-                                             final_points, seed_grad, As, G, amp, data, grad_out,
-                                             moments, partials, dense, grad_data, cfg, s),
+                                             final_points, seed_grad, As, G, amp, edge, data,
+                                             grad_out, moments, partials, dense, grad_data, cfg, s),
                  "cpab_transform_data_backward");
   prof_end(timed, ev, "image_backward", s);
   if (rc) return rc;

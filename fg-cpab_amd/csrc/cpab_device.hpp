@@ -186,6 +186,211 @@ __device__ __forceinline__ int cell_2d(float px, float py, int nx, int ny) {
   return key_cell(cell_key_2d(px, py, nx, ny));
 }
 
+// The inside rule alone: the key cell_key_2d returns for a wave whose lanes
+// all lie in (0, kClampHi]^2, without the per-step domain-edge test.  Used by
+// waves that edge_safe (below) has shown stay there for the whole trajectory.
+__device__ __forceinline__ CellKey cell_key_2d_inside(float px, float py, int nx, int ny) {
+  const float fx = (float)nx, fy = (float)ny;
+  const float sx = __builtin_floorf(px * fx), sy = __builtin_floorf(py * fy);
+  const float lx = fmaf(px, fx, -sx), ly = fmaf(py, fy, -sy);
+  return {fmaf(sy, fx, sx), __builtin_amdgcn_ballot_w64(lx < ly),
+          __builtin_amdgcn_ballot_w64((1.0f - lx) < ly)};
+}
+
+// ---------------------------------------------------------------------------
+// Domain-edge bound of a theta row's replay maps (2D).
+//
+// cell_key_2d spends 4 VALU operations and a branch per step on the test
+// whether some lane lies outside (0, kClampHi]^2.  The test can be skipped for
+// a trajectory that provably stays inside.  For each edge e of the domain
+// (left: d = x, right: d = 1 - x, bottom: y, top: 1 - y), with d' the distance
+// after one computed step:
+//   - over the cells a point at d < r_lo = 1/(2n) can lie in (the triangles
+//     with a vertex closer than r_lo), d' >= alpha d - beta;
+//   - over all cells, d' >= d - reach;
+// both up to the computed step's rounding err.  The exact step map is affine
+// in each cell, so both hold on a triangle where they hold at its three
+// vertices; they are widened by kEdgeEta times the map's slope for points the
+// lookup assigns to a cell from just outside it (the rounded cell coordinates
+// misplace a point by a few 2^-24 at most).  With m = min(alpha, 1) > 0,
+// b = beta + err and thr = 2^-23, a point with d >= delta_k =
+// (thr + (k - 1) b) / m^(k-1) stays at d > thr for k steps: a step takes
+// d in [delta_k, r_lo) to alpha d - b >= delta_{k-1}, and d >= r_lo to
+// d - reach - err >= delta_{k-1}, provided delta_T < r_lo and
+// delta_T + reach + err <= r_lo.  d > thr on all four edges puts the point in
+// (0, kClampHi]^2.  So a wave whose lanes all start at distance >= the row's
+// delta_T from every edge takes the inside rule at each of its T steps: the
+// same cells, bit for bit, without the test.
+//
+// adjoint_table_kernel evaluates this in double from the fp32 fields for the
+// backward replay's explicit-midpoint maps, per block of cells; the backward
+// merges a row's blocks and forms delta_T (rounded up); rows whose maps are
+// not finite, or push points toward an edge too fast, get +inf (never skip).
+// ---------------------------------------------------------------------------
+
+// Largest distance (domain units) between a point and the triangle the lookup
+// assigns it to: floor(x n) and the local coordinates are each rounded once
+// (about 4 * 2^-24 in all); 2^-20 leaves a wide margin.
+constexpr double kEdgeEta = 9.5367431640625e-07;  // 2^-20
+constexpr double kUlp = 5.9604644775390625e-08;    // 2^-24, fp32 unit roundoff
+
+// Over a row's cells and the four edges: the smallest alpha, the largest
+// beta, reach and rounding bound (delta_T needs no more: it grows as alpha
+// falls and as the others grow).
+struct EdgeAcc {
+  double alpha, beta, reach, err;
+  __device__ __forceinline__ void init() {
+    alpha = INFINITY;
+    beta = reach = err = 0.0;
+  }
+  __device__ __forceinline__ void merge(const EdgeAcc& o) {
+    alpha = fmin(alpha, o.alpha);
+    beta = fmax(beta, o.beta);
+    reach = fmax(reach, o.reach);
+    err = fmax(err, o.err);
+  }
+  // All 64 lanes of the wave end with the wave's merged value.
+  __device__ __forceinline__ void wave_merge() {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      EdgeAcc o;
+      o.alpha = __shfl_xor(alpha, off);
+      o.beta = __shfl_xor(beta, off);
+      o.reach = __shfl_xor(reach, off);
+      o.err = __shfl_xor(err, off);
+      merge(o);
+    }
+  }
+};
+
+// Rounding bound of one computed explicit-midpoint replay step with the cell's
+// velocity field a (row-major 2x3): v = A [p; 1], p_mid = p + hh v,
+// v_mid = A [p_mid; 1], p' = p + h v_mid, each rounded, for |x|, |y| <= 1.
+__device__ __forceinline__ double midpoint_step_err(const float* a, double h, double hh) {
+  double S = 0.0;
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+    S = fmax(S, fabs((double)a[3 * r]) + fabs((double)a[3 * r + 1]) + fabs((double)a[3 * r + 2]));
+  const double dv = 2.02 * kUlp * S;                   // v
+  const double pm = 1.0 + hh * S;                      // |p_mid| bound
+  const double dpm = hh * dv + 1.01 * kUlp * pm;       // p_mid
+  const double dvm = 2.02 * kUlp * S * pm + S * dpm;   // v_mid
+  return 1.05 * (h * dvm + 1.01 * kUlp * (1.0 + h * S * pm));  // p'
+}
+
+// The replay step of field a as an exact affine map of p:
+// [I + h A + h hh A^2 | h b + h hh A b] (float h and hh as the replay uses them).
+__device__ __forceinline__ void midpoint_map_2d(const float* a, float h, double (&m)[2][3]) {
+  const double hd = h, h2 = (double)h * (double)(h * 0.5f);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const double ab = (double)a[3 * i] * a[2] + (double)a[3 * i + 1] * a[5];
+    m[i][2] = hd * a[3 * i + 2] + h2 * ab;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const double sq = (double)a[3 * i] * a[j] + (double)a[3 * i + 1] * a[3 + j];
+      m[i][j] = (i == j ? 1.0 : 0.0) + hd * a[3 * i + j] + h2 * sq;
+    }
+  }
+}
+
+// Adds cell c (triangle t of square (cx, cy), c = 4 (cx + cy nx) + t) whose one
+// step is p' = m [p; 1] in exact arithmetic, computed with rounding error at
+// most err per coordinate, for each of the four edges.  A non-finite map or
+// err makes the row unusable (alpha = -inf).
+__device__ __forceinline__ void edge_bound_cell_2d(const double (&m)[2][3], int c, int nx, int ny,
+                                                   double err, EdgeAcc& acc) {
+  const int sq = c >> 2, t = c & 3;
+  const int cy = sq / nx, cx = sq - cy * nx;
+  const double x0 = (double)cx / nx, x1 = (double)(cx + 1) / nx;
+  const double y0 = (double)cy / ny, y1 = (double)(cy + 1) / ny;
+  const double xc = 0.5 * (x0 + x1), yc = 0.5 * (y0 + y1);
+  // t: 0 bottom, 1 right, 2 top, 3 left (cpab_ops_2d.cu:119-127); the
+  // square's centre is every triangle's third vertex.
+  const double vx[3] = {t == 1 ? x1 : x0, t == 3 ? x0 : x1, xc};
+  const double vy[3] = {t == 2 ? y1 : y0, t == 0 ? y0 : y1, yc};
+  bool finite = isfinite(err);
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) finite = finite && isfinite(m[a][j]);
+  if (!finite) {
+    acc.alpha = -INFINITY;
+    return;
+  }
+  acc.err = fmax(acc.err, err);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int ax = e >> 1;
+    const bool far_side = e & 1;
+    const double rlo = 0.5 / (ax ? ny : nx);
+    double d[3], dp[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const double pos = ax ? vy[k] : vx[k];
+      const double img = m[ax][0] * vx[k] + m[ax][1] * vy[k] + m[ax][2];
+      d[k] = far_side ? 1.0 - pos : pos;
+      dp[k] = far_side ? 1.0 - img : img;
+    }
+    const double dmin = fmin(fmin(d[0], d[1]), d[2]);
+    const double slope = fabs(m[ax][0]) + fabs(m[ax][1]);
+    double approach = 0.0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) approach = fmax(approach, d[k] - dp[k]);
+    acc.reach = fmax(acc.reach, approach + (slope + 1.0) * kEdgeEta);
+    if (dmin < rlo) {
+      double bv = 0.0;
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+        if (d[k] == 0.0) bv = fmax(bv, -dp[k]);
+      double al = INFINITY;
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+        if (d[k] > 0.0) al = fmin(al, (dp[k] + bv) / d[k]);
+      acc.alpha = fmin(acc.alpha, al);
+      acc.beta = fmax(acc.beta, bv + (slope + fmax(fabs(al), 1.0)) * kEdgeEta);
+    }
+  }
+}
+
+// x^n for n >= 0 by square and multiply (a fixed sequence of double products).
+__device__ __forceinline__ double pow_int(double x, int n) {
+  double r = 1.0;
+  while (n > 0) {
+    if (n & 1) r *= x;
+    x *= x;
+    n >>= 1;
+  }
+  return r;
+}
+
+// delta_T of a row from its merged accumulator, rounded up to float; +inf when
+// the row allows no bound.
+__device__ __forceinline__ float edge_delta_2d(const EdgeAcc& acc, int T, int nx, int ny) {
+  // alpha > 0 fails for NaN and for an unusable row (-inf)
+  const double U =
+      acc.alpha > 0.0 ? pow_int(1.0 / fmin(acc.alpha, 1.0), T - 1) * (1.0 + 1e-12) : INFINITY;
+  const double E = acc.err;
+  const double delta = U * (1.1920928955078125e-07 + (double)(T - 1) * (acc.beta + E)) * (1.0 + 1e-12);
+  const double rlo = 0.5 / (double)max(nx, ny);
+  const bool ok = T >= 1 && delta < rlo && (delta + acc.reach + E) * (1.0 + 1e-12) <= rlo;
+  return ok ? __double2float_ru(delta) : INFINITY;
+}
+
+// Whether every lane of the wave starts at distance >= delta from each domain
+// edge (so that its next T steps stay in (0, kClampHi]^2, delta being the
+// row's delta_T); NaN coordinates fail.
+template <int N>
+__device__ __forceinline__ bool edge_safe(const float (&x)[N], const float (&y)[N], float delta) {
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const float d = fminf(fminf(x[k], 1.0f - x[k]), fminf(y[k], 1.0f - y[k]));
+    ok = ok && x[k] == x[k] && y[k] == y[k] && d >= delta;
+  }
+  return __builtin_amdgcn_ballot_w64(!ok) == 0;
+}
+
 // Issue priority of a wave from its lanes' positions at the start of a
 // trajectory: lanes on or beyond the domain's edge take the lookup's clamping
 // path, and beyond a corner the corner rule too, at most steps, so their

@@ -8,6 +8,9 @@
 
 namespace cpab {
 
+struct EdgeAcc;  // cpab_device.hpp: one part of a row's domain-edge bound (4 doubles)
+constexpr int kEdgeAccBytes = 32;
+
 struct Geometry {
   int ndim;
   int nx, ny, nz;   // cells per axis (unused axes = 1)
@@ -50,10 +53,13 @@ hipError_t launch_project(int64_t n_theta, int D, int d, const float* moments,
 // G [rows, nC, RevStride]: per cell h A + (h^2/2) A^2 and the inverse one-step
 // map (cpab_device.hpp), h = 1/T; amp [rows, adjoint_table_blocks(nC)]: the
 // largest ||M_c||_2 of the inverse maps over each block of a row's cells;
+// ebound (2D, may be null) [rows, adjoint_table_blocks(nC)]: each block's part
+// of the row's domain-edge bound of the replay maps (nx, ny: the 2D grid);
 // zeroes moments [rows, nC, ppc] (the HBM sums) and dense_parts [n_words].
 int adjoint_table_blocks(int nC);
-hipError_t launch_adjoint_table(int ndim, int64_t rows, int nC, int T, const float* As, float* G,
-                                float* moments, float* amp, uint64_t* dense_parts, int64_t n_words,
+hipError_t launch_adjoint_table(int ndim, int64_t rows, int nx, int ny, int nC, int T,
+                                const float* As, float* G, float* moments, float* amp,
+                                EdgeAcc* ebound, uint64_t* dense_parts, int64_t n_words,
                                 hipStream_t s);
 // moments [rows, nC, ppc] from the reverse sweep's per-cell sums S, in place:
 // the HBM sums in `moments` plus the partial tables [rows, nparts, nC, ppc] of
@@ -76,8 +82,10 @@ hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, in
                               int adaptive, const float* points, const float* Trels,
                               const float* As, int32_t* cells, hipStream_t s);
 // lam: [n_batch, ndim, nP] scratch carrying the adjoint between stages (K > 1).
-// G, amp: the reverse-sweep table and its per-block norms from
-// launch_adjoint_table, same rows as As.  The register variant recovers
+// G, amp, edge: the reverse-sweep table, its per-block norms and (2D, may be
+// null) the domain-edge bound parts from launch_adjoint_table, same rows as
+// As; with edge, waves whose trajectories provably stay inside the domain
+// replay them without the lookup's per-step edge test.  The register variant recovers
 // positions through the inverse maps only for rows whose amplification bound
 // (max ||M_c||_2)^T stays within kRecoverGrowth; other rows replay from
 // checkpoints.
@@ -88,7 +96,7 @@ hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, in
 hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
                            int K, int adaptive, const float* points, const float* stage_points,
                            const float* As, const float* G, const float* amp,
-                           const float* grad_out, float* moments,
+                           const EdgeAcc* edge, const float* grad_out, float* moments,
                            float* partials, uint64_t* dense_parts, float* lam, float* grad_points,
                            const LaunchCfg& cfg, hipStream_t s);
 
@@ -101,7 +109,8 @@ hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_
 hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
                                  int adaptive, const float* axes, const float* final_points,
                                  const float* seed_grad,
-                                 const float* As, const float* G, const float* amp, const float* data,
+                                 const float* As, const float* G, const float* amp,
+                                 const EdgeAcc* edge, const float* data,
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
                                  hipStream_t s);

@@ -11,6 +11,7 @@ from cpab.pytorch._native import native
 from cpab.pytorch.transformer import basis_tables
 from oracle import oracle as orc
 
+import edge_bound as eb
 from helpers import (assert_adjoint_close, assert_grad_close, cpab_for, edge_lattice, meshgrid,
                      recover_growth, scatter_magnitude, seeded_theta, uniform_points)
 
@@ -225,6 +226,42 @@ def test_backward_parity(cuda, tess, kind, n, adaptive):
     g = np.random.default_rng(62).standard_normal((3, nd, pts.shape[-1])).astype(np.float32)
     As, mom, gp = _backward_case(T, theta, pts, g, cuda, adaptive=adaptive)
     ref_m, ref_gp = orc.backward(pts, As, g, tess, 50, adaptive=bool(adaptive))
+    assert_adjoint_close(gp, ref_gp)
+    assert_grad_close(mom, ref_m, rtol=2e-5)
+
+
+@pytest.mark.parametrize("tess,scale", [([20, 20], 0.5), ([6, 5], 1.0), ([16, 16], 2.0)])
+def test_backward_edge_bound_start_points(cuda, tess, scale):
+    # 2D register backward: a wave whose lanes all start at least the row's
+    # bound delta_T (restated in tests/edge_bound.py) from every edge replays
+    # without the lookup's edge test.  Points at the largest row bound, one
+    # float closer, and 1.01x further, along every edge, in runs of whole waves,
+    # beside uniform points and the edge lattice: moments and point adjoints
+    # against the oracle (a wrong cell at any step would move the adjoint far
+    # outside its tolerance).  At scale 2 some rows have no bound.
+    T = cpab_for(tess)
+    p = T.params
+    nx, ny = p.nc
+    theta = seeded_theta(T, 3, scale, 140)
+    A = orc.affine(theta, p.basis).reshape(3, p.nC, 2, 3)
+    deltas = np.array([eb.midpoint_delta(A[b], 50, nx, ny) for b in range(3)])
+    if scale <= 0.5:
+        assert np.isfinite(deltas).all(), deltas
+    finite = deltas[np.isfinite(deltas)]
+    rng = np.random.default_rng(141)
+    parts = [uniform_points(2, 8192, 142), edge_lattice(tess, 143)]
+    for d in (finite.max(), np.nextafter(np.float32(finite.max()), np.float32(0)),
+              np.float32(1.01) * finite.max()) if finite.size else ():
+        d = np.float32(d)
+        for side in range(4):
+            u = rng.random(256).astype(np.float32)
+            fixed = np.full(256, d if side % 2 == 0 else np.float32(1) - d, np.float32)
+            parts.append(np.stack((fixed, u) if side < 2 else (u, fixed)))
+    pts = np.concatenate(parts, axis=1).astype(np.float32)
+    g = rng.standard_normal((3, 2, pts.shape[1])).astype(np.float32)
+    As, mom, gp = _backward_case(T, theta, pts, g, cuda)
+    np.testing.assert_array_equal(As, A)
+    ref_m, ref_gp = orc.backward(pts, As, g, tess, 50)
     assert_adjoint_close(gp, ref_gp)
     assert_grad_close(mom, ref_m, rtol=2e-5)
 
