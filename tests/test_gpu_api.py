@@ -48,6 +48,28 @@ def test_transform_grid_fwd_bwd(cuda, tess, n, B):
                                atol=1e-6 * np.abs(ref_gp).max())
 
 
+def test_retained_graph_backward_twice(cuda):
+    # A retained graph's backward runs twice on the same saved tensors (the
+    # forward's As and points): both give the oracle's gradient, and the
+    # points' gradient is the same bit for bit.
+    T = cpab_for([20, 20])
+    theta = seeded_theta(T, 4, 0.5, 230)
+    pts = uniform_points(2, 20000, 231)
+    g = np.random.default_rng(232).standard_normal((4, 2, 20000)).astype(np.float32)
+    th = torch.tensor(theta, device=cuda, requires_grad=True)
+    x = torch.tensor(pts, device=cuda, requires_grad=True)
+    out = T.transform_grid(x, th)
+    gt = torch.tensor(g, device=cuda)
+    out.backward(gt, retain_graph=True)
+    g1, x1 = th.grad.clone(), x.grad.clone()
+    th.grad, x.grad = None, None
+    out.backward(gt)
+    _, ref_m, _ = _oracle_grid(T, theta, pts, g)
+    for gth in (g1, th.grad):
+        assert_theta_grad_close(gth.cpu().numpy(), ref_m, T.params.basis)
+    np.testing.assert_array_equal(x1.cpu().numpy(), x.grad.cpu().numpy())
+
+
 def test_transform_grid_mse_loss_c2_shape(cuda):
     # C2's loss: MSE to a second seeded theta's warped points (reduced nP).
     T = cpab_for([20, 20])
