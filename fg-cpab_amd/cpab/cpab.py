@@ -48,6 +48,7 @@ class Cpab(object):
                            / self.params.nc[i] for i in range(self.params.ndim)]
         self.params.nstepsolver = 50
         self.params.adaptive_substeps = False
+        self.params.deterministic_grad = False
 
         self._dir = get_dir(__file__) + '/../basis_files/'
         create_dir(self._dir)
@@ -107,18 +108,28 @@ class Cpab(object):
             self.params.basis_gpu_sparse_t = B.transpose(0, 1).coalesce()
         return B
 
-    def set_solver_params(self, nstepsolver=50, adaptive_substeps=False):
-        """Set parameters controlling the integration algorithm.
+    def set_solver_params(self, nstepsolver=50, adaptive_substeps=False, *,
+                          deterministic_grad=False):
+        """Set parameters controlling the integration algorithm
+        (``cpab/cpab.py:112-129``).
 
         Arguments:
             nstepsolver: int, number of integration steps
             adaptive_substeps: bool, Heun correction when a step crosses a cell
+            deterministic_grad: bool (an addition to the reference's arguments),
+                the GPU backward reduces its per-cell sums in 64-bit integers
+                over two passes, so theta gradients (and the points' gradient)
+                are bit-identical from run to run on one device (the
+                benchmark steps take 1.9-2.9x their default time;
+                transform_data's data gradient keeps its float-atomic scatter)
         """
         assert nstepsolver > 0, 'nstepsolver must be a positive number'
         assert type(nstepsolver) == int, 'nstepsolver must be integer'
         assert type(adaptive_substeps) == bool, 'adaptive_substeps must be bool'
+        assert type(deterministic_grad) == bool, 'deterministic_grad must be bool'
         self.params.nstepsolver = nstepsolver
         self.params.adaptive_substeps = adaptive_substeps
+        self.params.deterministic_grad = deterministic_grad
 
     def uniform_meshgrid(self, n_points):
         """[ndim, prod(n_points)] grid over the domain, coordinate 0 varying fastest."""

@@ -6,6 +6,7 @@ or a call fails, a ``RuntimeError`` carrying the library's own message is
 raised, mirroring the ``RuntimeError`` the reference's TORCH_CHECKs produce
 (``cpab/pytorch/transformer_cuda.cpp:25-27``).
 """
+import contextlib
 import ctypes
 import os
 import threading
@@ -61,6 +62,8 @@ _SIGNATURES = {
     "cpab_sum_batch": (_c_int, [_c_i64, _c_i64, _c_vp, _c_vp, _c_vp]),
     "cpab_interp_forward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                      _c_vp]),
+    "cpab_set_deterministic": (None, [_c_int]),
+    "cpab_deterministic": (_c_int, []),
     "cpab_profile_enable": (None, [_c_int]),
     "cpab_profile_read": (_c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                    ctypes.POINTER(_c_i64)]),
@@ -157,6 +160,19 @@ class Native:
         _check(self.lib.cpab_trace_cells(ndim, nP, n_theta, int(batched), int(T), ncx, ncy, ncz,
                                          int(adaptive), _ptr(points), _ptr(Trels), _ptr(As),
                                          _ptr(cells), _stream(points.device)), "cpab_trace_cells")
+
+    @contextlib.contextmanager
+    def deterministic(self, on):
+        """Within the block, this thread's backward entry points (and their
+        workspace sizes) use the deterministic two-pass reduction when ``on``:
+        bit-identical moments, theta gradients and grad_data from run to run.
+        The previous setting is restored on exit."""
+        prev = int(self.lib.cpab_deterministic())
+        self.lib.cpab_set_deterministic(1 if on else 0)
+        try:
+            yield
+        finally:
+            self.lib.cpab_set_deterministic(prev)
 
     def backward_workspace_size(self, ndim, nP, n_theta, nC):
         return int(self.lib.cpab_backward_workspace_size(ndim, nP, n_theta, nC))

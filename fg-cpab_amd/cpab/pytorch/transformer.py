@@ -81,6 +81,12 @@ def basis_tables(params, device):
     return t
 
 
+def _deterministic(params):
+    """Whether the backward uses the deterministic two-pass reduction
+    (``Cpab.set_solver_params(deterministic_grad=True)``)."""
+    return bool(getattr(params, "deterministic_grad", False))
+
+
 def _check_inputs(points, theta, params):
     if theta.dtype != torch.float32 or points.dtype != torch.float32:
         raise RuntimeError(f"expected float32 tensors, got points {points.dtype}, "
@@ -151,16 +157,17 @@ class _CPABFunction(torch.autograd.Function):
         grad = grad.detach().to(torch.float32).contiguous()
 
         moments = torch.empty((n_theta, nC, ppc), device=dev, dtype=torch.float32)
-        ws_bytes = lib.backward_workspace_size(ndim, nP, n_theta, nC)
-        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
         want_points = ctx.compute_points_grad and ctx.needs_input_grad[0]
         gp = (torch.empty((n_theta, ndim, nP), device=dev, dtype=torch.float32)
               if want_points else None)
         tab = basis_tables(params, dev)
         grad_theta = torch.empty((n_theta, tab["d"]), device=dev, dtype=torch.float32)
-        # moments and their projection dtheta = B^T vec(M) in one launch
-        lib.backward_project(ndim, points, ctx.batched, n_theta, nP, ctx.nstepsolver, ctx.nc,
-                             ctx.adaptive_substeps, As, grad, tab, moments, grad_theta, gp, ws)
+        with lib.deterministic(_deterministic(params)):
+            ws_bytes = lib.backward_workspace_size(ndim, nP, n_theta, nC)
+            ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
+            # moments and their projection dtheta = B^T vec(M) in one launch
+            lib.backward_project(ndim, points, ctx.batched, n_theta, nP, ctx.nstepsolver, ctx.nc,
+                                 ctx.adaptive_substeps, As, grad, tab, moments, grad_theta, gp, ws)
         if want_points and points.dim() == 2:
             summed = torch.empty((ndim, nP), device=dev, dtype=torch.float32)
             lib.sum_batch(gp, summed)
@@ -241,16 +248,17 @@ class _CPABChainFunction(torch.autograd.Function):
         grad = grad.detach().to(torch.float32).contiguous()
 
         moments = torch.empty((K * n_batch, nC, ppc), device=dev, dtype=torch.float32)
-        ws_bytes = lib.chain_backward_workspace_size(ndim, nP, n_batch, K, nC)
-        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
         want_points = ctx.needs_input_grad[0]
         gp = (torch.empty((n_batch, ndim, nP), device=dev, dtype=torch.float32)
               if want_points else None)
         tab = basis_tables(params, dev)
         grad_theta = torch.empty((K * n_batch, tab["d"]), device=dev, dtype=torch.float32)
-        lib.chain_backward(ndim, points, ctx.batched, n_batch, K, nP, ctx.nstepsolver, ctx.nc,
-                           ctx.adaptive_substeps, stage_points, As, grad, moments, gp, ws,
-                           tab=tab, grad_theta=grad_theta)
+        with lib.deterministic(_deterministic(params)):
+            ws_bytes = lib.chain_backward_workspace_size(ndim, nP, n_batch, K, nC)
+            ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
+            lib.chain_backward(ndim, points, ctx.batched, n_batch, K, nP, ctx.nstepsolver, ctx.nc,
+                               ctx.adaptive_substeps, stage_points, As, grad, moments, gp, ws,
+                               tab=tab, grad_theta=grad_theta)
         if want_points and points.dim() == 2:
             summed = torch.empty((ndim, nP), device=dev, dtype=torch.float32)
             lib.sum_batch(gp, summed)
@@ -343,14 +351,15 @@ class _CPABImageFunction(torch.autograd.Function):
         n, nC, ndim = As.shape[0], As.shape[1], As.shape[2]
         grad = grad.detach().to(torch.float32).contiguous()
         moments = torch.empty((n, nC, ndim * (ndim + 1)), device=dev, dtype=torch.float32)
-        ws_bytes = lib.transform_data_backward_workspace_size(ndim, n, ctx.outsize, nC)
-        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
         grad_data = torch.empty_like(data) if ctx.needs_input_grad[0] else None
         tab, grad_theta = None, None
         if ctx.needs_input_grad[1]:
             tab = basis_tables(params, dev)
             grad_theta = torch.empty((n, tab["d"]), device=dev, dtype=torch.float32)
-        lib.transform_data_backward(ndim, data, axes, ctx.outsize, ctx.T, ctx.nc, ctx.adaptive,
-                                    final, As, grad, moments, grad_data, ws, tab=tab,
-                                    grad_theta=grad_theta, seed_grad=seed_grad)
+        with lib.deterministic(_deterministic(params)):
+            ws_bytes = lib.transform_data_backward_workspace_size(ndim, n, ctx.outsize, nC)
+            ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
+            lib.transform_data_backward(ndim, data, axes, ctx.outsize, ctx.T, ctx.nc,
+                                        ctx.adaptive, final, As, grad, moments, grad_data, ws,
+                                        tab=tab, grad_theta=grad_theta, seed_grad=seed_grad)
         return grad_data, grad_theta, None, None, None

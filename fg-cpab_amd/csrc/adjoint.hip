@@ -412,13 +412,31 @@ struct ImageIO {
   __device__ __forceinline__ void finish(int, bool, const float (&)[D]) const {}
 };
 
+// Where a flush adds a run's sums: full LDS bins, or the LDS cell cache with
+// HBM for the cells it has no slot for.
+// kSpread: full bins, whose components the register variant may add one at a
+// time (add1).
+template <int BINS, int PP>
+struct FloatSink {
+  static constexpr bool kSpread = full_bins(BINS);
+  float* bins;
+  int* keys;
+  float* __restrict__ mom;
+  __device__ __forceinline__ void operator()(int c, const float (&m)[PP]) const {
+    if (full_bins(BINS)) flush_lds<PP>(bins, c, m);
+    else flush_cache<PP>(keys, bins, mom, c, m);
+  }
+  __device__ __forceinline__ void add1(int c, int k, float v) const {
+    __hip_atomic_fetch_add(bins + PP * c + k, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+};
+
 // Segmented variant (any T <= kSeg * MAXSEG).
-// One stage of one theta over this workgroup's point range; moments go to
-// bins / keys / mom_b.
-template <int D, bool ADAPTIVE, int BINS, int MAXSEG = kMaxSeg, typename P, typename IO>
-__device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ gtab, int nP, int T,
-                                               const Cells& g, const IO& io, float* bins,
-                                               int* keys, float* __restrict__ mom_b) {
+// One stage of one theta over this workgroup's point range; each run's sums go
+// to `flush` (a sink above, or the deterministic one below).
+template <int D, bool ADAPTIVE, int MAXSEG, typename P, typename IO, typename Sink>
+__device__ __forceinline__ void segmented_run(P tab, const float* __restrict__ gtab, int nP, int T,
+                                              const Cells& g, const IO& io, const Sink& flush) {
   constexpr int PP = Dim<D>::P;
   const float h = 1.0f / (float)T;
   const float hh = h * 0.5f;
@@ -484,11 +502,7 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
         if (s < len) {
           const int c = sc[s];
           const bool need = valid && c != prev && prev >= 0;
-          if (full_bins(BINS)) {
-            if (need) flush_lds<PP>(bins, prev, m);
-          } else {
-            if (need) flush_cache<PP>(keys, bins, mom_b, prev, m);
-          }
+          if (need) flush(prev, m);
           if (c != prev) {
 #pragma unroll
             for (int k = 0; k < PP; ++k) m[k] = 0.0f;
@@ -501,17 +515,23 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
     float r[PP];
     bool on;
     wave_run_sums<PP>(valid, prev, m, r, on);
-    if (on) {
-      if (full_bins(BINS)) flush_lds<PP>(bins, prev, r);
-      else flush_cache<PP>(keys, bins, mom_b, prev, r);
-    }
+    if (on) flush(prev, r);
     io.finish(pi, valid, lam);
   }
 }
 
-// Register variant: T == TS known at compile time, moments in full LDS bins
-// or (3D) in the LDS cell cache.  Without adaptive substeps every replay step
-// is p' = E_c [p; 1] with the cell's fixed midpoint map, so phase 1 keeps only
+template <int D, bool ADAPTIVE, int BINS, int MAXSEG = kMaxSeg, typename P, typename IO>
+__device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ gtab, int nP, int T,
+                                               const Cells& g, const IO& io, float* bins,
+                                               int* keys, float* __restrict__ mom_b) {
+  segmented_run<D, ADAPTIVE, MAXSEG>(tab, gtab, nP, T, g, io,
+                                     FloatSink<BINS, Dim<D>::P>{bins, keys, mom_b});
+}
+
+// Register variant: T == TS known at compile time; each run's sums go to
+// `flush` (FloatSink: full LDS bins or, 3D, the LDS cell cache; or the
+// deterministic sink).  Without adaptive substeps every replay step is
+// p' = E_c [p; 1] with the cell's fixed midpoint map, so phase 1 keeps only
 // the cells and phase 2 recovers each position from the next through the
 // cell's inverse map (a few ulp per step; the positions only feed the sums
 // S, the cells stay exact).  With adaptive substeps (Heun on crossings) the
@@ -519,10 +539,9 @@ __device__ __forceinline__ void segmented_body(P tab, const float* __restrict__ 
 // substeps, else +inf): the row's domain-edge bound for TS replay steps; a wave
 // whose lanes all start at least that far from every edge replays without the
 // lookup's per-step edge test (the same cells).
-template <int D, bool ADAPTIVE, int BINS, int TS, typename P, typename PG, typename IO>
-__device__ __forceinline__ void register_body(P tab, PG gtab, int nP,
-                                              const Cells& g, const IO& io, float* bins,
-                                              int* keys, float* __restrict__ mom_b, float delta) {
+template <int D, bool ADAPTIVE, int TS, typename P, typename PG, typename IO, typename Sink>
+__device__ __forceinline__ void register_body(P tab, PG gtab, int nP, const Cells& g,
+                                              const IO& io, const Sink& flush, float delta) {
   constexpr int PP = Dim<D>::P;
   // A trajectory's last flush has all 64 lanes of every wave adding to
   // scattered bins at the same moment, a burst the LDS atomic pipe drains at
@@ -530,7 +549,7 @@ __device__ __forceinline__ void register_body(P tab, PG gtab, int nP,
   // registers to spare) it is kept pending instead and issued one component
   // every TS / PP steps during the next range's phase 1, alongside its VALU
   // work; the last range's flush follows the loop.
-  constexpr bool kSpread = D <= 2 && !ADAPTIVE && full_bins(BINS);
+  constexpr bool kSpread = D <= 2 && !ADAPTIVE && Sink::kSpread;
   const float h = 1.0f / (float)TS;
   const float hh = h * 0.5f;
   float pend[PP];
@@ -567,9 +586,7 @@ __device__ __forceinline__ void register_body(P tab, PG gtab, int nP,
         if constexpr (kSpread) {
 #pragma unroll
           for (int k = 0; k < PP; ++k) {
-            if (t == (k * TS) / PP && pend_on)
-              __hip_atomic_fetch_add(bins + PP * pend_c + k, pend[k], __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (t == (k * TS) / PP && pend_on) flush.add1(pend_c, k, pend[k]);
           }
         }
         const int c = (t == 0) ? cur : look();
@@ -628,10 +645,7 @@ __device__ __forceinline__ void register_body(P tab, PG gtab, int nP,
           // adds would wait for them before the next step can use it.
           G = fetch_adj<D>(gtab, cn);
           if (!ADAPTIVE) E = fetch_inv<D>(gtab, cn);
-          if (valid) {
-            if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, c, m);
-            else flush_lds<PP>(bins, c, m);
-          }
+          if (valid) flush(c, m);
 #pragma unroll
           for (int k = 0; k < PP; ++k) m[k] = 0.0f;
         }
@@ -645,14 +659,11 @@ __device__ __forceinline__ void register_body(P tab, PG gtab, int nP,
       float r[PP];
       bool on;
       wave_run_sums<PP>(valid, c, m, r, on);
-      if (on) {
-        if (BINS == kBinsCache) flush_cache<PP>(keys, bins, mom_b, c, r);
-        else flush_lds<PP>(bins, c, r);
-      }
+      if (on) flush(c, r);
     }
     io.finish(pi, valid, lam);
   }
-  if (kSpread && pend_on) flush_lds<PP>(bins, pend_c, pend);
+  if (kSpread && pend_on) flush(pend_c, pend);
 }
 
 // LDS layout of a backward workgroup: [A table (LDS_A)] then either the full
@@ -801,10 +812,11 @@ __device__ __forceinline__ void run_stage(const StageLds<D, LDS_A, BINS>& L, con
         return;
       }
     }
+    const FloatSink<BINS, Dim<D>::P> sink{L.bins, L.keys, mom_b};
     if constexpr (BINS == kBinsFullRev)
-      register_body<D, ADAPTIVE, BINS, TS>(Ag, as_lds(L.ldsG), nP, g, io, L.bins, L.keys, mom_b, delta);
-    else if (LDS_A) register_body<D, ADAPTIVE, BINS, TS>(as_lds(L.ldsA), Gg, nP, g, io, L.bins, L.keys, mom_b, delta);
-    else register_body<D, ADAPTIVE, BINS, TS>(Ag, Gg, nP, g, io, L.bins, L.keys, mom_b, delta);
+      register_body<D, ADAPTIVE, TS>(Ag, as_lds(L.ldsG), nP, g, io, sink, delta);
+    else if (LDS_A) register_body<D, ADAPTIVE, TS>(as_lds(L.ldsA), Gg, nP, g, io, sink, delta);
+    else register_body<D, ADAPTIVE, TS>(Ag, Gg, nP, g, io, sink, delta);
   } else {
     if (LDS_A) segmented_body<D, ADAPTIVE, BINS>(as_lds(L.ldsA), Gg, nP, T, g, io, L.bins, L.keys, mom_b);
     else segmented_body<D, ADAPTIVE, BINS>(Ag, Gg, nP, T, g, io, L.bins, L.keys, mom_b);
@@ -906,6 +918,232 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
         moments + (size_t)b * R, nC, &touched_cnt);
 }
 
+// ---------------------------------------------------------------------------
+// Deterministic reduction (opt in: cpab_set_deterministic).  Float atomics add
+// the runs' sums in whatever order the lanes, waves and workgroups reach them,
+// so the last bits of the moments vary from run to run.  Here the backward
+// runs twice over the same trajectories, with the same bodies and launch
+// shape, so both passes flush the same values.  Pass 0 records each row's
+// largest finite |flushed value| (an atomic max: the same result in any
+// order).  Pass 1 adds every finite flushed value as a 64-bit integer,
+// rint(value * 2^s) with the row's scale 2^s, into LDS (the row's full table
+// or a cell cache) and HBM: integer adds give the same sums in any order.  The scale leaves the
+// sums of all of a row's flushes below 2^62 in magnitude (det_scale), so none
+// overflows; the quantum is 2^-(62 - lg) of the row's largest value, lg =
+// ceil(log2(nP T)).  A non-finite value sets its component's flag instead
+// (bit 0 +inf, bit 1 -inf, bit 2 NaN, an atomic or), and the finish gives
+// that component the float sum's result: +inf, -inf or NaN.  The finish
+// divides the integer sums by the scale.
+// ---------------------------------------------------------------------------
+template <int D> constexpr int kDetSlots = kDetCacheSlots[D];
+constexpr int kDetThreads = kDetBlock;
+
+// Dynamic LDS of a pass: none for pass 0; for pass 1 the row's full table
+// (FULL, direct-indexed by cell) or the hashed cache of kDetSlots cells.
+template <int D, int PASS, bool FULL>
+size_t det_lds_bytes(int nC) {
+  constexpr int P = Dim<D>::P;
+  if (PASS == 0) return 0;
+  if (FULL) return (size_t)nC * P * sizeof(unsigned long long);
+  return (size_t)kDetSlots<D> * (P * sizeof(unsigned long long) + sizeof(int));
+}
+static_assert(det_cache_bytes_for(1) == (int64_t)kDetSlots<1> * (2 * 8 + 4) &&
+                  det_cache_bytes_for(2) == (int64_t)kDetSlots<2> * (6 * 8 + 4) &&
+                  det_cache_bytes_for(3) == (int64_t)kDetSlots<3> * (12 * 8 + 4),
+              "the host's LDS size is the kernel's");
+
+template <int D, int PASS, bool FULL>
+struct DetSink {
+  static constexpr bool kSpread = false;
+  int* keys;                               // LDS [kDetSlots] (cache)
+  unsigned long long* vals;                // LDS [nC * P] (FULL) or [kDetSlots * P] (cache)
+  unsigned long long* __restrict__ mom;    // HBM sums of this row [nC * P]
+  unsigned* wg_max;                        // LDS
+  unsigned* __restrict__ flags;            // HBM non-finite flags of this row [nC * P]
+  double scale;
+  __device__ __forceinline__ void operator()(int c, const float (&m)[Dim<D>::P]) const {
+    constexpr int P = Dim<D>::P;
+    if constexpr (PASS == 0) {
+      float a = 0.0f;
+#pragma unroll
+      for (int k = 0; k < P; ++k)
+        if (__builtin_isfinite(m[k])) a = fmaxf(a, fabsf(m[k]));
+      __hip_atomic_fetch_max(wg_max, __float_as_uint(a), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+      unsigned long long q[P];
+#pragma unroll
+      for (int k = 0; k < P; ++k) {
+        const bool fin = __builtin_isfinite(m[k]);
+        q[k] = fin ? (unsigned long long)(long long)__builtin_rint((double)m[k] * scale) : 0ull;
+        if (!fin)
+          __hip_atomic_fetch_or(flags + (size_t)c * P + k,
+                                m[k] != m[k] ? 4u : (m[k] > 0.0f ? 1u : 2u), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if constexpr (FULL) {
+#pragma unroll
+        for (int j = 0; j < P; ++j)
+          __hip_atomic_fetch_add(vals + (size_t)c * P + j, q[j], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+        return;
+      }
+      int slot = c & (kDetSlots<D> - 1);
+      for (int probe = 0; probe < kCacheProbes; ++probe) {
+        int k = __hip_atomic_load(keys + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (k == -1) {
+          int expected = -1;
+          __hip_atomic_compare_exchange_strong(keys + slot, &expected, c, __ATOMIC_RELAXED,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          k = expected == -1 ? c : expected;
+        }
+        if (k == c) {
+#pragma unroll
+          for (int j = 0; j < P; ++j)
+            __hip_atomic_fetch_add(vals + (size_t)slot * P + j, q[j], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+          return;
+        }
+        slot = (slot + 1) & (kDetSlots<D> - 1);
+      }
+#pragma unroll
+      for (int j = 0; j < P; ++j)
+        __hip_atomic_fetch_add(mom + (size_t)c * P + j, q[j], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+};
+
+// Clears the workgroup maximum (pass 0) or the LDS sums (pass 1) before a
+// stage, then, after it, publishes them: pass 0 the maximum into the row's
+// stat, pass 1 the nonzero sums into the row's HBM sums.
+template <int D, int PASS, bool FULL>
+struct DetLds {
+  int* keys;
+  unsigned long long* vals;
+  unsigned* wg_max;
+  int nC;
+  __device__ __forceinline__ int n_vals() const {
+    return FULL ? nC * Dim<D>::P : kDetSlots<D> * Dim<D>::P;
+  }
+  __device__ __forceinline__ void begin() const {
+    if constexpr (PASS == 0) {
+      if (threadIdx.x == 0) *wg_max = 0u;
+    } else {
+      if constexpr (!FULL)
+        for (int i = threadIdx.x; i < kDetSlots<D>; i += blockDim.x) keys[i] = -1;
+      for (int i = threadIdx.x; i < n_vals(); i += blockDim.x) vals[i] = 0ull;
+    }
+    __syncthreads();
+  }
+  __device__ __forceinline__ void end(unsigned* __restrict__ stat,
+                                      unsigned long long* __restrict__ mom) const {
+    constexpr int P = Dim<D>::P;
+    __syncthreads();
+    if constexpr (PASS == 0) {
+      if (threadIdx.x == 0 && *wg_max != 0u)
+        __hip_atomic_fetch_max(stat, *wg_max, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      for (int i = threadIdx.x; i < n_vals(); i += blockDim.x) {
+        const int c = FULL ? i / P : keys[i / P];
+        if (c >= 0 && vals[i] != 0ull)
+          __hip_atomic_fetch_add(mom + (size_t)c * P + (i % P), vals[i], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+};
+
+// A deterministic pass's body: the register variant where the default
+// backward takes it (T == TS > 0; without adaptive substeps only for rows whose
+// positions may be recovered), else the segmented one.
+template <int D, bool ADAPTIVE, int TS, typename P, typename IO, typename Sink>
+__device__ __forceinline__ void det_body(P tab, const float* __restrict__ gtab, int nP, int T,
+                                         const Cells& g, const IO& io, const Sink& sink,
+                                         const Recover& rec, size_t row) {
+  if constexpr (TS > 0) {
+    if (ADAPTIVE || recover_ok(rec.amp + row * rec.namp, rec.namp, rec.amp_max))
+      register_body<D, ADAPTIVE, TS>(tab, gtab, nP, g, io, sink, INFINITY);
+    else
+      segmented_run<D, ADAPTIVE, (TS + kSeg - 1) / kSeg>(tab, gtab, nP, TS, g, io, sink);
+  } else {
+    segmented_run<D, ADAPTIVE, kMaxSeg>(tab, gtab, nP, T, g, io, sink);
+  }
+}
+
+template <int D, bool ADAPTIVE, int PASS, bool FULL, int TS>
+__global__ __launch_bounds__(kDetThreads) void det_backward_kernel(
+    int nP, int batched, int T, Cells g, int nC, int K, const float* __restrict__ points,
+    const float* __restrict__ stage_points, const float* __restrict__ As,
+    const float* __restrict__ Gs, Recover rec, const float* __restrict__ grad_out,
+    unsigned* __restrict__ stat, unsigned long long* __restrict__ sums,
+    unsigned* __restrict__ flags, float* __restrict__ lam, float* __restrict__ grad_points) {
+  extern __shared__ __align__(16) unsigned long long det_lds[];
+  __shared__ unsigned wg_max;
+  constexpr int P = Dim<D>::P;
+  const DetLds<D, PASS, FULL> L{reinterpret_cast<int*>(det_lds + (size_t)kDetSlots<D> * P),
+                                det_lds, &wg_max, nC};
+  const WgSlot w = wg_slot();
+  const int b = w.row;
+  const int n_batch = gridDim.y;
+  const int R = nC * P;
+  const size_t plane = (size_t)D * nP;
+  for (int k = K - 1; k >= 0; --k) {
+    const size_t row = (size_t)k * n_batch + b;
+    PlainIO<D> io;
+    io.nP = nP;
+    io.pts = k == 0 ? points + (batched ? (size_t)b * plane : 0)
+                    : stage_points + ((size_t)(k - 1) * n_batch + b) * plane;
+    io.gout = k == K - 1 ? grad_out + (size_t)b * plane : lam + (size_t)b * plane;
+    io.lam_out = k == 0 ? (grad_points ? grad_points + (size_t)b * plane : nullptr)
+                        : lam + (size_t)b * plane;
+    const double scale = PASS == 0 ? 0.0 : det_scale(stat[row], nP, T);
+    L.begin();
+    det_body<D, ADAPTIVE, TS>(
+        As + row * R, Gs + row * nC * RevStride<D>::S, nP, T, g, io,
+        DetSink<D, PASS, FULL>{L.keys, L.vals, sums + row * R, L.wg_max, flags + row * R, scale},
+        rec, row);
+    L.end(stat + row, sums + row * R);
+    if (k > 0) __syncthreads();
+  }
+}
+
+template <int D, bool ADAPTIVE, int PASS, bool FULL, int TS>
+__global__ __launch_bounds__(kDetThreads) void det_image_backward_kernel(
+    ImageShape s, int T, Cells g, int nC, const float* __restrict__ axes,
+    const float* __restrict__ final_points, const float* __restrict__ seed_grad,
+    const float* __restrict__ As, const float* __restrict__ Gs, Recover rec,
+    const float* __restrict__ data,
+    const float* __restrict__ grad_out, unsigned* __restrict__ stat,
+    unsigned long long* __restrict__ sums, unsigned* __restrict__ flags,
+    float* __restrict__ grad_data) {
+  extern __shared__ __align__(16) unsigned long long det_lds[];
+  __shared__ unsigned wg_max;
+  constexpr int P = Dim<D>::P;
+  const DetLds<D, PASS, FULL> L{reinterpret_cast<int*>(det_lds + (size_t)kDetSlots<D> * P),
+                                det_lds, &wg_max, nC};
+  const WgSlot w = wg_slot();
+  const int b = w.row;
+  const int R = nC * P;
+  ImageIO<D> io;
+  io.s = s;
+  io.axes = axes;
+  io.fin = final_points ? final_points + (size_t)b * D * s.nP : nullptr;
+  io.sgrad = seed_grad ? seed_grad + (size_t)b * D * s.nP : nullptr;
+  io.gout = grad_out + (size_t)b * s.C * s.nP;
+  io.data = data + (size_t)b * s.C * s.plane_in;
+  // grad_data is scattered once, in pass 1
+  io.gdata = (PASS == 1 && grad_data) ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
+  const double scale = PASS == 0 ? 0.0 : det_scale(stat[b], s.nP, T);
+  L.begin();
+  det_body<D, ADAPTIVE, TS>(As + (size_t)b * R, Gs + (size_t)b * nC * RevStride<D>::S, s.nP, T, g,
+                            io,
+                            DetSink<D, PASS, FULL>{L.keys, L.vals, sums + (size_t)b * R, L.wg_max,
+                                                   flags + (size_t)b * R, scale},
+                            rec, (size_t)b);
+  L.end(stat + b, sums + (size_t)b * R);
+}
+
 template <int D, bool LDS_A, int BINS>
 size_t stage_lds_bytes(int nC) {
   const size_t R = (size_t)nC * Dim<D>::P;
@@ -936,7 +1174,69 @@ struct BackwardJob {
   const ImageShape* image;
   const float *axes, *final_points, *seed_grad, *data;
   float* grad_data;
+  // deterministic reduction: pass 1 or 2 (0: float atomics), its row stats and
+  // integer sums
+  int det_pass;
+  unsigned* det_stat;
+  unsigned long long* det_sums;
+  unsigned* det_flags;
 };
+
+template <int D, bool ADAPTIVE, int PASS, bool FULL, int TS>
+hipError_t go_det(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
+  const size_t lds = det_lds_bytes<D, PASS, FULL>(j.geo.nC);
+  const Cells g{j.geo.nx, j.geo.ny, j.geo.nz};
+  const Recover rec{j.amp, adjoint_table_blocks(j.geo.nC),
+                    (float)std::pow((double)kRecoverGrowth, 1.0 / (double)j.T), nullptr};
+  const dim3 grid((unsigned)cfg.chunks, (unsigned)j.n_batch), block((unsigned)kDetThreads);
+  if (j.image) {
+    auto kernel = det_image_backward_kernel<D, ADAPTIVE, PASS, FULL, TS>;
+    hipError_t e = allow_lds(kernel, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, *j.image, j.T, g, j.geo.nC, j.axes,
+                       j.final_points, j.seed_grad, j.As, j.G, rec, j.data, j.grad_out,
+                       j.det_stat, j.det_sums, j.det_flags, j.grad_data);
+  } else {
+    auto kernel = det_backward_kernel<D, ADAPTIVE, PASS, FULL, TS>;
+    hipError_t e = allow_lds(kernel, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, (int)j.nP, j.batched, j.T, g, j.geo.nC, j.K,
+                       j.points, j.stage_points, j.As, j.G, rec, j.grad_out, j.det_stat,
+                       j.det_sums, j.det_flags, j.lam, j.grad_points);
+  }
+  return hipGetLastError();
+}
+
+// Both passes must flush the same values, so they take the same body: the
+// register variant for T == kRegSteps, with adaptive substeps only in 1D/2D
+// with full tables (as the default backward; with the cache its unrolled
+// steps do not fit in registers).
+template <int D, bool ADAPTIVE, int PASS, bool FULL>
+hipError_t go_det_steps(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
+  if constexpr (D == 3 && ADAPTIVE) {
+    return go_det<D, ADAPTIVE, PASS, FULL, 0>(j, cfg, s);
+  } else if constexpr (ADAPTIVE && PASS == 1 && !FULL) {
+    return go_det<D, ADAPTIVE, PASS, FULL, 0>(j, cfg, s);
+  } else {
+    if (j.T == kRegSteps && (!ADAPTIVE || cfg.lds_bins))
+      return go_det<D, ADAPTIVE, PASS, FULL, kRegSteps>(j, cfg, s);
+    return go_det<D, ADAPTIVE, PASS, FULL, 0>(j, cfg, s);
+  }
+}
+
+// Pass 0 needs no LDS table (FULL false); pass 1 takes cfg.lds_bins: the
+// row's full table in LDS, else the cache.
+template <int D>
+hipError_t dispatch_det(const BackwardJob& j, int adaptive, const LaunchCfg& cfg, hipStream_t s) {
+  if (j.det_pass == 1)
+    return adaptive ? go_det_steps<D, true, 0, false>(j, cfg, s)
+                    : go_det_steps<D, false, 0, false>(j, cfg, s);
+  if (cfg.lds_bins)
+    return adaptive ? go_det_steps<D, true, 1, true>(j, cfg, s)
+                    : go_det_steps<D, false, 1, true>(j, cfg, s);
+  return adaptive ? go_det_steps<D, true, 1, false>(j, cfg, s)
+                  : go_det_steps<D, false, 1, false>(j, cfg, s);
+}
 
 template <int D, bool ADAPTIVE, bool LDS_A, int BINS, int TS>
 hipError_t go(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
@@ -1002,6 +1302,13 @@ hipError_t dispatch(const BackwardJob& j, int adaptive, const LaunchCfg& cfg, hi
 
 hipError_t dispatch_any(const BackwardJob& j, int adaptive, const LaunchCfg& cfg, hipStream_t s) {
   if (j.nP <= 0 || j.n_batch <= 0 || j.K <= 0) return hipSuccess;
+  if (j.det_pass) {
+    switch (j.geo.ndim) {
+      case 1: return dispatch_det<1>(j, adaptive, cfg, s);
+      case 2: return dispatch_det<2>(j, adaptive, cfg, s);
+      default: return dispatch_det<3>(j, adaptive, cfg, s);
+    }
+  }
   switch (j.geo.ndim) {
     case 1: return dispatch<1>(j, adaptive, cfg, s);
     case 2: return dispatch<2>(j, adaptive, cfg, s);
@@ -1016,8 +1323,13 @@ hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int b
                            const float* As, const float* G, const float* amp,
                            const EdgeAcc* edge, const float* grad_out, float* moments,
                            float* partials, uint64_t* dense_parts, float* lam, float* grad_points,
-                           const LaunchCfg& cfg, hipStream_t s) {
+                           const LaunchCfg& cfg, hipStream_t s, int det_pass, unsigned* det_stat,
+                           unsigned long long* det_sums, unsigned* det_flags) {
   BackwardJob j{};
+  j.det_pass = det_pass;
+  j.det_stat = det_stat;
+  j.det_sums = det_sums;
+  j.det_flags = det_flags;
   j.edge = edge;
   j.geo = g;
   j.nP = nP;
@@ -1046,8 +1358,13 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
                                  const EdgeAcc* edge, const float* data,
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
-                                 hipStream_t s) {
+                                 hipStream_t s, int det_pass, unsigned* det_stat,
+                                 unsigned long long* det_sums, unsigned* det_flags) {
   BackwardJob j{};
+  j.det_pass = det_pass;
+  j.det_stat = det_stat;
+  j.det_sums = det_sums;
+  j.det_flags = det_flags;
   j.edge = edge;
   j.geo = g;
   j.nP = img.nP;

@@ -206,13 +206,20 @@ __global__ __launch_bounds__(kTableThreads) void adjoint_table_kernel(
 // threads read consecutive floats of each partial table.
 template <int D> constexpr int kFinCells = 256 / (D * (D + 1));
 
-template <int D>
+// DET: S from the deterministic reduction's integer sums, divided by the row's
+// scale (det_scale), or +inf / -inf / NaN where the component's flags record
+// non-finite values, in place of the HBM float sums and partials.
+template <int D, bool DET = false>
 __global__ __launch_bounds__(256) void finish_moments_kernel(int64_t rows, int nC, int nblk,
                                                              int nparts, float h,
                                                              const float* __restrict__ partials,
                                                              const uint64_t* __restrict__ dense_parts,
                                                              const float* __restrict__ As,
-                                                             float* __restrict__ moments) {
+                                                             float* __restrict__ moments,
+                                                             const unsigned* __restrict__ det_stat = nullptr,
+                                                             const unsigned long long* __restrict__ det_sums = nullptr,
+                                                             const unsigned* __restrict__ det_flags = nullptr,
+                                                             int64_t det_nP = 0, int det_T = 0) {
   constexpr int P = D * (D + 1);
   constexpr int W = D + 1;
   constexpr int CB = kFinCells<D>;
@@ -223,7 +230,13 @@ __global__ __launch_bounds__(256) void finish_moments_kernel(int64_t rows, int n
   const int cl = t / P, comp = t - cl * P;
   const bool live = t < CB * P && c0 + cl < nC;
   const int64_t idx = (row * nC + c0 + cl) * P + comp;   // this thread's float of the row's table
-  if (live) {
+  if (live && DET) {
+    const double scale = det_scale(det_stat[row], det_nP, det_T);
+    const unsigned f = det_flags[idx];
+    s_lds[t] = f == 0u ? (scale > 0.0 ? (float)((double)(long long)det_sums[idx] / scale) : NAN)
+                       : (f == 1u ? INFINITY : f == 2u ? -INFINITY : NAN);
+    a_lds[t] = As[idx];
+  } else if (live) {
     float s = moments[idx];
     if (nparts > 0) {
       const int64_t R = (int64_t)nC * P;
@@ -592,11 +605,29 @@ hipError_t launch_finish_moments(int ndim, int64_t rows, int nC, int nparts, int
   auto go = [&](auto kernel, int cb) {
     const int nblk = (nC + cb - 1) / cb;
     hipLaunchKernelGGL(kernel, dim3((unsigned)(rows * nblk)), dim3(256), 0, s, rows, nC, nblk,
-                       nparts, h, partials, dense_parts, As, moments);
+                       nparts, h, partials, dense_parts, As, moments, nullptr, nullptr, nullptr,
+                       (int64_t)0, 0);
   };
   if (ndim == 1) go(finish_moments_kernel<1>, kFinCells<1>);
   else if (ndim == 2) go(finish_moments_kernel<2>, kFinCells<2>);
   else go(finish_moments_kernel<3>, kFinCells<3>);
+  return hipGetLastError();
+}
+
+hipError_t launch_finish_moments_det(int ndim, int64_t rows, int nC, int64_t nP, int T,
+                                     const unsigned* det_stat, const unsigned long long* det_sums,
+                                     const unsigned* det_flags, const float* As, float* moments,
+                                     hipStream_t s) {
+  if (rows <= 0 || nC <= 0) return hipSuccess;
+  const float h = 1.0f / (float)T;
+  auto go = [&](auto kernel, int cb) {
+    const int nblk = (nC + cb - 1) / cb;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)(rows * nblk)), dim3(256), 0, s, rows, nC, nblk, 0,
+                       h, nullptr, nullptr, As, moments, det_stat, det_sums, det_flags, nP, T);
+  };
+  if (ndim == 1) go(finish_moments_kernel<1, true>, kFinCells<1>);
+  else if (ndim == 2) go(finish_moments_kernel<2, true>, kFinCells<2>);
+  else go(finish_moments_kernel<3, true>, kFinCells<3>);
   return hipGetLastError();
 }
 

@@ -295,15 +295,20 @@ int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 // the inverse maps [rows, adjoint_table_blocks(nC)] and (2D) the per-block
 // parts of the rows' domain-edge bounds [rows, adjoint_table_blocks(nC)].
 struct BackwardWorkspace {
-  int64_t dense_words, partials_offset, lam_offset, g_offset, amp_offset, edge_offset, total;
+  int64_t dense_words, partials_offset, lam_offset, g_offset, amp_offset, edge_offset;
+  int64_t det_stat_offset, det_sums_offset, det_flags_offset, total;
 };
+
+// Deterministic reduction (cpab_set_deterministic), per calling thread.
+thread_local int t_deterministic = 0;
 
 
 BackwardWorkspace backward_workspace(const cpab::Geometry& g, int64_t nP, int64_t n_batch, int K,
-                                     const cpab::LaunchCfg& cfg) {
+                                     const cpab::LaunchCfg& cfg, bool det = false) {
   BackwardWorkspace w{};
-  const int64_t parts = cfg.lds_bins ? (int64_t)K * n_batch * cfg.chunks : 0;
-  w.dense_words = cfg.lds_bins ? (int64_t)K * n_batch * ((cfg.chunks + 63) / 64) : 0;
+  const bool dense = cfg.lds_bins && !det;
+  const int64_t parts = dense ? (int64_t)K * n_batch * cfg.chunks : 0;
+  w.dense_words = dense ? (int64_t)K * n_batch * ((cfg.chunks + 63) / 64) : 0;
   w.partials_offset = align_up(w.dense_words * 8);
   w.lam_offset = align_up(w.partials_offset + parts * g.nC * g.ppc() * 4);
   w.g_offset = K > 1 ? align_up(w.lam_offset + n_batch * g.ndim * nP * 4) : w.lam_offset;
@@ -311,6 +316,13 @@ BackwardWorkspace backward_workspace(const cpab::Geometry& g, int64_t nP, int64_
   const int64_t blocks = (int64_t)K * n_batch * cpab::adjoint_table_blocks(g.nC);
   w.edge_offset = align_up(w.amp_offset + blocks * 4);
   w.total = w.edge_offset + (g.ndim == 2 ? blocks * cpab::kEdgeAccBytes : 0);
+  // deterministic reduction: row stats [rows], 64-bit sums [rows, nC, ppc] and
+  // non-finite flags [rows, nC, ppc]
+  const int64_t comps = (int64_t)K * n_batch * g.nC * g.ppc();
+  w.det_stat_offset = align_up(w.total);
+  w.det_sums_offset = align_up(w.det_stat_offset + (int64_t)K * n_batch * 4);
+  w.det_flags_offset = w.det_sums_offset + comps * 8;
+  if (det) w.total = w.det_flags_offset + comps * 4;
   return w;
 }
 
@@ -333,11 +345,42 @@ int check_projection(const Projection& pr) {
 }
 
 
+// Launch shape of the deterministic passes: pass 1 keeps the row's full table
+// of 64-bit sums in LDS when it fits in kDetFullBytes (lds_bins), else a
+// hashed cache; about four workgroups per CU (the passes' register use allows
+// four 256-thread workgroups per CU), at most one pass over a row's points.
+// The shape depends only on the device and the problem, so every run groups
+// the trajectories' sums the same way.
+bool det_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta, cpab::LaunchCfg* out) {
+  const DeviceInfo dev = device_info();
+  cpab::LaunchCfg c{};
+  c.block = cpab::kDetBlock;
+  c.lds_bins = cpab::det_full_bytes_for(g.ndim, g.nC) <= cpab::kDetFullBytes ? 1 : 0;
+  const int64_t lds = c.lds_bins ? cpab::det_full_bytes_for(g.ndim, g.nC)
+                                 : cpab::det_cache_bytes_for(g.ndim);
+  if (lds + 16 > dev.lds) {
+    fail(CPAB_ERR_DEVICE, "the deterministic backward needs %lld bytes of LDS per workgroup, the "
+         "device has %d", (long long)(lds + 16), dev.lds);
+    return false;
+  }
+  const int64_t per_cu = 4;
+  int64_t chunks = std::max<int64_t>(1, div_up(dev.cus * per_cu, std::max<int64_t>(n_theta, 1)));
+  chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
+  c.chunks = (int)chunks;
+  *out = c;
+  return true;
+}
+
 int64_t workspace_size_impl(int ndim, int64_t nP, int64_t n_batch, int K, int nC) {
   if (ndim < 1 || ndim > 3 || nP <= 0 || n_batch <= 0 || nC <= 0 || K < 1) return 0;
   cpab::Geometry g{};
   g.ndim = ndim;
   g.nC = nC;
+  if (t_deterministic) {
+    cpab::LaunchCfg det;
+    if (!det_cfg(g, nP, n_batch, &det)) return 0;
+    return backward_workspace(g, nP, n_batch, K, det, true).total;
+  }
   // Whichever variant runs (register or segmented) fits.
   cpab::LaunchCfg reg, seg;
   if (!backward_cfg(g, nP, n_batch, cpab::kRegSteps, 0, &reg) || !backward_cfg(g, nP, n_batch, 0, 1, &seg))
@@ -390,12 +433,14 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(points, 4); CPAB_ALIGNED(grad_out, 4);
   CPAB_ALIGNED(workspace, 16);
   if (K > 1) CPAB_REQUIRE(stage_points);
+  const bool det = t_deterministic != 0;
   cpab::LaunchCfg cfg;
-  if (!backward_cfg(g, nP, n_batch, nstepsolver, adaptive, &cfg)) return CPAB_ERR_DEVICE;
+  if (det ? !det_cfg(g, nP, n_batch, &cfg) : !backward_cfg(g, nP, n_batch, nstepsolver, adaptive, &cfg))
+    return CPAB_ERR_DEVICE;
   // A chain restages each stage's table: measured slower than L2 reads (C5
   // backward 185 -> 190 us), so chains keep the reverse-sweep table in HBM.
   if (K > 1) cfg.lds_rev = 0;
-  const BackwardWorkspace w = backward_workspace(g, nP, n_batch, K, cfg);
+  const BackwardWorkspace w = backward_workspace(g, nP, n_batch, K, cfg, det);
   if (workspace == nullptr || workspace_bytes < w.total)
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
                 (long long)w.total, (long long)workspace_bytes);
@@ -409,14 +454,40 @@ int backward_impl(const char* who, int ndim, int64_t nP, int64_t n_batch, int ba
   // skip the lookup's edge test.  Not for chains: each stage would pay the
   // bound's reduction, and a chain's slowest waves (those on the domain's
   // edge, which never qualify) set its time (C5 backward 174 -> 185 us).
-  cpab::EdgeAcc* edge =
-      ndim == 2 && K == 1 ? reinterpret_cast<cpab::EdgeAcc*>(ws + w.edge_offset) : nullptr;
+  cpab::EdgeAcc* edge = ndim == 2 && K == 1 && !det
+                           ? reinterpret_cast<cpab::EdgeAcc*>(ws + w.edge_offset)
+                           : nullptr;
   // G table, inverse-map norms and domain-edge bound parts; the HBM sums and
   // dense-part masks cleared.
   rc = check_hip(cpab::launch_adjoint_table(ndim, rows, g.nx, g.ny, g.nC, nstepsolver, As, G,
                                             moments, amp, edge, dense, w.dense_words, s),
                  who);
   if (rc) return rc;
+  if (det) {
+    unsigned* stat = reinterpret_cast<unsigned*>(ws + w.det_stat_offset);
+    auto* sums = reinterpret_cast<unsigned long long*>(ws + w.det_sums_offset);
+    unsigned* flags = reinterpret_cast<unsigned*>(ws + w.det_flags_offset);
+    rc = check_hip(cpab::launch_fill(reinterpret_cast<float*>(stat),
+                                     (w.total - w.det_stat_offset) / 4, 0.0f, s),
+                   who);
+    hipEvent_t dev_ev = nullptr;
+    const bool dtimed = rc == CPAB_OK && timing && prof_begin(s, &dev_ev);
+    for (int pass = 1; rc == CPAB_OK && pass <= 2; ++pass)
+      rc = check_hip(cpab::launch_backward(g, nP, n_batch, batched ? 1 : 0, nstepsolver, K,
+                                           adaptive, points, stage_points, As, G, amp, nullptr,
+                                           grad_out, moments, nullptr, nullptr, lam, grad_points,
+                                           cfg, s, pass, stat, sums, flags),
+                     who);
+    prof_end(dtimed, dev_ev, "backward", s);
+    if (rc) return rc;
+    rc = check_hip(cpab::launch_finish_moments_det(ndim, rows, g.nC, nP, nstepsolver, stat, sums,
+                                                   flags, As, moments, s),
+                   who);
+    if (rc || !pr.grad_theta || pr.d == 0) return rc;
+    return check_hip(cpab::launch_project(rows, g.nC * g.ppc(), pr.d, moments, pr.col_ptr,
+                                          pr.row_idx, pr.vals, pr.grad_theta, s),
+                     who);
+  }
   hipEvent_t ev = nullptr;
   const bool timed = timing && prof_begin(s, &ev);
   rc = check_hip(cpab::launch_backward(g, nP, n_batch, batched ? 1 : 0, nstepsolver, K, adaptive,
@@ -637,8 +708,11 @@ int cpab_backward_noalloc(int ndim, int64_t nP, int64_t n_theta, int batched, in
   if (adaptive != 0 && adaptive != 1) return fail(CPAB_ERR_INVALID, "adaptive_substeps must be 0 or 1");
   if (n_theta > 0 && nP > 0) {
     cpab::LaunchCfg cfg;
-    if (!backward_cfg(g, nP, n_theta, nstepsolver, adaptive, &cfg)) return CPAB_ERR_DEVICE;
-    const int64_t need = backward_workspace(g, nP, n_theta, 1, cfg).total;
+    const bool det = t_deterministic != 0;
+    if (det ? !det_cfg(g, nP, n_theta, &cfg)
+            : !backward_cfg(g, nP, n_theta, nstepsolver, adaptive, &cfg))
+      return CPAB_ERR_DEVICE;
+    const int64_t need = backward_workspace(g, nP, n_theta, 1, cfg, det).total;
     if (need > kScratchBytes)
       return fail(CPAB_ERR_INVALID,
                   "cpab_backward_noalloc: this problem needs %lld bytes of workspace, beyond the "
@@ -741,9 +815,12 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   CPAB_ALIGNED(As, 16); CPAB_ALIGNED(workspace, 16);
   CPAB_REQUIRE(grad_out); CPAB_REQUIRE(moments);
   hipStream_t s = as_stream(stream);
+  const bool det = t_deterministic != 0;
   cpab::LaunchCfg cfg;
-  if (!backward_cfg(g, img.nP, n_batch, nstepsolver, adaptive, &cfg)) return CPAB_ERR_DEVICE;
-  const BackwardWorkspace w = backward_workspace(g, img.nP, n_batch, 1, cfg);
+  if (det ? !det_cfg(g, img.nP, n_batch, &cfg)
+          : !backward_cfg(g, img.nP, n_batch, nstepsolver, adaptive, &cfg))
+    return CPAB_ERR_DEVICE;
+  const BackwardWorkspace w = backward_workspace(g, img.nP, n_batch, 1, cfg, det);
   if (workspace == nullptr || workspace_bytes < w.total)
     return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
                 (long long)w.total, (long long)workspace_bytes);
@@ -752,27 +829,55 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
   float* partials = reinterpret_cast<float*>(ws + w.partials_offset);
   float* G = reinterpret_cast<float*>(ws + w.g_offset);
   float* amp = reinterpret_cast<float*>(ws + w.amp_offset);
-  cpab::EdgeAcc* edge = ndim == 2 ? reinterpret_cast<cpab::EdgeAcc*>(ws + w.edge_offset) : nullptr;
+  cpab::EdgeAcc* edge =
+      ndim == 2 && !det ? reinterpret_cast<cpab::EdgeAcc*>(ws + w.edge_offset) : nullptr;
+  const char* who = "cpab_transform_data_backward";
   rc = check_hip(cpab::launch_adjoint_table(ndim, n_batch, g.nx, g.ny, g.nC, nstepsolver, As, G,
                                             moments, amp, edge, dense, w.dense_words, s),
-                 "cpab_transform_data_backward");
+                 who);
   if (rc) return rc;
   if (grad_data) {
-    rc = check_hip(cpab::launch_fill(grad_data, n_batch * n_channels * img.plane_in, 0.0f, s),
-                   "cpab_transform_data_backward");
+    rc = check_hip(cpab::launch_fill(grad_data, n_batch * n_channels * img.plane_in, 0.0f, s), who);
     if (rc) return rc;
   }
   hipEvent_t ev = nullptr;
   const bool timed = prof_begin(s, &ev);
+  if (det) {
+    unsigned* stat = reinterpret_cast<unsigned*>(ws + w.det_stat_offset);
+    auto* sums = reinterpret_cast<unsigned long long*>(ws + w.det_sums_offset);
+    unsigned* flags = reinterpret_cast<unsigned*>(ws + w.det_flags_offset);
+    rc = check_hip(cpab::launch_fill(reinterpret_cast<float*>(stat),
+                                     (w.total - w.det_stat_offset) / 4, 0.0f, s),
+                   who);
+    for (int pass = 1; rc == CPAB_OK && pass <= 2; ++pass)
+      rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, axes,
+                                                 final_points, seed_grad, As, G, amp, nullptr,
+                                                 data, grad_out, moments, nullptr, nullptr,
+                                                 grad_data, cfg, s, pass, stat, sums, flags),
+                     who);
+    prof_end(timed, ev, "image_backward", s);
+    if (rc) return rc;
+    rc = check_hip(cpab::launch_finish_moments_det(ndim, n_batch, g.nC, img.nP, nstepsolver, stat,
+                                                   sums, flags, As, moments, s),
+                   who);
+    if (rc || !pr.grad_theta || pr.d == 0) return rc;
+    return check_hip(cpab::launch_project(n_batch, g.nC * g.ppc(), pr.d, moments, pr.col_ptr,
+                                          pr.row_idx, pr.vals, pr.grad_theta, s),
+                     who);
+  }
   rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, axes,
                                              final_points, seed_grad, As, G, amp, edge, data,
                                              grad_out, moments, partials, dense, grad_data, cfg, s),
-                 "cpab_transform_data_backward");
+                 who);
   prof_end(timed, ev, "image_backward", s);
   if (rc) return rc;
-  return finish_and_project("cpab_transform_data_backward", ndim, n_batch, g.nC, cfg, nstepsolver,
-                            partials, dense, As, moments, pr, s);
+  return finish_and_project(who, ndim, n_batch, g.nC, cfg, nstepsolver, partials, dense, As,
+                            moments, pr, s);
 }
+
+void cpab_set_deterministic(int on) { t_deterministic = on ? 1 : 0; }
+
+int cpab_deterministic(void) { return t_deterministic; }
 
 int cpab_project(int64_t n_theta, int D, int d, const float* moments, const int32_t* col_ptr,
                  const int32_t* row_idx, const float* vals, float* grad_theta, void* stream) {

@@ -391,6 +391,22 @@ __device__ __forceinline__ bool edge_safe(const float (&x)[N], const float (&y)[
   return __builtin_amdgcn_ballot_w64(!ok) == 0;
 }
 
+// Scale 2^s of a row's integer sums in the deterministic reduction: `stat`
+// holds the bits of the row's largest |flushed value| (+inf when one was not
+// finite; 0 when all were zero).  A row has at most nP * T flushes (a
+// trajectory flushes at most once per step), so with every value below 2^e,
+// value * 2^s < 2^(62 - lg) and the sum of all of them stays below 2^62.
+// Returns 0 for a non-finite row.
+__device__ __forceinline__ double det_scale(unsigned stat, int64_t nP, int T) {
+  if (stat == 0u) return 1.0;
+  if (stat >= 0x7f800000u) return 0.0;
+  int e;
+  frexpf(__uint_as_float(stat), &e);  // value < 2^e
+  const int64_t n = nP * (int64_t)T;
+  const int lg = n > 1 ? 64 - __builtin_clzll((unsigned long long)(n - 1)) : 0;
+  return ldexp(1.0, 62 - e - lg);
+}
+
 // Issue priority of a wave from its lanes' positions at the start of a
 // trajectory: lanes on or beyond the domain's edge take the lookup's clamping
 // path, and beyond a corner the corner rule too, at most steps, so their

@@ -10,6 +10,18 @@ namespace cpab {
 
 struct EdgeAcc;  // cpab_device.hpp: one part of a row's domain-edge bound (4 doubles)
 constexpr int kEdgeAccBytes = 32;
+// Workgroup size of the deterministic backward passes, and the LDS of their
+// second pass (adjoint.hip): a row's full table of 64-bit sums when it takes at
+// most kDetFullBytes, else a hashed cache of kDetCacheSlots[ndim] cells.
+constexpr int kDetBlock = 256;
+constexpr int64_t kDetFullBytes = 40 << 10;
+constexpr int kDetCacheSlots[4] = {0, 1024, 512, 256};
+constexpr int64_t det_full_bytes_for(int ndim, int nC) {
+  return (int64_t)nC * ndim * (ndim + 1) * 8;
+}
+constexpr int64_t det_cache_bytes_for(int ndim) {
+  return (int64_t)kDetCacheSlots[ndim] * (ndim * (ndim + 1) * 8 + 4);
+}
 
 struct Geometry {
   int ndim;
@@ -67,6 +79,13 @@ hipError_t launch_adjoint_table(int ndim, int64_t rows, int nx, int ny, int nC, 
 hipError_t launch_finish_moments(int ndim, int64_t rows, int nC, int nparts, int T,
                                  const float* partials, const uint64_t* dense_parts,
                                  const float* As, float* moments, hipStream_t s);
+// The same from the deterministic reduction's integer sums and non-finite
+// flags [rows, nC, ppc] and row stats (launch_backward with det_pass 1 then 2,
+// nP trajectories per row).
+hipError_t launch_finish_moments_det(int ndim, int64_t rows, int nC, int64_t nP, int T,
+                                     const unsigned* det_stat, const unsigned long long* det_sums,
+                                     const unsigned* det_flags, const float* As, float* moments,
+                                     hipStream_t s);
 hipError_t launch_sum_batch(int64_t n_theta, int64_t n, const float* src, float* dst, hipStream_t s);
 
 hipError_t launch_forward_1d(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int K,
@@ -93,12 +112,18 @@ hipError_t launch_trace_cells(const Geometry& g, int64_t nP, int64_t n_theta, in
 // full-bin workgroup that touched a quarter of the cells or more, to its
 // partial table [rows, chunks, nC, ppc] with its bit set in dense_parts
 // [rows, ceil(chunks/64)] (zero on entry).  launch_finish_moments follows.
+// det_pass 1, 2: the two passes of the deterministic reduction (segmented
+// body, LDS cell cache of 64-bit integers; det_stat [rows], det_sums
+// [rows, nC, ppc] and det_flags [rows, nC, ppc] zero before pass 1; partials
+// and dense_parts unused), then launch_finish_moments_det.
 hipError_t launch_backward(const Geometry& g, int64_t nP, int64_t n_batch, int batched, int T,
                            int K, int adaptive, const float* points, const float* stage_points,
                            const float* As, const float* G, const float* amp,
                            const EdgeAcc* edge, const float* grad_out, float* moments,
                            float* partials, uint64_t* dense_parts, float* lam, float* grad_points,
-                           const LaunchCfg& cfg, hipStream_t s);
+                           const LaunchCfg& cfg, hipStream_t s, int det_pass = 0,
+                           unsigned* det_stat = nullptr, unsigned long long* det_sums = nullptr,
+                           unsigned* det_flags = nullptr);
 
 // Fused transform_data (image-ordered outputs; see cpab_sample.hpp ImageShape).
 hipError_t launch_image_forward(const Geometry& g, const ImageShape& img, int64_t n_batch, int T,
@@ -113,7 +138,9 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
                                  const EdgeAcc* edge, const float* data,
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
-                                 hipStream_t s);
+                                 hipStream_t s, int det_pass = 0, unsigned* det_stat = nullptr,
+                                 unsigned long long* det_sums = nullptr,
+                                 unsigned* det_flags = nullptr);
 
 hipError_t launch_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
                                  const int64_t* out_size, const float* data, const float* grid,

@@ -126,6 +126,26 @@ int cpab_backward_project(int ndim, int64_t nP, int64_t n_theta, int batched, in
                           float* grad_theta, float* grad_points, void* workspace,
                           int64_t workspace_bytes, void* stream);
 
+/* Deterministic backward, for debugging (no counterpart in the reference,
+ * whose float atomics make the theta gradients vary in their last bits from
+ * run to run: stn/demos/demo_classify_2d.py:7-10).  With on != 0, the backward
+ * entry points called afterwards from the calling thread (cpab_backward,
+ * cpab_backward_project, cpab_backward_noalloc, cpab_chain_backward,
+ * cpab_transform_data_backward) reduce the per-cell sums in two passes over
+ * the trajectories: the first finds each theta row's largest flushed value,
+ * the second adds every value as a 64-bit integer at a per-row power-of-two
+ * scale (integer sums do not depend on their order), so moments, theta
+ * gradients and point adjoints are the same bit for bit on every run on the
+ * same device.  They equal the default mode's to its tolerance (the integer
+ * quantum is 2^-(62 - ceil(log2(nP * nstepsolver))) of the row's largest
+ * value); a component that sums non-finite values is +inf, -inf or NaN as
+ * the float sum would be.  grad_data of cpab_transform_data_backward keeps
+ * its float-atomic scatter.  Both passes take the default's bodies; the
+ * benchmark steps take 1.9-2.9x their default time.  The *_workspace_size
+ * functions size the workspace of the calling thread's current mode. */
+void cpab_set_deterministic(int on);
+int cpab_deterministic(void);
+
 /* Device memory the library keeps per GPU for cpab_backward_noalloc. */
 #define CPAB_NOALLOC_SCRATCH_BYTES (32LL << 20)
 

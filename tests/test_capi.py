@@ -199,3 +199,33 @@ def _check_misaligned_tables_rejected():
     assert rc == 1 and "aligned" in _err(lib)
     rc = lib.cpab_expm(2, 4, 0.02, bad, p, None)
     assert rc == 1 and "aligned" in _err(lib)
+
+
+def test_deterministic_toggle_is_per_thread():
+    # cpab_set_deterministic sets the calling thread's mode only (no HIP call);
+    # Native.deterministic restores the previous mode on exit.
+    import threading
+    lib = _native.load_library()
+    assert lib.cpab_deterministic() == 0
+    lib.cpab_set_deterministic(7)
+    try:
+        assert lib.cpab_deterministic() == 1
+        seen = []
+        t = threading.Thread(target=lambda: seen.append(lib.cpab_deterministic()))
+        t.start()
+        t.join()
+        assert seen == [0]
+    finally:
+        lib.cpab_set_deterministic(0)
+    assert lib.cpab_deterministic() == 0
+    nat = _native.Native()
+    with nat.deterministic(True):
+        assert lib.cpab_deterministic() == 1
+        with nat.deterministic(False):
+            assert lib.cpab_deterministic() == 0
+        assert lib.cpab_deterministic() == 1
+    assert lib.cpab_deterministic() == 0
+    with pytest.raises(ValueError):
+        with nat.deterministic(True):
+            raise ValueError("inside")
+    assert lib.cpab_deterministic() == 0
