@@ -120,7 +120,7 @@ class Cpab(object):
                 the GPU backward reduces its per-cell sums in 64-bit integers
                 over two passes, so theta gradients (and the points' gradient)
                 are bit-identical from run to run on one device (the
-                benchmark steps take 1.9-2.9x their default time;
+                benchmark steps take about twice their default time;
                 transform_data's data gradient keeps its float-atomic scatter)
         """
         assert nstepsolver > 0, 'nstepsolver must be a positive number'

@@ -928,7 +928,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
 // order).  Pass 1 adds every finite flushed value as a 64-bit integer,
 // rint(value * 2^s) with the row's scale 2^s, into LDS (the row's full table
 // or a cell cache) and HBM: integer adds give the same sums in any order.  The scale leaves the
-// sums of all of a row's flushes below 2^62 in magnitude (det_scale), so none
+// sums of all of a row's flushes below 2^62 in magnitude (det_shift), so none
 // overflows; the quantum is 2^-(62 - lg) of the row's largest value, lg =
 // ceil(log2(nP T)).  A non-finite value sets its component's flag instead
 // (bit 0 +inf, bit 1 -inf, bit 2 NaN, an atomic or), and the finish gives
@@ -936,7 +936,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
 // divides the integer sums by the scale.
 // ---------------------------------------------------------------------------
 template <int D> constexpr int kDetSlots = kDetCacheSlots[D];
-constexpr int kDetThreads = kDetBlock;
+template <int D> constexpr int kDetThreads = kDetBlock[D];
 
 // Dynamic LDS of a pass: none for pass 0; for pass 1 the row's full table
 // (FULL, direct-indexed by cell) or the hashed cache of kDetSlots cells.
@@ -960,7 +960,7 @@ struct DetSink {
   unsigned long long* __restrict__ mom;    // HBM sums of this row [nC * P]
   unsigned* wg_max;                        // LDS
   unsigned* __restrict__ flags;            // HBM non-finite flags of this row [nC * P]
-  double scale;
+  int shift;                               // the row's scale exponent (det_shift)
   __device__ __forceinline__ void operator()(int c, const float (&m)[Dim<D>::P]) const {
     constexpr int P = Dim<D>::P;
     if constexpr (PASS == 0) {
@@ -972,14 +972,22 @@ struct DetSink {
                              __HIP_MEMORY_SCOPE_WORKGROUP);
     } else {
       unsigned long long q[P];
+      bool fin = true;
 #pragma unroll
-      for (int k = 0; k < P; ++k) {
-        const bool fin = __builtin_isfinite(m[k]);
-        q[k] = fin ? (unsigned long long)(long long)__builtin_rint((double)m[k] * scale) : 0ull;
-        if (!fin)
-          __hip_atomic_fetch_or(flags + (size_t)c * P + k,
-                                m[k] != m[k] ? 4u : (m[k] > 0.0f ? 1u : 2u), __ATOMIC_RELAXED,
-                                __HIP_MEMORY_SCOPE_AGENT);
+      for (int k = 0; k < P; ++k) fin = fin && __builtin_isfinite(m[k]);
+      if (__builtin_expect(fin, 1)) {
+#pragma unroll
+        for (int k = 0; k < P; ++k) q[k] = det_fixed(m[k], shift);
+      } else {
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+          const bool f = __builtin_isfinite(m[k]);
+          q[k] = f ? det_fixed(m[k], shift) : 0ull;
+          if (!f)
+            __hip_atomic_fetch_or(flags + (size_t)c * P + k,
+                                  m[k] != m[k] ? 4u : (m[k] > 0.0f ? 1u : 2u), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
       if constexpr (FULL) {
 #pragma unroll
@@ -1072,7 +1080,7 @@ __device__ __forceinline__ void det_body(P tab, const float* __restrict__ gtab, 
 }
 
 template <int D, bool ADAPTIVE, int PASS, bool FULL, int TS>
-__global__ __launch_bounds__(kDetThreads) void det_backward_kernel(
+__global__ __launch_bounds__(kDetThreads<D>) void det_backward_kernel(
     int nP, int batched, int T, Cells g, int nC, int K, const float* __restrict__ points,
     const float* __restrict__ stage_points, const float* __restrict__ As,
     const float* __restrict__ Gs, Recover rec, const float* __restrict__ grad_out,
@@ -1097,11 +1105,11 @@ __global__ __launch_bounds__(kDetThreads) void det_backward_kernel(
     io.gout = k == K - 1 ? grad_out + (size_t)b * plane : lam + (size_t)b * plane;
     io.lam_out = k == 0 ? (grad_points ? grad_points + (size_t)b * plane : nullptr)
                         : lam + (size_t)b * plane;
-    const double scale = PASS == 0 ? 0.0 : det_scale(stat[row], nP, T);
+    const int shift = PASS == 0 ? 0 : det_shift(stat[row], nP, T);
     L.begin();
     det_body<D, ADAPTIVE, TS>(
         As + row * R, Gs + row * nC * RevStride<D>::S, nP, T, g, io,
-        DetSink<D, PASS, FULL>{L.keys, L.vals, sums + row * R, L.wg_max, flags + row * R, scale},
+        DetSink<D, PASS, FULL>{L.keys, L.vals, sums + row * R, L.wg_max, flags + row * R, shift},
         rec, row);
     L.end(stat + row, sums + row * R);
     if (k > 0) __syncthreads();
@@ -1109,7 +1117,7 @@ __global__ __launch_bounds__(kDetThreads) void det_backward_kernel(
 }
 
 template <int D, bool ADAPTIVE, int PASS, bool FULL, int TS>
-__global__ __launch_bounds__(kDetThreads) void det_image_backward_kernel(
+__global__ __launch_bounds__(kDetThreads<D>) void det_image_backward_kernel(
     ImageShape s, int T, Cells g, int nC, const float* __restrict__ axes,
     const float* __restrict__ final_points, const float* __restrict__ seed_grad,
     const float* __restrict__ As, const float* __restrict__ Gs, Recover rec,
@@ -1134,12 +1142,12 @@ __global__ __launch_bounds__(kDetThreads) void det_image_backward_kernel(
   io.data = data + (size_t)b * s.C * s.plane_in;
   // grad_data is scattered once, in pass 1
   io.gdata = (PASS == 1 && grad_data) ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
-  const double scale = PASS == 0 ? 0.0 : det_scale(stat[b], s.nP, T);
+  const int shift = PASS == 0 ? 0 : det_shift(stat[b], s.nP, T);
   L.begin();
   det_body<D, ADAPTIVE, TS>(As + (size_t)b * R, Gs + (size_t)b * nC * RevStride<D>::S, s.nP, T, g,
                             io,
                             DetSink<D, PASS, FULL>{L.keys, L.vals, sums + (size_t)b * R, L.wg_max,
-                                                   flags + (size_t)b * R, scale},
+                                                   flags + (size_t)b * R, shift},
                             rec, (size_t)b);
   L.end(stat + b, sums + (size_t)b * R);
 }
@@ -1188,7 +1196,7 @@ hipError_t go_det(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
   const Cells g{j.geo.nx, j.geo.ny, j.geo.nz};
   const Recover rec{j.amp, adjoint_table_blocks(j.geo.nC),
                     (float)std::pow((double)kRecoverGrowth, 1.0 / (double)j.T), nullptr};
-  const dim3 grid((unsigned)cfg.chunks, (unsigned)j.n_batch), block((unsigned)kDetThreads);
+  const dim3 grid((unsigned)cfg.chunks, (unsigned)j.n_batch), block((unsigned)kDetThreads<D>);
   if (j.image) {
     auto kernel = det_image_backward_kernel<D, ADAPTIVE, PASS, FULL, TS>;
     hipError_t e = allow_lds(kernel, lds);

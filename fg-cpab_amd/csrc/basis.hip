@@ -207,7 +207,7 @@ __global__ __launch_bounds__(kTableThreads) void adjoint_table_kernel(
 template <int D> constexpr int kFinCells = 256 / (D * (D + 1));
 
 // DET: S from the deterministic reduction's integer sums, divided by the row's
-// scale (det_scale), or +inf / -inf / NaN where the component's flags record
+// scale 2^det_shift, or +inf / -inf / NaN where the component's flags record
 // non-finite values, in place of the HBM float sums and partials.
 template <int D, bool DET = false>
 __global__ __launch_bounds__(256) void finish_moments_kernel(int64_t rows, int nC, int nblk,
@@ -231,9 +231,9 @@ __global__ __launch_bounds__(256) void finish_moments_kernel(int64_t rows, int n
   const bool live = t < CB * P && c0 + cl < nC;
   const int64_t idx = (row * nC + c0 + cl) * P + comp;   // this thread's float of the row's table
   if (live && DET) {
-    const double scale = det_scale(det_stat[row], det_nP, det_T);
+    const int shift = det_shift(det_stat[row], det_nP, det_T);
     const unsigned f = det_flags[idx];
-    s_lds[t] = f == 0u ? (scale > 0.0 ? (float)((double)(long long)det_sums[idx] / scale) : NAN)
+    s_lds[t] = f == 0u ? (float)ldexp((double)(long long)det_sums[idx], -shift)
                        : (f == 1u ? INFINITY : f == 2u ? -INFINITY : NAN);
     a_lds[t] = As[idx];
   } else if (live) {

@@ -345,17 +345,16 @@ int check_projection(const Projection& pr) {
 }
 
 
-// Launch shape of the deterministic passes: pass 1 keeps the row's full table
-// of 64-bit sums in LDS when it fits in kDetFullBytes (lds_bins), else a
-// hashed cache; about four workgroups per CU (the passes' register use allows
-// four 256-thread workgroups per CU), at most one pass over a row's points.
-// The shape depends only on the device and the problem, so every run groups
-// the trajectories' sums the same way.
+// Launch shape of the deterministic passes (kDetBlock, kDetPerCU): pass 1
+// keeps the row's full table of 64-bit sums in LDS when it fits in
+// kDetFullBytes (lds_bins), else a hashed cache; at most one pass over a row's
+// points.  The shape depends only on the device and the problem, so every run
+// groups the trajectories' sums the same way.
 bool det_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta, cpab::LaunchCfg* out) {
   const DeviceInfo dev = device_info();
   cpab::LaunchCfg c{};
-  c.block = cpab::kDetBlock;
-  c.lds_bins = cpab::det_full_bytes_for(g.ndim, g.nC) <= cpab::kDetFullBytes ? 1 : 0;
+  c.block = cpab::kDetBlock[g.ndim];
+  c.lds_bins = cpab::det_full_bytes_for(g.ndim, g.nC) <= cpab::kDetFullBytes[g.ndim] ? 1 : 0;
   const int64_t lds = c.lds_bins ? cpab::det_full_bytes_for(g.ndim, g.nC)
                                  : cpab::det_cache_bytes_for(g.ndim);
   if (lds + 16 > dev.lds) {
@@ -363,7 +362,7 @@ bool det_cfg(const cpab::Geometry& g, int64_t nP, int64_t n_theta, cpab::LaunchC
          "device has %d", (long long)(lds + 16), dev.lds);
     return false;
   }
-  const int64_t per_cu = 4;
+  const int64_t per_cu = cpab::kDetPerCU[g.ndim];
   int64_t chunks = std::max<int64_t>(1, div_up(dev.cus * per_cu, std::max<int64_t>(n_theta, 1)));
   chunks = std::min(chunks, std::max<int64_t>(1, div_up(nP, c.block)));
   c.chunks = (int)chunks;

@@ -391,20 +391,33 @@ __device__ __forceinline__ bool edge_safe(const float (&x)[N], const float (&y)[
   return __builtin_amdgcn_ballot_w64(!ok) == 0;
 }
 
-// Scale 2^s of a row's integer sums in the deterministic reduction: `stat`
-// holds the bits of the row's largest |flushed value| (+inf when one was not
-// finite; 0 when all were zero).  A row has at most nP * T flushes (a
-// trajectory flushes at most once per step), so with every value below 2^e,
-// value * 2^s < 2^(62 - lg) and the sum of all of them stays below 2^62.
-// Returns 0 for a non-finite row.
-__device__ __forceinline__ double det_scale(unsigned stat, int64_t nP, int T) {
-  if (stat == 0u) return 1.0;
-  if (stat >= 0x7f800000u) return 0.0;
+// Scale exponent s of a row's integer sums in the deterministic reduction:
+// `stat` holds the bits of the row's largest finite |flushed value| (0 when
+// all were zero).  A row has at most nP * T flushes (a trajectory flushes at
+// most once per step), so with every value below 2^e, value * 2^s < 2^(62 - lg)
+// and the sum of all of them stays below 2^62 in magnitude.
+__device__ __forceinline__ int det_shift(unsigned stat, int64_t nP, int T) {
+  if (stat == 0u || stat >= 0x7f800000u) return 0;
   int e;
   frexpf(__uint_as_float(stat), &e);  // value < 2^e
   const int64_t n = nP * (int64_t)T;
   const int lg = n > 1 ? 64 - __builtin_clzll((unsigned long long)(n - 1)) : 0;
-  return ldexp(1.0, 62 - e - lg);
+  return 62 - e - lg;
+}
+
+// rint(v * 2^s) as a two's-complement 64-bit integer, for finite v with
+// |v| 2^s < 2^63.  v * 2^s is exact in float (ldexp), and so is its rounding to
+// an integer; the magnitude a then splits exactly into 32-bit words: the high
+// word floor(a 2^-32) and the low word a - high 2^32, which is below 2^32 and,
+// when a >= 2^32, a multiple of a's ulp (>= 2^9), so it needs at most 23 bits.
+__device__ __forceinline__ unsigned long long det_fixed(float v, int s) {
+  const float x = __builtin_rintf(ldexpf(v, s));
+  const float a = fabsf(x);
+  const float hi = floorf(a * 0x1p-32f);
+  const float lo = fmaf(-hi, 0x1p32f, a);
+  const unsigned long long u =
+      ((unsigned long long)(unsigned)hi << 32) | (unsigned long long)(unsigned)lo;
+  return x < 0.0f ? 0ull - u : u;
 }
 
 // Issue priority of a wave from its lanes' positions at the start of a

@@ -10,11 +10,15 @@ namespace cpab {
 
 struct EdgeAcc;  // cpab_device.hpp: one part of a row's domain-edge bound (4 doubles)
 constexpr int kEdgeAccBytes = 32;
-// Workgroup size of the deterministic backward passes, and the LDS of their
-// second pass (adjoint.hip): a row's full table of 64-bit sums when it takes at
-// most kDetFullBytes, else a hashed cache of kDetCacheSlots[ndim] cells.
-constexpr int kDetBlock = 256;
-constexpr int64_t kDetFullBytes = 40 << 10;
+// Workgroup size and workgroups per CU of the deterministic backward passes,
+// and the LDS of their second pass (adjoint.hip): a row's full table of 64-bit
+// sums when it takes at most kDetFullBytes (an equal share of a CU's 160 KiB),
+// else a hashed cache of kDetCacheSlots cells.  Per ndim: 1D/2D 512 threads,
+// two per CU (16 waves at ~100 VGPRs); 3D 256 threads, four per CU (its
+// ~150 VGPRs leave room for 3 waves per SIMD, which 512-thread groups waste).
+constexpr int kDetBlock[4] = {0, 512, 512, 256};
+constexpr int kDetPerCU[4] = {0, 2, 2, 4};
+constexpr int64_t kDetFullBytes[4] = {0, (80 << 10) - 256, (80 << 10) - 256, (40 << 10) - 256};
 constexpr int kDetCacheSlots[4] = {0, 1024, 512, 256};
 constexpr int64_t det_full_bytes_for(int ndim, int nC) {
   return (int64_t)nC * ndim * (ndim + 1) * 8;

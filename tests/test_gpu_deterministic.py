@@ -30,9 +30,14 @@ def _grid_grads(T, theta, pts, g, cuda):
     return th.grad.cpu().numpy(), x.grad.cpu().numpy()
 
 
+# [20, 20] and [10, 10, 10] take the LDS cell cache in the integer pass; [6, 6]
+# and [3, 3, 3] the row's full table.
 @pytest.mark.parametrize("tess,n,B,adaptive", [([50], 10000, 4, False),
                                                ([20, 20], 20000, 4, False),
                                                ([20, 20], 12000, 3, True),
+                                               ([6, 6], 8000, 2, True),
+                                               ([6, 6], 8000, 2, False),
+                                               ([3, 3, 3], 6000, 2, False),
                                                ([10, 10, 10], 5000, 2, False)])
 def test_transform_grid_repeatable(cuda, tess, n, B, adaptive):
     T = _det_cpab(tess, adaptive)
