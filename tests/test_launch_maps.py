@@ -2,7 +2,8 @@
 here: for every grid shape it must hand out each logical (part, row) exactly
 once, whatever the number of workgroups modulo the 8 XCDs; and at C2's grid
 (16 point ranges x 16 thetas) each XCD must serve 4 thetas over half the
-ranges."""
+ranges.  tests/test_gpu_launch_map.py runs the kernel's own map on the GPU
+over grids of these kinds."""
 
 
 def wg_slot(bx, by, nx, ny, row_block=4):

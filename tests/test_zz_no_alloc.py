@@ -133,3 +133,31 @@ def test_noalloc_under_graph_capture(cuda):
         assert_grad_close(m.cpu().numpy(), ref_m * k, rtol=2e-5)
         assert_adjoint_close(gp.cpu().numpy(), ref_gp * k)
     del graph
+
+
+def test_noalloc_deterministic_is_bitwise(cuda):
+    # In the deterministic mode (cpab_set_deterministic) the allocation-free
+    # entry point runs the same two passes as cpab_backward: moments and point
+    # adjoints equal bit for bit, on two calls in a row, the second smaller.
+    # Scaling grad_out by a power of two scales every flushed value and the
+    # row's scale exactly, so the moments scale exactly too.
+    lib = native()
+    for tess, n_theta, nP, batched, seed in (([20, 20], 4, 20000, False, 311),
+                                             ([4, 4], 2, 300, True, 312)):
+        p, pts, As, g = _case(cuda, tess, n_theta, nP, batched, seed)
+        nd, ppc = p.ndim, p.ndim * (p.ndim + 1)
+        with lib.deterministic(True):
+            ref_m = torch.empty((n_theta, p.nC, ppc), device=cuda)
+            ref_gp = torch.empty((n_theta, nd, nP), device=cuda)
+            ws = torch.empty(lib.backward_workspace_size(nd, nP, n_theta, p.nC),
+                             dtype=torch.uint8, device=cuda)
+            lib.backward(nd, pts, batched, n_theta, nP, 50, p.nc, 0, As, g, ref_m, ref_gp, ws)
+            m = torch.full((n_theta, p.nC, ppc), 7.0, device=cuda)
+            gp = torch.full((n_theta, nd, nP), -3.0, device=cuda)
+            lib.backward_noalloc(nd, pts, batched, n_theta, nP, 50, p.nc, 0, As, g, m, gp)
+            m4 = torch.empty_like(m)
+            lib.backward_noalloc(nd, pts, batched, n_theta, nP, 50, p.nc, 0, As, g * 4.0, m4,
+                                 torch.empty_like(gp))
+        torch.cuda.synchronize()
+        assert torch.equal(m, ref_m) and torch.equal(gp, ref_gp)
+        assert torch.equal(m4, m * 4.0)
