@@ -130,7 +130,7 @@ def setup(cfg, nstep, dev):
 
         traj = pts.shape[1] * theta.shape[0]
         info = {"ndim": T.params.ndim, "traj": traj, "desc": desc,
-                "global_batch": theta.shape[0], "points": pts.shape[1]}
+                "global_batch": theta.shape[0], "points": pts.shape[1], "params": T.params}
         if cfg != "c1":
             info["ref_latency"] = lambda: reference_latency(T, x, th0)
         return step, info
@@ -178,7 +178,7 @@ def setup(cfg, nstep, dev):
         grid_b = B * nd * nP * 4
         interp_bytes = {"interp_forward": grid_b + img + img,
                         "interp_backward": img + grid_b + img + grid_b}
-        return step, {"ndim": nd, "traj": B * nP, "desc": desc, "global_batch": B,
+        return step, {"ndim": nd, "traj": B * nP, "desc": desc, "global_batch": B, "params": T.params,
                       "points": nP, "interp_bytes": interp_bytes, "interp_step": interp_step}
 
     # c5: chain of 8 stages on a 512x512 meshgrid
@@ -203,7 +203,7 @@ def setup(cfg, nstep, dev):
     return step, {"ndim": 2, "traj": nP * K, "points_per_step": nP, "desc":
                   "C5: 2D CPAB transform_grid_chain fwd+MSE+backward, tess [16,16], 8 stages, "
                   "scale_by_dt, 262144 grid points, nstepsolver %d" % nstep,
-                  "global_batch": 1, "points": nP}
+                  "global_batch": 1, "points": nP, "params": T.params}
 
 
 def reference_latency(T, x, th0, n_warmup=10, n_iter=100):
@@ -252,6 +252,29 @@ def reference_latency(T, x, th0, n_warmup=10, n_iter=100):
             "method": "benchmarks/benchmark_transformer.py:71-128 (sync-to-sync mean of 100, "
                       "backward = sum().backward() alone; backward_peak_MiB = allocator peak during "
                       "that backward above the memory allocated before it)"}
+
+
+def deterministic_timing(step, params, steps, warmup):
+    """The same step with ``Cpab.set_solver_params(deterministic_grad=True)``:
+    uninstrumented ms per step, and whether two steps' theta gradients are the
+    same bit for bit (they are not in the default mode's float-atomic sums)."""
+    import torch
+
+    params.deterministic_grad = True
+    try:
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        a, b = step().clone(), step().clone()
+        return {"ms_per_step": round((t1 - t0) * 1e3 / steps, 4),
+                "repeat_bitwise_equal": bool(torch.equal(a, b))}
+    finally:
+        params.deterministic_grad = False
 
 
 def step_memory(step):
@@ -339,6 +362,7 @@ def gpu_bench(cfg, args):
     total = sum(v["work"] * v["per_step"] for v in kern.values())
     out["integrator_tflops_per_step"] = round(total / (ms_step * 1e-3) / 1e12, 3)
     out["memory"] = step_memory(step)
+    out["deterministic"] = deterministic_timing(step, info["params"], args.steps, args.warmup)
     if "ref_latency" in info:
         out["reference_style_latency"] = info["ref_latency"]()
     if "interp_step" in info:
@@ -461,6 +485,7 @@ def line_for(cfg, r, args, cpu):
         "kernels": r["kernels"],
         "integrator_tflops_per_step": r["integrator_tflops_per_step"],
         "memory": r["memory"],
+        "deterministic": r["deterministic"],
     }
     if "reference_style_latency" in r:
         line["reference_style_latency"] = r["reference_style_latency"]

@@ -19,7 +19,7 @@ constexpr int kEdgeAccBytes = 32;
 constexpr int kDetBlock[4] = {0, 512, 512, 256};
 constexpr int kDetPerCU[4] = {0, 2, 2, 4};
 constexpr int64_t kDetFullBytes[4] = {0, (80 << 10) - 256, (80 << 10) - 256, (40 << 10) - 256};
-constexpr int kDetCacheSlots[4] = {0, 1024, 512, 256};
+constexpr int kDetCacheSlots[4] = {0, 1024, 1024, 256};
 constexpr int64_t det_full_bytes_for(int ndim, int nC) {
   return (int64_t)nC * ndim * (ndim + 1) * 8;
 }

@@ -30,11 +30,12 @@ def _grid_grads(T, theta, pts, g, cuda):
     return th.grad.cpu().numpy(), x.grad.cpu().numpy()
 
 
-# [20, 20] and [10, 10, 10] take the LDS cell cache in the integer pass; [6, 6]
-# and [3, 3, 3] the row's full table.
+# [30, 30] and [10, 10, 10] take the LDS cell cache in the integer pass; [20, 20],
+# [6, 6] and [3, 3, 3] the row's full table.
 @pytest.mark.parametrize("tess,n,B,adaptive", [([50], 10000, 4, False),
                                                ([20, 20], 20000, 4, False),
-                                               ([20, 20], 12000, 3, True),
+                                               ([30, 30], 20000, 3, False),
+                                               ([30, 30], 12000, 3, True),
                                                ([6, 6], 8000, 2, True),
                                                ([6, 6], 8000, 2, False),
                                                ([3, 3, 3], 6000, 2, False),
