@@ -1,7 +1,7 @@
 // Device-side building blocks of the CPAB integrator for gfx950 (CDNA4).
 //
 // Everything here is a __forceinline__ helper used by the kernels in
-// integrate.hip / adjoint.hip.  Floating-point operation order is fixed on
+// integrate.hip / adjoint.hip / adjoint_det.hip.  Floating-point operation order is fixed on
 // purpose: the whole library is compiled with -ffp-contract=off, every fused
 // multiply-add is written as fmaf(), and the oracle under oracle/ performs the
 // same sequence so the two agree bit for bit.

@@ -11,7 +11,7 @@ namespace cpab {
 struct EdgeAcc;  // cpab_device.hpp: one part of a row's domain-edge bound (4 doubles)
 constexpr int kEdgeAccBytes = 32;
 // Workgroup size and workgroups per CU of the deterministic backward passes,
-// and the LDS of their second pass (adjoint.hip): a row's full table of 64-bit
+// and the LDS of their second pass (adjoint_det.hip): a row's full table of 64-bit
 // sums when it takes at most kDetFullBytes (an equal share of a CU's 160 KiB),
 // else a hashed cache of kDetCacheSlots cells.  Per ndim: 1D/2D 512 threads,
 // two per CU (16 waves at ~100 VGPRs); 3D 256 threads, four per CU (its

@@ -1,6 +1,6 @@
 """numpy restatement of the 2D domain-edge bound (fg-cpab_amd/csrc/cpab_device.hpp:
 EdgeAcc, edge_bound_cell_2d, midpoint_step_err, midpoint_map_2d, pow_int,
-edge_delta_2d; basis.hip: adjoint_table_kernel; adjoint.hip: row_edge_delta),
+edge_delta_2d; basis.hip: adjoint_table_kernel; backward_body.hpp: row_edge_delta),
 in the device code's float64 operation order.  Test infrastructure only.
 
 delta_T of a theta row: every point whose distance to each domain edge is at

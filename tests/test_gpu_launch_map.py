@@ -1,4 +1,4 @@
-"""The backward's own workgroup map (wg_slot in adjoint.hip), exercised on the
+"""The backward's own workgroup map (wg_slot in backward_body.hpp), exercised on the
 GPU: grids whose workgroup count is not a multiple of the 8 XCDs, row counts
 that leave a partial block of rows, one theta row, and the segmented variant's
 other launch shape.  Outputs are prefilled with NaN, so a (point range, theta

@@ -1,4 +1,4 @@
-"""CPU check of the backward's workgroup map (adjoint.hip, wg_slot), restated
+"""CPU check of the backward's workgroup map (backward_body.hpp, wg_slot), restated
 here: for every grid shape it must hand out each logical (part, row) exactly
 once, whatever the number of workgroups modulo the 8 XCDs; and at C2's grid
 (16 point ranges x 16 thetas) each XCD must serve 4 thetas over half the
