@@ -39,6 +39,7 @@ def _grid_grads(T, theta, pts, g, cuda):
                                                ([6, 6], 8000, 2, True),
                                                ([6, 6], 8000, 2, False),
                                                ([3, 3, 3], 6000, 2, False),
+                                               ([3, 3, 3], 4000, 2, True),
                                                ([10, 10, 10], 5000, 2, False)])
 def test_transform_grid_repeatable(cuda, tess, n, B, adaptive):
     T = _det_cpab(tess, adaptive)
