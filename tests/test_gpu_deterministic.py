@@ -16,9 +16,9 @@ from helpers import (assert_adjoint_close, assert_grad_close, assert_theta_grad_
 pytestmark = pytest.mark.gpu
 
 
-def _det_cpab(tess, adaptive=False):
+def _det_cpab(tess, adaptive=False, nstep=50):
     T = Cpab(list(tess))
-    T.set_solver_params(nstepsolver=50, adaptive_substeps=adaptive, deterministic_grad=True)
+    T.set_solver_params(nstepsolver=nstep, adaptive_substeps=adaptive, deterministic_grad=True)
     return T
 
 
@@ -31,18 +31,20 @@ def _grid_grads(T, theta, pts, g, cuda):
 
 
 # [30, 30] and [10, 10, 10] take the LDS cell cache in the integer pass; [20, 20],
-# [6, 6] and [3, 3, 3] the row's full table.
-@pytest.mark.parametrize("tess,n,B,adaptive", [([50], 10000, 4, False),
-                                               ([20, 20], 20000, 4, False),
-                                               ([30, 30], 20000, 3, False),
-                                               ([30, 30], 12000, 3, True),
-                                               ([6, 6], 8000, 2, True),
-                                               ([6, 6], 8000, 2, False),
-                                               ([3, 3, 3], 6000, 2, False),
-                                               ([3, 3, 3], 4000, 2, True),
-                                               ([10, 10, 10], 5000, 2, False)])
-def test_transform_grid_repeatable(cuda, tess, n, B, adaptive):
-    T = _det_cpab(tess, adaptive)
+# [6, 6] and [3, 3, 3] the row's full table.  nstepsolver 37: the segmented body.
+@pytest.mark.parametrize("tess,n,B,adaptive,nstep", [([50], 10000, 4, False, 50),
+                                                     ([20, 20], 20000, 4, False, 50),
+                                                     ([20, 20], 8000, 2, False, 37),
+                                                     ([30, 30], 20000, 3, False, 50),
+                                                     ([30, 30], 12000, 3, True, 50),
+                                                     ([6, 6], 8000, 2, True, 50),
+                                                     ([6, 6], 8000, 2, False, 50),
+                                                     ([3, 3, 3], 6000, 2, False, 50),
+                                                     ([3, 3, 3], 4000, 2, True, 50),
+                                                     ([10, 10, 10], 5000, 2, False, 50),
+                                                     ([10, 10, 10], 3000, 2, False, 23)])
+def test_transform_grid_repeatable(cuda, tess, n, B, adaptive, nstep):
+    T = _det_cpab(tess, adaptive, nstep)
     nd = len(tess)
     theta = seeded_theta(T, B, 0.5, 300 + nd)
     pts = (np.linspace(0, 1, n, dtype=np.float32)[None] if nd == 1 else uniform_points(nd, n, 301))
@@ -54,7 +56,7 @@ def test_transform_grid_repeatable(cuda, tess, n, B, adaptive):
     assert native().lib.cpab_deterministic() == 0  # the mode does not leak past the backward
     p = T.params
     As = orc.affine(theta, p.basis).reshape(B, p.nC, nd, nd + 1)
-    mom, gp = orc.backward(pts, As, g, p.nc, 50, adaptive=adaptive)
+    mom, gp = orc.backward(pts, As, g, p.nc, nstep, adaptive=adaptive)
     assert_theta_grad_close(gth1, mom.reshape(B, -1), p.basis)
     assert_adjoint_close(gx1, gp.astype(np.float64).sum(0))
 
