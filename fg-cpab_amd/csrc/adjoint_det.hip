@@ -28,10 +28,10 @@ namespace {
 // largest finite |flushed value| (an atomic max: the same result in any
 // order).  Pass 1 adds every finite flushed value as a 64-bit integer,
 // rint(value * 2^s) with the row's scale 2^s, into LDS (the row's full table
-// or a cell cache) and HBM: integer adds give the same sums in any order.  The scale leaves the
-// sums of all of a row's flushes below 2^62 in magnitude (det_shift), so none
-// overflows; the quantum is 2^-(62 - lg) of the row's largest value, lg =
-// ceil(log2(nP T)).  A non-finite value sets its component's flag instead
+// or a cell cache) and HBM: integer adds give the same sums in any order.
+// The scale leaves the sums of all of a row's flushes below 2^62 in magnitude
+// (det_shift), so none overflows; the quantum is 2^-(62 - lg) of the row's
+// largest value, lg = ceil(log2(nP T)).  A non-finite value sets its component's flag instead
 // (bit 0 +inf, bit 1 -inf, bit 2 NaN, an atomic or), and the finish gives
 // that component the float sum's result: +inf, -inf or NaN.  The finish
 // divides the integer sums by the scale.

@@ -210,16 +210,12 @@ template <int D> constexpr int kFinCells = 256 / (D * (D + 1));
 // scale 2^det_shift, or +inf / -inf / NaN where the component's flags record
 // non-finite values, in place of the HBM float sums and partials.
 template <int D, bool DET = false>
-__global__ __launch_bounds__(256) void finish_moments_kernel(int64_t rows, int nC, int nblk,
-                                                             int nparts, float h,
-                                                             const float* __restrict__ partials,
-                                                             const uint64_t* __restrict__ dense_parts,
-                                                             const float* __restrict__ As,
-                                                             float* __restrict__ moments,
-                                                             const unsigned* __restrict__ det_stat = nullptr,
-                                                             const unsigned long long* __restrict__ det_sums = nullptr,
-                                                             const unsigned* __restrict__ det_flags = nullptr,
-                                                             int64_t det_nP = 0, int det_T = 0) {
+__global__ __launch_bounds__(256) void finish_moments_kernel(
+    int64_t rows, int nC, int nblk, int nparts, float h, const float* __restrict__ partials,
+    const uint64_t* __restrict__ dense_parts, const float* __restrict__ As,
+    float* __restrict__ moments, const unsigned* __restrict__ det_stat,
+    const unsigned long long* __restrict__ det_sums, const unsigned* __restrict__ det_flags,
+    int64_t det_nP, int det_T) {
   constexpr int P = D * (D + 1);
   constexpr int W = D + 1;
   constexpr int CB = kFinCells<D>;
