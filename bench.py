@@ -13,7 +13,9 @@ Prints one JSON line per config with, besides the throughput,
   roofline      the dominant kernel: algorithmic work per launch (fp32 FLOPs, or
                 bytes for the resampling kernels) over its average duration,
                 timed with HIP events that the library records on the launch
-                stream around every launch during the timed steps;
+                stream around every launch, in a separate run of the same
+                number of steps (the timed steps run uninstrumented, last,
+                after the other measurements have kept the GPU busy);
   cpu_baseline  the reference-semantics CPU restatement (oracle/, C + OpenMP)
                 timed on this host on a bounded sample of the same workload
                 (default config only).
@@ -298,17 +300,32 @@ FLOP_KIND = {"forward": "forward", "backward": "backward", "image_forward": "for
              "image_backward": "backward"}
 
 
-def timed_steps(step, steps, warmup):
-    """(seconds for `steps` steps after `warmup`, {kernel: (total ms, launches)}).
-
-    The wall time comes from steps run without instrumentation.  The kernel
-    durations come from the same number of steps run right after, with the
-    library's HIP-event timing on: each event the library records on the launch
-    stream leaves the GPU idle for a few microseconds between kernels (about
-    5.5 us per timed kernel on MI355X), which would otherwise count against the
-    step's throughput."""
+def kernel_timing(step, steps, warmup):
+    """{kernel: (total ms, launches)} over ``steps`` steps run after ``warmup``
+    ones with the library's HIP-event timing on.  Those events leave the GPU
+    idle for a few microseconds between kernels (about 5.5 us per timed kernel
+    on MI355X), so the wall time comes from separate, uninstrumented steps
+    (wall_time)."""
     import torch
     from cpab.pytorch import _native
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    for n in NAMES:
+        _native.profile_read(n)
+    _native.profile_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    _native.profile_enable(False)
+    return {n: _native.profile_read(n) for n in NAMES}
+
+
+def wall_time(step, steps, warmup):
+    """Seconds for exactly ``steps`` uninstrumented steps after ``warmup``
+    untimed ones, bracketed by device synchronisations."""
+    import torch
 
     for _ in range(warmup):
         step()
@@ -319,14 +336,7 @@ def timed_steps(step, steps, warmup):
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     assert torch.isfinite(g).all()
-    for n in NAMES:
-        _native.profile_read(n)
-    _native.profile_enable(True)
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    _native.profile_enable(False)
-    return t1 - t0, {n: _native.profile_read(n) for n in NAMES}
+    return t1 - t0
 
 
 def gpu_bench(cfg, args):
@@ -334,7 +344,27 @@ def gpu_bench(cfg, args):
 
     dev = torch.device("cuda:0")
     step, info = setup(cfg, args.nstep, dev)
-    secs, timing = timed_steps(step, args.steps, args.warmup)
+    # The bench's other measurements first, the kernel timing and the timed
+    # steps last: the GPU then comes to them busy, at its sustained clocks (from
+    # a cold start the first few tens of steps run ~5 % slower).
+    extras = {"memory": step_memory(step),
+              "deterministic": deterministic_timing(step, info["params"], args.steps,
+                                                    args.warmup)}
+    if "ref_latency" in info:
+        extras["reference_style_latency"] = info["ref_latency"]()
+    if "interp_step" in info:
+        # HBM roofline of the standalone resampling kernels on this workload's shapes
+        itiming = kernel_timing(info["interp_step"], args.steps, args.warmup)
+        for n, nbytes in info["interp_bytes"].items():
+            ms, cnt = itiming[n]
+            if cnt:
+                rate = nbytes / (ms / cnt * 1e-3) / 1e9
+                extras.setdefault("interp_roofline", {})[n] = {
+                    "avg_ms": round(ms / cnt, 5), "achieved_GBs": round(rate, 1),
+                    "peak_GBs": PEAK_HBM_GBS, "frac": round(rate / PEAK_HBM_GBS, 4),
+                    "algorithmic_bytes": nbytes, "traffic": profiled_traffic(cfg, n)}
+    timing = kernel_timing(step, args.steps, args.warmup)
+    secs = wall_time(step, args.steps, args.warmup)
     ms_step = secs * 1e3 / args.steps
     nd, traj, T = info["ndim"], info["traj"], args.nstep
     kern = {}
@@ -361,21 +391,7 @@ def gpu_bench(cfg, args):
                            v["unit"]: round(v["rate"], 3)} for k, v in kern.items()}}
     total = sum(v["work"] * v["per_step"] for v in kern.values())
     out["integrator_tflops_per_step"] = round(total / (ms_step * 1e-3) / 1e12, 3)
-    out["memory"] = step_memory(step)
-    out["deterministic"] = deterministic_timing(step, info["params"], args.steps, args.warmup)
-    if "ref_latency" in info:
-        out["reference_style_latency"] = info["ref_latency"]()
-    if "interp_step" in info:
-        # HBM roofline of the standalone resampling kernels on this workload's shapes
-        _, itiming = timed_steps(info["interp_step"], args.steps, args.warmup)
-        for n, nbytes in info["interp_bytes"].items():
-            ms, cnt = itiming[n]
-            if cnt:
-                rate = nbytes / (ms / cnt * 1e-3) / 1e9
-                out.setdefault("interp_roofline", {})[n] = {
-                    "avg_ms": round(ms / cnt, 5), "achieved_GBs": round(rate, 1),
-                    "peak_GBs": PEAK_HBM_GBS, "frac": round(rate / PEAK_HBM_GBS, 4),
-                    "algorithmic_bytes": nbytes, "traffic": profiled_traffic(cfg, n)}
+    out.update(extras)
     return out
 
 
