@@ -141,7 +141,7 @@ int cpab_backward_project(int ndim, int64_t nP, int64_t n_theta, int batched, in
  * value); a component that sums non-finite values is +inf, -inf or NaN as
  * the float sum would be.  grad_data of cpab_transform_data_backward keeps
  * its float-atomic scatter.  Both passes take the default's bodies; the
- * benchmark steps take 1.8-2.1x their default time.  The *_workspace_size
+ * benchmark steps take 1.8-2.2x their default time.  The *_workspace_size
  * functions size the workspace of the calling thread's current mode. */
 void cpab_set_deterministic(int on);
 int cpab_deterministic(void);
