@@ -117,11 +117,11 @@ class Cpab(object):
             nstepsolver: int, number of integration steps
             adaptive_substeps: bool, Heun correction when a step crosses a cell
             deterministic_grad: bool (an addition to the reference's arguments),
-                the GPU backward reduces its per-cell sums in 64-bit integers
-                over two passes, so theta gradients (and the points' gradient)
-                are bit-identical from run to run on one device (the
-                benchmark steps take about twice their default time;
-                transform_data's data gradient keeps its float-atomic scatter)
+                the GPU backward reduces its per-cell sums (and
+                transform_data's data gradient) in 64-bit integers over two
+                passes, so theta, point and data gradients are bit-identical
+                from run to run on one device (the benchmark steps take about
+                twice their default time)
         """
         assert nstepsolver > 0, 'nstepsolver must be a positive number'
         assert type(nstepsolver) == int, 'nstepsolver must be integer'

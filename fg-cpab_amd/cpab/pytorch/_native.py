@@ -54,6 +54,7 @@ _SIGNATURES = {
                                              _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
                                              _c_vp, _c_vp, _c_vp, _c_vp]),
     "cpab_transform_data_backward_workspace_size": (_c_i64, [_c_int, _c_i64, _c_vp, _c_int]),
+    "cpab_transform_data_backward_data_workspace_size": (_c_i64, [_c_int, _c_i64, _c_i64, _c_vp]),
     "cpab_transform_data_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int,
                                               _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
                                               _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
@@ -247,6 +248,12 @@ class Native:
     def transform_data_backward_workspace_size(self, ndim, n_batch, outsize, nC):
         return int(self.lib.cpab_transform_data_backward_workspace_size(
             ndim, n_batch, _lengths(outsize), nC))
+
+    def transform_data_backward_data_workspace_size(self, ndim, data):
+        """Extra workspace bytes for grad_data in this thread's current mode
+        (0 unless deterministic)."""
+        return int(self.lib.cpab_transform_data_backward_data_workspace_size(
+            ndim, data.shape[0], data.shape[1], _lengths(data.shape[2:])))
 
     def transform_data_backward(self, ndim, data, axes, outsize, T, nc, adaptive, final_points,
                                 As, grad_out, moments, grad_data, workspace, tab=None,

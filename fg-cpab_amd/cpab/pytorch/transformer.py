@@ -358,6 +358,8 @@ class _CPABImageFunction(torch.autograd.Function):
             grad_theta = torch.empty((n, tab["d"]), device=dev, dtype=torch.float32)
         with lib.deterministic(_deterministic(params)):
             ws_bytes = lib.transform_data_backward_workspace_size(ndim, n, ctx.outsize, nC)
+            if grad_data is not None:
+                ws_bytes += lib.transform_data_backward_data_workspace_size(ndim, data)
             ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
             lib.transform_data_backward(ndim, data, axes, ctx.outsize, ctx.T, ctx.nc,
                                         ctx.adaptive, final, As, grad, moments, grad_data, ws,

@@ -142,7 +142,7 @@ __global__ __launch_bounds__((kBwdThreads<D, ADAPTIVE, TS>)) void image_backward
   io.sgrad = seed_grad ? seed_grad + (size_t)b * D * s.nP : nullptr;
   io.gout = grad_out + (size_t)b * s.C * s.nP;
   io.data = data + (size_t)b * s.C * s.plane_in;
-  io.gdata = grad_data ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
+  io.gdata = FloatScatter{grad_data ? grad_data + (size_t)b * s.C * s.plane_in : nullptr};
   const float delta = stage_delta<D, ADAPTIVE, TS>(rec, (size_t)b, g);
   L.begin(Ag, Gg, R, nC * RevStride<D>::S, &touched_cnt);
   run_stage<D, ADAPTIVE, LDS_A, BINS, TS>(L, Ag, Gg, s.nP, T, g, io, moments + (size_t)b * R, rec,
@@ -277,12 +277,15 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
                                  const float* grad_out, float* moments, float* partials,
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
                                  hipStream_t s, int det_pass, unsigned* det_stat,
-                                 unsigned long long* det_sums, unsigned* det_flags) {
+                                 unsigned long long* det_sums, unsigned* det_flags,
+                                 const unsigned* det_gstat, unsigned long long* det_gsums) {
   BackwardJob j{};
   j.det_pass = det_pass;
   j.det_stat = det_stat;
   j.det_sums = det_sums;
   j.det_flags = det_flags;
+  j.det_gstat = det_gstat;
+  j.det_gsums = det_gsums;
   j.edge = edge;
   j.geo = g;
   j.nP = img.nP;

@@ -163,6 +163,36 @@ struct DetLds {
   }
 };
 
+// grad_data of the deterministic image backward (pass 1): every finite
+// contribution added as a 64-bit integer rint(v * 2^shift) into `q`, the
+// batch row's integer sums, at the row's scale; a non-finite one as a float
+// atomic into grad_data itself (`f`, zero before), whose sum of +inf, -inf and
+// NaN terms is the same in any order.  det_data_finish adds the two.
+struct FixedScatter {
+  unsigned long long* __restrict__ q;
+  float* __restrict__ f;
+  int shift;
+  __device__ __forceinline__ bool on() const { return q != nullptr; }
+  __device__ __forceinline__ FixedScatter channel(int64_t off) const {
+    return {q + off, f + off, shift};
+  }
+  __device__ __forceinline__ void add(int i, float v) const {
+    if (__builtin_isfinite(v))
+      __hip_atomic_fetch_add(q + i, det_fixed(v, shift), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    else
+      add_at(f, i, v);
+  }
+};
+
+// The largest finite |contribution| of a scatter, through the same arithmetic.
+struct AbsMaxSink {
+  float* m;
+  __device__ __forceinline__ void add(int, float v) const {
+    if (__builtin_isfinite(v)) *m = fmaxf(*m, fabsf(v));
+  }
+};
+
 // A deterministic pass's body: the register variant where the default
 // backward takes it (T == TS > 0; without adaptive substeps only for rows whose
 // positions may be recovered), else the segmented one.
@@ -225,7 +255,8 @@ __global__ __launch_bounds__(kDetThreads<D>) void det_image_backward_kernel(
     const float* __restrict__ data,
     const float* __restrict__ grad_out, unsigned* __restrict__ stat,
     unsigned long long* __restrict__ sums, unsigned* __restrict__ flags,
-    float* __restrict__ grad_data) {
+    float* __restrict__ grad_data, const unsigned* __restrict__ gstat,
+    unsigned long long* __restrict__ gsums) {
   extern __shared__ __align__(16) unsigned long long det_lds[];
   __shared__ unsigned wg_max;
   constexpr int P = Dim<D>::P;
@@ -234,15 +265,19 @@ __global__ __launch_bounds__(kDetThreads<D>) void det_image_backward_kernel(
   const WgSlot w = wg_slot();
   const int b = w.row;
   const int R = nC * P;
-  ImageIO<D> io;
+  ImageIO<D, FixedScatter> io;
   io.s = s;
   io.axes = axes;
   io.fin = final_points ? final_points + (size_t)b * D * s.nP : nullptr;
   io.sgrad = seed_grad ? seed_grad + (size_t)b * D * s.nP : nullptr;
   io.gout = grad_out + (size_t)b * s.C * s.nP;
   io.data = data + (size_t)b * s.C * s.plane_in;
-  // grad_data is scattered once, in pass 1
-  io.gdata = (PASS == 1 && grad_data) ? grad_data + (size_t)b * s.C * s.plane_in : nullptr;
+  // grad_data is scattered once, in pass 1, at the batch row's scale for at
+  // most 2^D contributions per output position into one element
+  const size_t goff = (size_t)b * s.C * s.plane_in;
+  io.gdata = (PASS == 1 && grad_data)
+                 ? FixedScatter{gsums + goff, grad_data + goff, det_shift(gstat[b], s.nP, 1 << D)}
+                 : FixedScatter{nullptr, nullptr, 0};
   const int shift = PASS == 0 ? 0 : det_shift(stat[b], s.nP, T);
   L.begin();
   det_body<D, ADAPTIVE, TS>(As + (size_t)b * R, Gs + (size_t)b * nC * RevStride<D>::S, s.nP, T, g,
@@ -266,7 +301,8 @@ hipError_t go_det(const BackwardJob& j, const LaunchCfg& cfg, hipStream_t s) {
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, grid, block, lds, s, *j.image, j.T, g, j.geo.nC, j.axes,
                        j.final_points, j.seed_grad, j.As, j.G, rec, j.data, j.grad_out,
-                       j.det_stat, j.det_sums, j.det_flags, j.grad_data);
+                       j.det_stat, j.det_sums, j.det_flags, j.grad_data, j.det_gstat,
+                       j.det_gsums);
   } else {
     auto kernel = det_backward_kernel<D, ADAPTIVE, PASS, FULL, TS>;
     hipError_t e = allow_lds(kernel, lds);
@@ -309,7 +345,77 @@ hipError_t dispatch_det(const BackwardJob& j, int adaptive, const LaunchCfg& cfg
                   : go_det_steps<D, false, 1, false>(j, cfg, s);
 }
 
+// gstat[b]: the bits of the largest finite |contribution| of batch row b's
+// grad_data scatter (the scatter's own arithmetic, AbsMaxSink), over every
+// output position and channel; zero before.  One thread per output position.
+template <int D>
+__global__ __launch_bounds__(256) void det_data_stat_kernel(ImageShape s,
+                                                            const float* __restrict__ fin,
+                                                            const float* __restrict__ gout,
+                                                            unsigned* __restrict__ gstat) {
+  const int b = blockIdx.y;
+  float m = 0.0f;
+  const float* fb = fin + (size_t)b * D * s.nP;
+  const float* gb = gout + (size_t)b * s.C * s.nP;
+  for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < s.nP; q += gridDim.x * blockDim.x) {
+    const Axis ax = axis_of(fb[q], s.in[0]);
+    const Axis ay = D >= 2 ? axis_of(fb[q + (size_t)s.nP], s.in[1]) : Axis{0, 0, 0.0f};
+    const Axis az = D == 3 ? axis_of(fb[q + 2 * (size_t)s.nP], s.in[2]) : Axis{0, 0, 0.0f};
+    for (int c = 0; c < s.C; ++c)
+      scatter_to<D>(s.in, AbsMaxSink{&m}, ax, ay, az, gb[(size_t)c * s.nP + q]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (__lane_id() == 0 && m > 0.0f)
+    __hip_atomic_fetch_max(gstat + b, __float_as_uint(m), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// grad_data[b, i] = gsums[b, i] / 2^shift_b + grad_data[b, i] (the non-finite
+// contributions' float sum, else zero).
+__global__ __launch_bounds__(256) void det_data_finish_kernel(int64_t per_row, int nP, int ndim,
+                                                              const unsigned* __restrict__ gstat,
+                                                              const unsigned long long* __restrict__ gsums,
+                                                              float* __restrict__ grad_data) {
+  const int b = blockIdx.y;
+  const int shift = det_shift(gstat[b], nP, 1 << ndim);
+  const size_t base = (size_t)b * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < per_row;
+       i += (int64_t)gridDim.x * blockDim.x)
+    grad_data[base + i] =
+        (float)ldexp((double)(long long)gsums[base + i], -shift) + grad_data[base + i];
+}
+
 }  // namespace
+
+hipError_t launch_det_data_stat(int ndim, const ImageShape& img, int64_t n_batch,
+                                const float* final_points, const float* grad_out,
+                                unsigned* gstat, hipStream_t s) {
+  if (n_batch <= 0 || img.nP <= 0) return hipSuccess;
+  const dim3 grid((unsigned)std::min<int64_t>(((int64_t)img.nP + 255) / 256, 1024),
+                  (unsigned)n_batch);
+  if (ndim == 1)
+    hipLaunchKernelGGL(det_data_stat_kernel<1>, grid, dim3(256), 0, s, img, final_points, grad_out,
+                       gstat);
+  else if (ndim == 2)
+    hipLaunchKernelGGL(det_data_stat_kernel<2>, grid, dim3(256), 0, s, img, final_points, grad_out,
+                       gstat);
+  else
+    hipLaunchKernelGGL(det_data_stat_kernel<3>, grid, dim3(256), 0, s, img, final_points, grad_out,
+                       gstat);
+  return hipGetLastError();
+}
+
+hipError_t launch_det_data_finish(int ndim, const ImageShape& img, int64_t n_batch,
+                                  const unsigned* gstat, const unsigned long long* gsums,
+                                  float* grad_data, hipStream_t s) {
+  const int64_t per_row = (int64_t)img.C * img.plane_in;
+  if (n_batch <= 0 || per_row <= 0) return hipSuccess;
+  const dim3 grid((unsigned)std::min<int64_t>((per_row + 255) / 256, 4096), (unsigned)n_batch);
+  hipLaunchKernelGGL(det_data_finish_kernel, grid, dim3(256), 0, s, per_row, img.nP, ndim, gstat,
+                     gsums, grad_data);
+  return hipGetLastError();
+}
 
 hipError_t dispatch_det_any(const BackwardJob& j, int adaptive, const LaunchCfg& cfg,
                             hipStream_t s) {

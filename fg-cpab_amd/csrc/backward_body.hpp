@@ -32,6 +32,9 @@ struct BackwardJob {
   unsigned* det_stat;
   unsigned long long* det_sums;
   unsigned* det_flags;
+  // and of grad_data (the image backward): batch rows' scales and integer sums
+  const unsigned* det_gstat;
+  unsigned long long* det_gsums;
 };
 
 
@@ -344,8 +347,9 @@ struct PlainIO {
 // seed reads in 64-byte runs.  Otherwise 1D/2D walk the points in image order
 // (coalesced seed reads) and 3D in meshgrid order (lanes along coordinate 0:
 // fewer cells per wave than image order, strided seed reads).  Start points
-// come from the per-axis coordinate vectors either way.
-template <int D>
+// come from the per-axis coordinate vectors either way.  GS: where the seed's
+// corner scatter adds grad_data (FloatScatter: float atomics).
+template <int D, typename GS = FloatScatter>
 struct ImageIO {
   static constexpr bool kMeshOrder = D == 3;
   ImageShape s;
@@ -355,7 +359,7 @@ struct ImageIO {
                                     // grad_data), or null
   const float* __restrict__ gout;   // [C, nP] image gradient of this theta
   const float* __restrict__ data;   // [C, plane_in]
-  float* __restrict__ gdata;        // [C, plane_in] or null
+  GS gdata;                         // [C, plane_in], off (on() false) without grad_data
   __device__ __forceinline__ void walk_index(int i, int (&ix)[3]) const {
     if (D >= 2 && s.walk_tiles) tile_index<D>(s, i, ix);
     else if (kMeshOrder) mesh_index<D>(s, i, ix);
@@ -388,9 +392,12 @@ struct ImageIO {
     const Axis ay = D >= 2 ? axis_of(fin[q + (size_t)s.nP], s.in[1]) : Axis{0, 0, 0.0f};
     const Axis az = D == 3 ? axis_of(fin[q + 2 * (size_t)s.nP], s.in[2]) : Axis{0, 0, 0.0f};
     float dd[3] = {0.0f, 0.0f, 0.0f};
-    for (int c = 0; c < s.C; ++c)
-      sample_grad<D>(s.in, data + c * s.plane_in, ax, ay, az, gout[(size_t)c * s.nP + q], dd,
-                     (gdata && valid) ? gdata + c * s.plane_in : nullptr);
+    const bool scatter = gdata.on() && valid;
+    for (int c = 0; c < s.C; ++c) {
+      const GS gc = scatter ? gdata.channel(c * s.plane_in) : gdata;
+      sample_grad_to<D>(s.in, data + c * s.plane_in, ax, ay, az, gout[(size_t)c * s.nP + q], dd,
+                        scatter ? &gc : nullptr);
+    }
 #pragma unroll
     for (int k = 0; k < D; ++k) lam[k] = dd[k] * (float)(s.in[k] - 1);
   }

@@ -780,6 +780,35 @@ int64_t cpab_transform_data_backward_workspace_size(int ndim, int64_t n_batch,
   return workspace_size_impl(ndim, nP, n_batch, 1, nC);
 }
 
+// The deterministic grad_data's part of the transform_data backward's
+// workspace, after backward_workspace(...).total: batch rows' scales [n_batch]
+// and 64-bit sums [n_batch, n_channels, plane_in].
+struct DataWorkspace {
+  int64_t gstat_offset, gsums_offset, total;
+};
+
+DataWorkspace data_workspace(int64_t base, int64_t n_batch, int64_t n_channels, int64_t plane_in) {
+  DataWorkspace d{};
+  d.gstat_offset = align_up(base);
+  d.gsums_offset = align_up(d.gstat_offset + n_batch * 4);
+  d.total = d.gsums_offset + n_batch * n_channels * plane_in * 8;
+  return d;
+}
+
+int64_t cpab_transform_data_backward_data_workspace_size(int ndim, int64_t n_batch,
+                                                         int64_t n_channels,
+                                                         const int64_t* in_size) {
+  if (!t_deterministic || ndim < 1 || ndim > 3 || n_batch <= 0 || n_channels <= 0 || !in_size)
+    return 0;
+  int64_t plane = 1;
+  for (int k = 0; k < ndim; ++k) {
+    if (in_size[k] <= 0) return 0;
+    plane *= in_size[k];
+  }
+  // the slack covers the two alignments after any base size
+  return data_workspace(0, n_batch, n_channels, plane).total + 2 * kAlign;
+}
+
 int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
                                  const int64_t* in_size, const int64_t* out_size, int nstepsolver,
                                  int ncx, int ncy, int ncz, int adaptive, const float* axes,
@@ -820,9 +849,17 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
           : !backward_cfg(g, img.nP, n_batch, nstepsolver, adaptive, &cfg))
     return CPAB_ERR_DEVICE;
   const BackwardWorkspace w = backward_workspace(g, img.nP, n_batch, 1, cfg, det);
-  if (workspace == nullptr || workspace_bytes < w.total)
-    return fail(CPAB_ERR_INVALID, "workspace too small: need %lld bytes, got %lld",
-                (long long)w.total, (long long)workspace_bytes);
+  // the deterministic grad_data's sums follow
+  const bool det_data = det && grad_data != nullptr;
+  const DataWorkspace dw = data_workspace(w.total, n_batch, n_channels, img.plane_in);
+  const int64_t need = det_data ? dw.total : w.total;
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(CPAB_ERR_INVALID,
+                "workspace too small: need %lld bytes, got %lld%s", (long long)need,
+                (long long)workspace_bytes,
+                det_data ? " (cpab_transform_data_backward_workspace_size plus "
+                           "cpab_transform_data_backward_data_workspace_size)"
+                         : "");
   char* ws = static_cast<char*>(workspace);
   uint64_t* dense = reinterpret_cast<uint64_t*>(ws);
   float* partials = reinterpret_cast<float*>(ws + w.partials_offset);
@@ -845,16 +882,27 @@ int cpab_transform_data_backward(int ndim, int64_t n_batch, int64_t n_channels,
     unsigned* stat = reinterpret_cast<unsigned*>(ws + w.det_stat_offset);
     auto* sums = reinterpret_cast<unsigned long long*>(ws + w.det_sums_offset);
     unsigned* flags = reinterpret_cast<unsigned*>(ws + w.det_flags_offset);
+    unsigned* gstat = det_data ? reinterpret_cast<unsigned*>(ws + dw.gstat_offset) : nullptr;
+    auto* gsums =
+        det_data ? reinterpret_cast<unsigned long long*>(ws + dw.gsums_offset) : nullptr;
     rc = check_hip(cpab::launch_fill(reinterpret_cast<float*>(stat),
-                                     (w.total - w.det_stat_offset) / 4, 0.0f, s),
+                                     (need - w.det_stat_offset) / 4, 0.0f, s),
                    who);
+    if (rc == CPAB_OK && det_data)
+      rc = check_hip(cpab::launch_det_data_stat(ndim, img, n_batch, final_points, grad_out, gstat,
+                                                s),
+                     who);
     for (int pass = 1; rc == CPAB_OK && pass <= 2; ++pass)
       rc = check_hip(cpab::launch_image_backward(g, img, n_batch, nstepsolver, adaptive, axes,
                                                  final_points, seed_grad, As, G, amp, nullptr,
                                                  data, grad_out, moments, nullptr, nullptr,
-                                                 grad_data, cfg, s, pass, stat, sums, flags),
+                                                 grad_data, cfg, s, pass, stat, sums, flags,
+                                                 gstat, gsums),
                      who);
     prof_end(timed, ev, "image_backward", s);
+    if (rc == CPAB_OK && det_data)
+      rc = check_hip(cpab::launch_det_data_finish(ndim, img, n_batch, gstat, gsums, grad_data, s),
+                     who);
     if (rc) return rc;
     rc = check_hip(cpab::launch_finish_moments_det(ndim, n_batch, g.nC, img.nP, nstepsolver, stat,
                                                    sums, flags, As, moments, s),

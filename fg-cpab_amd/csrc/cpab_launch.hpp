@@ -144,7 +144,19 @@ hipError_t launch_image_backward(const Geometry& g, const ImageShape& img, int64
                                  uint64_t* dense_parts, float* grad_data, const LaunchCfg& cfg,
                                  hipStream_t s, int det_pass = 0, unsigned* det_stat = nullptr,
                                  unsigned long long* det_sums = nullptr,
-                                 unsigned* det_flags = nullptr);
+                                 unsigned* det_flags = nullptr, const unsigned* det_gstat = nullptr,
+                                 unsigned long long* det_gsums = nullptr);
+// Deterministic grad_data of the image backward: det_gstat [n_batch] (zero
+// before) gets each batch row's largest finite |scatter contribution| from the
+// final points and grad_out; det pass 2 of launch_image_backward then adds the
+// contributions as 64-bit integers into det_gsums [n_batch, C, plane_in] (zero
+// before), and launch_det_data_finish adds their float value into grad_data.
+hipError_t launch_det_data_stat(int ndim, const ImageShape& img, int64_t n_batch,
+                                const float* final_points, const float* grad_out,
+                                unsigned* det_gstat, hipStream_t s);
+hipError_t launch_det_data_finish(int ndim, const ImageShape& img, int64_t n_batch,
+                                  const unsigned* det_gstat, const unsigned long long* det_gsums,
+                                  float* grad_data, hipStream_t s);
 
 hipError_t launch_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
                                  const int64_t* out_size, const float* data, const float* grid,

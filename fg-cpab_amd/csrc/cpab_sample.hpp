@@ -249,22 +249,32 @@ __device__ __forceinline__ void blend_grad(const float* c, const Axis& ax, const
   dxyz[2] += g * gz;
 }
 
-// The corner scatter of grad_data: g times each corner's weight added into gd.
-template <int ND>
-__device__ __forceinline__ void scatter(const int* in, float* __restrict__ gd, const Axis& ax,
-                                        const Axis& ay, const Axis& az, float g) {
+// Where the corner scatter of grad_data adds: float atomics into one channel's
+// plane (the deterministic backward brings its own sink with the same add()).
+struct FloatScatter {
+  float* __restrict__ p;
+  __device__ __forceinline__ bool on() const { return p != nullptr; }
+  __device__ __forceinline__ FloatScatter channel(int64_t off) const { return {p + off}; }
+  __device__ __forceinline__ void add(int i, float v) const { add_at(p, i, v); }
+};
+
+// The corner scatter of grad_data: g times each corner's weight added into gd
+// (gd.add(plane index, value)).
+template <int ND, typename G>
+__device__ __forceinline__ void scatter_to(const int* in, const G& gd, const Axis& ax,
+                                           const Axis& ay, const Axis& az, float g) {
   const float ux = 1.0f - ax.t, uy = 1.0f - ay.t, uz = 1.0f - az.t;
   if (ND == 1) {
-    add_at(gd, ax.i0, g * ux);
-    add_at(gd, ax.i1, g * ax.t);
+    gd.add(ax.i0, g * ux);
+    gd.add(ax.i1, g * ax.t);
     return;
   }
   if (ND == 2) {
     const float g0 = g * uy, g1 = g * ay.t;
-    add_at(gd, plane_index<2>(in, ax.i0, ay.i0, 0), g0 * ux);
-    add_at(gd, plane_index<2>(in, ax.i1, ay.i0, 0), g0 * ax.t);
-    add_at(gd, plane_index<2>(in, ax.i0, ay.i1, 0), g1 * ux);
-    add_at(gd, plane_index<2>(in, ax.i1, ay.i1, 0), g1 * ax.t);
+    gd.add(plane_index<2>(in, ax.i0, ay.i0, 0), g0 * ux);
+    gd.add(plane_index<2>(in, ax.i1, ay.i0, 0), g0 * ax.t);
+    gd.add(plane_index<2>(in, ax.i0, ay.i1, 0), g1 * ux);
+    gd.add(plane_index<2>(in, ax.i1, ay.i1, 0), g1 * ax.t);
     return;
   }
 #pragma unroll
@@ -274,21 +284,35 @@ __device__ __forceinline__ void scatter(const int* in, float* __restrict__ gd, c
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const float w = (a ? ax.t : ux) * (b ? ay.t : uy) * (e ? az.t : uz);
-        add_at(gd, plane_index<3>(in, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, e ? az.i1 : az.i0), g * w);
+        gd.add(plane_index<3>(in, a ? ax.i1 : ax.i0, b ? ay.i1 : ay.i0, e ? az.i1 : az.i0), g * w);
       }
 }
 
-// blend_grad into dxyz (may be null) and scatter into gd (may be null).
 template <int ND>
-__device__ __forceinline__ void sample_grad(const int* in, const float* __restrict__ d,
-                                            const Axis& ax, const Axis& ay, const Axis& az,
-                                            float g, float* dxyz, float* __restrict__ gd) {
+__device__ __forceinline__ void scatter(const int* in, float* __restrict__ gd, const Axis& ax,
+                                        const Axis& ay, const Axis& az, float g) {
+  scatter_to<ND>(in, FloatScatter{gd}, ax, ay, az, g);
+}
+
+// blend_grad into dxyz (may be null) and scatter into *gd (may be null).
+template <int ND, typename G>
+__device__ __forceinline__ void sample_grad_to(const int* in, const float* __restrict__ d,
+                                               const Axis& ax, const Axis& ay, const Axis& az,
+                                               float g, float* dxyz, const G* gd) {
   if (dxyz) {
     float c[1 << ND];
     gather<ND>(in, ChannelPtr{d}, ax, ay, az, c);
     blend_grad<ND>(c, ax, ay, az, g, dxyz);
   }
-  if (gd) scatter<ND>(in, gd, ax, ay, az, g);
+  if (gd) scatter_to<ND>(in, *gd, ax, ay, az, g);
+}
+
+template <int ND>
+__device__ __forceinline__ void sample_grad(const int* in, const float* __restrict__ d,
+                                            const Axis& ax, const Axis& ay, const Axis& az,
+                                            float g, float* dxyz, float* __restrict__ gd) {
+  const FloatScatter sink{gd};
+  sample_grad_to<ND>(in, d, ax, ay, az, g, dxyz, gd ? &sink : nullptr);
 }
 
 }  // namespace cpab

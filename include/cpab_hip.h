@@ -139,10 +139,14 @@ int cpab_backward_project(int ndim, int64_t nP, int64_t n_theta, int batched, in
  * same device.  They equal the default mode's to its tolerance (the integer
  * quantum is 2^-(62 - ceil(log2(nP * nstepsolver))) of the row's largest
  * value); a component that sums non-finite values is +inf, -inf or NaN as
- * the float sum would be.  grad_data of cpab_transform_data_backward keeps
- * its float-atomic scatter.  Both passes take the default's bodies; the
- * benchmark steps take 1.8-2.2x their default time.  The *_workspace_size
- * functions size the workspace of the calling thread's current mode. */
+ * the float sum would be.  grad_data of cpab_transform_data_backward is
+ * summed the same way (64-bit integers at each batch row's scale, from its
+ * largest scatter contribution; non-finite terms as floats), which takes
+ * cpab_transform_data_backward_data_workspace_size(...) more bytes of
+ * workspace (CPAB_ERR_INVALID without them).  Both passes take the default's
+ * bodies; the benchmark steps take 1.8-2.2x their default time.  The
+ * *_workspace_size functions size the workspace of the calling thread's
+ * current mode. */
 void cpab_set_deterministic(int on);
 int cpab_deterministic(void);
 
@@ -245,6 +249,17 @@ int cpab_transform_data_forward(int ndim, int64_t n_batch, int64_t n_channels,
 /* Bytes of device workspace cpab_transform_data_backward needs. */
 int64_t cpab_transform_data_backward_workspace_size(int ndim, int64_t n_batch,
                                                     const int64_t* out_size, int nC);
+
+/* Additional workspace bytes cpab_transform_data_backward needs for
+ * grad_data in the deterministic mode (no counterpart in the reference; for
+ * the callers of cpab_set_deterministic): 0 in the default mode; in the
+ * calling thread's deterministic mode, a 64-bit integer sum per grad_data
+ * element (n_batch * n_channels * prod(in_size) * 8 bytes and a few hundred
+ * more).  A deterministic backward that is given grad_data needs this and
+ * cpab_transform_data_backward_workspace_size(...) added together. */
+int64_t cpab_transform_data_backward_data_workspace_size(int ndim, int64_t n_batch,
+                                                         int64_t n_channels,
+                                                         const int64_t* in_size);
 
 /* Backward of cpab_transform_data_forward in one launch: the resampling
  * gradient at each final point (the interp backward, summed over channels)

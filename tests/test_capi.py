@@ -229,3 +229,19 @@ def test_deterministic_toggle_is_per_thread():
         with nat.deterministic(True):
             raise ValueError("inside")
     assert lib.cpab_deterministic() == 0
+
+
+def test_data_workspace_size_follows_the_mode():
+    # The deterministic grad_data's extra workspace: none in the default mode,
+    # a 64-bit sum per grad_data element in the deterministic one (no HIP call).
+    lib = _native.load_library()
+    ins = (ctypes.c_int64 * 2)(30, 26)
+    assert lib.cpab_transform_data_backward_data_workspace_size(2, 4, 3, ins) == 0
+    lib.cpab_set_deterministic(1)
+    try:
+        n = lib.cpab_transform_data_backward_data_workspace_size(2, 4, 3, ins)
+        assert 4 * 3 * 30 * 26 * 8 <= n <= 4 * 3 * 30 * 26 * 8 + 4096
+        assert lib.cpab_transform_data_backward_data_workspace_size(4, 4, 3, ins) == 0
+        assert lib.cpab_transform_data_backward_data_workspace_size(2, 4, 0, ins) == 0
+    finally:
+        lib.cpab_set_deterministic(0)

@@ -1,7 +1,7 @@
 """The deterministic backward (``Cpab.set_solver_params(deterministic_grad=True)``,
-``cpab_set_deterministic``): two runs give the same moments, theta gradients
-and point gradients bit for bit, and each stays within the oracle's tolerance,
-as the default mode's float-atomic sums do."""
+``cpab_set_deterministic``): two runs give the same moments, theta gradients,
+point gradients and transform_data data gradients bit for bit, and each stays
+within the oracle's tolerance, as the default mode's float-atomic sums do."""
 import numpy as np
 import pytest
 import torch
@@ -181,3 +181,45 @@ def test_transform_data_repeatable(cuda, tess, ins):
     gg, _ = orc.interp_backward(nd, data, grid_t, ins, gout, want_data=False)
     mom, _ = orc.backward(grid, As, gg, p.nc, 50)
     assert_theta_grad_close(g1, mom, p.basis)
+
+
+@pytest.mark.parametrize("tess,C,ins,outs", [([6, 6], 3, (30, 26), [24, 28]),
+                                             ([3, 3, 3], 2, (10, 9, 8), [8, 9, 7]),
+                                             ([10], 2, (50,), [40])])
+def test_transform_data_data_gradient_repeatable(cuda, tess, C, ins, outs):
+    # data and theta both require grad: grad_data, summed as 64-bit integers
+    # at each batch row's scale, is the same bit for bit on two runs and within
+    # the scatter tolerance of the oracle; the theta gradient too.
+    from helpers import scatter_magnitude
+    T = _det_cpab(tess)
+    nd = len(tess)
+    B = 2
+    rng = np.random.default_rng(350 + nd)
+    data = rng.random((B, C, *ins)).astype(np.float32)
+    theta = seeded_theta(T, B, 0.5, 351)
+    gout = rng.standard_normal((B, C, *outs)).astype(np.float32)
+
+    def run():
+        d_t = torch.tensor(data, device=cuda, requires_grad=True)
+        th = torch.tensor(theta, device=cuda, requires_grad=True)
+        out = T.transform_data(d_t, th, list(outs))
+        out.backward(torch.tensor(gout, device=cuda))
+        return d_t.grad.cpu().numpy(), th.grad.cpu().numpy()
+
+    gd1, gth1 = run()
+    gd2, gth2 = run()
+    np.testing.assert_array_equal(gd1, gd2)
+    np.testing.assert_array_equal(gth1, gth2)
+    p = T.params
+    grid = T.uniform_meshgrid(list(outs)).cpu().numpy()
+    As = orc.affine(theta, p.basis).reshape(B, p.nC, nd, nd + 1)
+    if nd == 1:
+        grid_t = orc.forward_closed_1d(grid, As, p.nc)
+    else:
+        grid_t = orc.forward_trels(grid, orc.expm(nd, As, 1 / 50), As, p.nc, 50)
+    gg, rd = orc.interp_backward(nd, data, grid_t, outs, gout)
+    mag = scatter_magnitude(data.shape, grid_t, outs, gout)
+    err = np.abs(gd1.astype(np.float64) - rd)
+    assert (err <= 1e-4 * mag + 1e-12).all()
+    mom, _ = orc.backward(grid, As, gg, p.nc, 50)
+    assert_theta_grad_close(gth1, mom, p.basis)
