@@ -208,8 +208,10 @@ class Cpab(object):
         return chain_transformer(grid, theta_chain * dt, self.params)
 
     def interpolate(self, data, grid, outsize):
-        """Border-clamped linear interpolation of ``data`` at ``grid``."""
-        return interpolate(self.params.ndim, data, grid, outsize)
+        """Border-clamped linear interpolation of ``data`` at ``grid``; its data
+        gradient is deterministic under ``set_solver_params(deterministic_grad=True)``."""
+        return interpolate(self.params.ndim, data, grid, outsize,
+                           deterministic=bool(getattr(self.params, "deterministic_grad", False)))
 
     def transform_data(self, data, theta, outsize):
         """Warp ``data`` [n_batch, C, *in_size] by theta onto an ``outsize`` grid.

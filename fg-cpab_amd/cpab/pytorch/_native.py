@@ -70,6 +70,9 @@ _SIGNATURES = {
                                    ctypes.POINTER(_c_i64)]),
     "cpab_interp_backward": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                       _c_vp, _c_vp, _c_vp]),
+    "cpab_interp_backward_workspace_size": (_c_i64, [_c_int, _c_i64, _c_i64, _c_vp]),
+    "cpab_interp_backward_ws": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                         _c_vp, _c_vp, _c_vp, _c_i64, _c_vp]),
 }
 
 
@@ -287,6 +290,22 @@ class Native:
                                             _lengths(data.shape[2:]), _lengths(outsize),
                                             _ptr(data), _ptr(grid), _ptr(out),
                                             _stream(data.device)), "cpab_interp_forward")
+
+    def interp_backward_workspace_size(self, ndim, data):
+        """Workspace bytes of interp_backward_ws's grad_data in this thread's
+        current mode (0 unless deterministic)."""
+        return int(self.lib.cpab_interp_backward_workspace_size(
+            ndim, data.shape[0], data.shape[1], _lengths(data.shape[2:])))
+
+    def interp_backward_ws(self, ndim, data, grid, outsize, grad_out, grad_grid, grad_data,
+                           workspace):
+        wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        _check(self.lib.cpab_interp_backward_ws(ndim, data.shape[0], data.shape[1],
+                                                _lengths(data.shape[2:]), _lengths(outsize),
+                                                _ptr(data), _ptr(grid), _ptr(grad_out),
+                                                _ptr(grad_grid), _ptr(grad_data), _ptr(workspace),
+                                                wbytes, _stream(data.device)),
+               "cpab_interp_backward_ws")
 
     def interp_backward(self, ndim, data, grid, outsize, grad_out, grad_grid, grad_data):
         _check(self.lib.cpab_interp_backward(ndim, data.shape[0], data.shape[1],

@@ -386,7 +386,86 @@ __global__ __launch_bounds__(256) void det_data_finish_kernel(int64_t per_row, i
         (float)ldexp((double)(long long)gsums[base + i], -shift) + grad_data[base + i];
 }
 
+// Cpab.interpolate's data gradient in the deterministic mode, per grid point
+// p = i0 + o0 (i1 + o1 i2) (the reference's point order; the output is
+// [B, C, o0(, o1(, o2))] with the last axis fastest): MODE 0 takes each batch
+// row's largest finite |contribution| into gstat (zero before), MODE 1 adds
+// the contributions through FixedScatter at the row's scale.  The
+// contributions are the gather kernels' scatter (scatter_to, the same
+// arithmetic).  One thread per grid point.
+template <int ND, int MODE>
+__global__ __launch_bounds__(256) void interp_det_kernel(int C, int in0, int in1, int in2, int o0,
+                                                         int o1, int o2, int nP,
+                                                         const float* __restrict__ grid,
+                                                         const float* __restrict__ grad_out,
+                                                         unsigned* __restrict__ gstat,
+                                                         unsigned long long* __restrict__ gsums,
+                                                         float* __restrict__ grad_data) {
+  const int b = blockIdx.y;
+  const int in[3] = {in0, in1, in2};
+  const int64_t plane_in = (int64_t)in0 * (ND >= 2 ? in1 : 1) * (ND == 3 ? in2 : 1);
+  const int shift = MODE == 1 ? det_shift(gstat[b], nP, 1 << ND) : 0;
+  float m = 0.0f;
+  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < nP; p += gridDim.x * blockDim.x) {
+    const int i0 = p % o0, r = p / o0;
+    const int i1 = ND >= 2 ? r % o1 : 0, i2 = ND == 3 ? r / o1 : 0;
+    const int o = ND == 1 ? p : ND == 2 ? i0 * o1 + i1 : (i0 * o1 + i1) * o2 + i2;
+    const float* gp = grid + (size_t)b * ND * nP + p;
+    const Axis ax = axis_of(gp[0], in0);
+    const Axis ay = ND >= 2 ? axis_of(gp[(size_t)nP], in1) : Axis{0, 0, 0.0f};
+    const Axis az = ND == 3 ? axis_of(gp[2 * (size_t)nP], in2) : Axis{0, 0, 0.0f};
+    for (int c = 0; c < C; ++c) {
+      const size_t bc = (size_t)b * C + c;
+      const float g = grad_out[bc * nP + o];
+      if constexpr (MODE == 0)
+        scatter_to<ND>(in, AbsMaxSink{&m}, ax, ay, az, g);
+      else
+        scatter_to<ND>(in, FixedScatter{gsums + bc * plane_in, grad_data + bc * plane_in, shift},
+                       ax, ay, az, g);
+    }
+  }
+  if constexpr (MODE == 0) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (__lane_id() == 0 && m > 0.0f)
+      __hip_atomic_fetch_max(gstat + b, __float_as_uint(m), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 }  // namespace
+
+hipError_t launch_det_interp_data(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                                  const int64_t* out_size, const float* grid,
+                                  const float* grad_out, unsigned* gstat,
+                                  unsigned long long* gsums, float* grad_data, hipStream_t s) {
+  int64_t nP = 1, plane = 1;
+  for (int k = 0; k < ndim; ++k) {
+    nP *= out_size[k];
+    plane *= in_size[k];
+  }
+  if (B <= 0 || nP <= 0 || C <= 0) return hipSuccess;
+  const int in0 = (int)in_size[0], in1 = ndim >= 2 ? (int)in_size[1] : 1;
+  const int in2 = ndim == 3 ? (int)in_size[2] : 1;
+  const int o0 = (int)out_size[0], o1 = ndim >= 2 ? (int)out_size[1] : 1;
+  const int o2 = ndim == 3 ? (int)out_size[2] : 1;
+  const dim3 blocks((unsigned)std::min<int64_t>((nP + 255) / 256, 1024), (unsigned)B);
+  auto run = [&](auto stat_kernel, auto add_kernel) {
+    hipLaunchKernelGGL(stat_kernel, blocks, dim3(256), 0, s, (int)C, in0, in1, in2, o0, o1, o2,
+                       (int)nP, grid, grad_out, gstat, gsums, grad_data);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(add_kernel, blocks, dim3(256), 0, s, (int)C, in0, in1, in2, o0, o1, o2,
+                       (int)nP, grid, grad_out, gstat, gsums, grad_data);
+    return hipGetLastError();
+  };
+  hipError_t e;
+  if (ndim == 1) e = run(interp_det_kernel<1, 0>, interp_det_kernel<1, 1>);
+  else if (ndim == 2) e = run(interp_det_kernel<2, 0>, interp_det_kernel<2, 1>);
+  else e = run(interp_det_kernel<3, 0>, interp_det_kernel<3, 1>);
+  if (e != hipSuccess) return e;
+  return launch_det_finish_rows(ndim, B, C * plane, nP, gstat, gsums, grad_data, s);
+}
 
 hipError_t launch_det_data_stat(int ndim, const ImageShape& img, int64_t n_batch,
                                 const float* final_points, const float* grad_out,
@@ -406,15 +485,21 @@ hipError_t launch_det_data_stat(int ndim, const ImageShape& img, int64_t n_batch
   return hipGetLastError();
 }
 
+hipError_t launch_det_finish_rows(int ndim, int64_t n_batch, int64_t per_row, int64_t nP,
+                                  const unsigned* gstat, const unsigned long long* gsums,
+                                  float* grad_data, hipStream_t s) {
+  if (n_batch <= 0 || per_row <= 0) return hipSuccess;
+  const dim3 grid((unsigned)std::min<int64_t>((per_row + 255) / 256, 4096), (unsigned)n_batch);
+  hipLaunchKernelGGL(det_data_finish_kernel, grid, dim3(256), 0, s, per_row, (int)nP, ndim, gstat,
+                     gsums, grad_data);
+  return hipGetLastError();
+}
+
 hipError_t launch_det_data_finish(int ndim, const ImageShape& img, int64_t n_batch,
                                   const unsigned* gstat, const unsigned long long* gsums,
                                   float* grad_data, hipStream_t s) {
-  const int64_t per_row = (int64_t)img.C * img.plane_in;
-  if (n_batch <= 0 || per_row <= 0) return hipSuccess;
-  const dim3 grid((unsigned)std::min<int64_t>((per_row + 255) / 256, 4096), (unsigned)n_batch);
-  hipLaunchKernelGGL(det_data_finish_kernel, grid, dim3(256), 0, s, per_row, img.nP, ndim, gstat,
-                     gsums, grad_data);
-  return hipGetLastError();
+  return launch_det_finish_rows(ndim, n_batch, (int64_t)img.C * img.plane_in, img.nP, gstat, gsums,
+                                grad_data, s);
 }
 
 hipError_t dispatch_det_any(const BackwardJob& j, int adaptive, const LaunchCfg& cfg,

@@ -1041,4 +1041,59 @@ int cpab_interp_backward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
   return rc;
 }
 
+int64_t cpab_interp_backward_workspace_size(int ndim, int64_t B, int64_t C,
+                                            const int64_t* in_size) {
+  if (!t_deterministic || ndim < 1 || ndim > 3 || B <= 0 || C <= 0 || !in_size) return 0;
+  int64_t plane = 1;
+  for (int k = 0; k < ndim; ++k) {
+    if (in_size[k] <= 0) return 0;
+    plane *= in_size[k];
+  }
+  return data_workspace(0, B, C, plane).total;
+}
+
+int cpab_interp_backward_ws(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                            const int64_t* out_size, const float* data, const float* grid,
+                            const float* grad_out, float* grad_grid, float* grad_data,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!t_deterministic || grad_data == nullptr)
+    return cpab_interp_backward(ndim, B, C, in_size, out_size, data, grid, grad_out, grad_grid,
+                                grad_data, stream);
+  int rc = check_interp(ndim, B, C, in_size, out_size);
+  if (rc) return rc;
+  CPAB_REQUIRE(data); CPAB_REQUIRE(grid); CPAB_REQUIRE(grad_out);
+  CPAB_ALIGNED(workspace, 16);
+  if (B == 0 || C == 0) return CPAB_OK;
+  int64_t plane = 1;
+  for (int k = 0; k < ndim; ++k) plane *= in_size[k];
+  const DataWorkspace dw = data_workspace(0, B, C, plane);
+  if (workspace == nullptr || workspace_bytes < dw.total)
+    return fail(CPAB_ERR_INVALID,
+                "workspace too small: need %lld bytes (cpab_interp_backward_workspace_size), got "
+                "%lld", (long long)dw.total, (long long)workspace_bytes);
+  hipStream_t s = as_stream(stream);
+  const char* who = "cpab_interp_backward_ws";
+  char* ws = static_cast<char*>(workspace);
+  auto* gstat = reinterpret_cast<unsigned*>(ws + dw.gstat_offset);
+  auto* gsums = reinterpret_cast<unsigned long long*>(ws + dw.gsums_offset);
+  hipEvent_t ev = nullptr;
+  const bool timed = prof_begin(s, &ev);
+  // grad_grid from the gather kernel without its scatter; grad_data from the
+  // deterministic scatter
+  if (grad_grid)
+    rc = check_hip(cpab::launch_interp_backward(ndim, B, C, in_size, out_size, data, grid,
+                                                grad_out, grad_grid, nullptr, s),
+                   who);
+  if (rc == CPAB_OK)
+    rc = check_hip(cpab::launch_fill(grad_data, B * C * plane, 0.0f, s), who);
+  if (rc == CPAB_OK)
+    rc = check_hip(cpab::launch_fill(reinterpret_cast<float*>(ws), dw.total / 4, 0.0f, s), who);
+  if (rc == CPAB_OK)
+    rc = check_hip(cpab::launch_det_interp_data(ndim, B, C, in_size, out_size, grid, grad_out,
+                                                gstat, gsums, grad_data, s),
+                   who);
+  prof_end(timed, ev, "interp_backward", s);
+  return rc;
+}
+
 }  // extern "C"

@@ -157,6 +157,18 @@ hipError_t launch_det_data_stat(int ndim, const ImageShape& img, int64_t n_batch
 hipError_t launch_det_data_finish(int ndim, const ImageShape& img, int64_t n_batch,
                                   const unsigned* det_gstat, const unsigned long long* det_gsums,
                                   float* grad_data, hipStream_t s);
+// grad_data [B, per_row] += gsums / 2^shift_b (det_shift of gstat[b] for nP
+// output positions of 2^ndim contributions each).
+hipError_t launch_det_finish_rows(int ndim, int64_t n_batch, int64_t per_row, int64_t nP,
+                                  const unsigned* gstat, const unsigned long long* gsums,
+                                  float* grad_data, hipStream_t s);
+// Cpab.interpolate's grad_data [B, C, *in_size] in the deterministic mode,
+// from the grid [B, ndim, prod(out_size)] and grad_out [B, C, *out_size]:
+// gstat [B] and gsums [B, C, prod(in_size)] zero, grad_data zero before.
+hipError_t launch_det_interp_data(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                                  const int64_t* out_size, const float* grid,
+                                  const float* grad_out, unsigned* gstat,
+                                  unsigned long long* gsums, float* grad_data, hipStream_t s);
 
 hipError_t launch_interp_forward(int ndim, int64_t B, int64_t C, const int64_t* in_size,
                                  const int64_t* out_size, const float* data, const float* grid,

@@ -143,7 +143,8 @@ int cpab_backward_project(int ndim, int64_t nP, int64_t n_theta, int batched, in
  * summed the same way (64-bit integers at each batch row's scale, from its
  * largest scatter contribution; non-finite terms as floats), which takes
  * cpab_transform_data_backward_data_workspace_size(...) more bytes of
- * workspace (CPAB_ERR_INVALID without them).  Both passes take the default's
+ * workspace (CPAB_ERR_INVALID without them); cpab_interp_backward_ws does
+ * the same for the resampling's grad_data.  Both passes take the default's
  * bodies; the benchmark steps take 1.8-2.2x their default time.  The
  * *_workspace_size functions size the workspace of the calling thread's
  * current mode. */
@@ -300,6 +301,25 @@ int cpab_interp_backward(int ndim, int64_t n_batch, int64_t n_channels, const in
                          const int64_t* out_size, const float* data, const float* grid,
                          const float* grad_out, float* grad_grid, float* grad_data,
                          void* stream);
+
+/* Workspace bytes cpab_interp_backward_ws needs for grad_data: 0 in the
+ * default mode; in the calling thread's deterministic mode
+ * (cpab_set_deterministic) a 64-bit integer sum per grad_data element
+ * (B * C * prod(in_size) * 8 bytes and a few hundred more).  No counterpart
+ * in the reference; for the callers of cpab_set_deterministic. */
+int64_t cpab_interp_backward_workspace_size(int ndim, int64_t B, int64_t C,
+                                            const int64_t* in_size);
+
+/* cpab_interp_backward with a workspace (no counterpart in the reference).
+ * In the calling thread's deterministic mode, grad_data (when requested) is
+ * summed as 64-bit integers at each batch row's scale, from its largest
+ * scatter contribution (non-finite terms as floats), so it is the same on
+ * every run; the workspace must hold cpab_interp_backward_workspace_size(...)
+ * bytes.  Otherwise it is cpab_interp_backward (the workspace unused). */
+int cpab_interp_backward_ws(int ndim, int64_t B, int64_t C, const int64_t* in_size,
+                            const int64_t* out_size, const float* data, const float* grid,
+                            const float* grad_out, float* grad_grid, float* grad_data,
+                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Kernel timing for benchmarks (no reference counterpart; the reference timed
  * with torch.cuda.synchronize + perf_counter, benchmarks/benchmark_transformer.py:76-84).

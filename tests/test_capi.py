@@ -245,3 +245,15 @@ def test_data_workspace_size_follows_the_mode():
         assert lib.cpab_transform_data_backward_data_workspace_size(2, 4, 0, ins) == 0
     finally:
         lib.cpab_set_deterministic(0)
+
+
+def test_interp_workspace_size_follows_the_mode():
+    lib = _native.load_library()
+    ins = (ctypes.c_int64 * 3)(9, 8, 10)
+    assert lib.cpab_interp_backward_workspace_size(3, 2, 3, ins) == 0
+    lib.cpab_set_deterministic(1)
+    try:
+        n = lib.cpab_interp_backward_workspace_size(3, 2, 3, ins)
+        assert 2 * 3 * 720 * 8 <= n <= 2 * 3 * 720 * 8 + 4096
+    finally:
+        lib.cpab_set_deterministic(0)

@@ -223,3 +223,41 @@ def test_transform_data_data_gradient_repeatable(cuda, tess, C, ins, outs):
     assert (err <= 1e-4 * mag + 1e-12).all()
     mom, _ = orc.backward(grid, As, gg, p.nc, 50)
     assert_theta_grad_close(gth1, mom, p.basis)
+
+
+@pytest.mark.parametrize("nd,ins,outs", [(1, (37,), (50,)), (2, (21, 30), (24, 33)),
+                                         (3, (9, 8, 10), (7, 6, 9))])
+def test_interpolate_data_gradient_repeatable(cuda, nd, ins, outs):
+    # Cpab.interpolate under deterministic_grad: the data gradient (summed as
+    # 64-bit integers, cpab_interp_backward_ws) is the same on two runs and
+    # within the scatter tolerance of the oracle, including points beyond the
+    # border (clamped corners, weights outside [0, 1]); grad_grid equals the
+    # default path's bit for bit.
+    from helpers import scatter_magnitude
+    tess = {1: [5], 2: [3, 3], 3: [2, 2, 2]}[nd]
+    T = _det_cpab(tess)
+    rng = np.random.default_rng(360 + nd)
+    B, C = 2, 3
+    data = rng.random((B, C, *ins)).astype(np.float32)
+    nP = int(np.prod(outs))
+    grid = (rng.random((B, nd, nP)) * 1.3 - 0.15).astype(np.float32)
+    gout = rng.standard_normal((B, C, *outs)).astype(np.float32)
+
+    def run(params_det):
+        T.params.deterministic_grad = params_det
+        d_t = torch.tensor(data, device=cuda, requires_grad=True)
+        g_t = torch.tensor(grid, device=cuda, requires_grad=True)
+        T.interpolate(d_t, g_t, list(outs)).backward(torch.tensor(gout, device=cuda))
+        return d_t.grad.cpu().numpy(), g_t.grad.cpu().numpy()
+
+    gd1, gg1 = run(True)
+    gd2, gg2 = run(True)
+    _, gg0 = run(False)
+    T.params.deterministic_grad = True
+    np.testing.assert_array_equal(gd1, gd2)
+    np.testing.assert_array_equal(gg1, gg2)
+    np.testing.assert_array_equal(gg1, gg0)
+    _, rd = orc.interp_backward(nd, data, grid, outs, gout)
+    mag = scatter_magnitude(data.shape, grid, outs, gout)
+    err = np.abs(gd1.astype(np.float64) - rd)
+    assert (err <= 1e-4 * mag + 1e-12).all(), float((err / (mag + 1e-30)).max())
