@@ -577,7 +577,7 @@ const char* cpab_last_error_string(void) { return g_last_error.c_str(); }
 // (cpab_backward_project; projection arguments of the chain and
 // transform_data backwards).  200: the fused transform_data entry points take
 // the uniform grid's per-axis coordinates instead of the meshgrid.
-int cpab_abi_version(void) { return 400; }
+int cpab_abi_version(void) { return 401; }
 
 int cpab_affine(int ndim, int64_t n_theta, int nC, int d, const float* theta,
                 const int32_t* row_ptr, const int32_t* col_idx, const float* vals, float* As,

@@ -46,7 +46,8 @@ extern "C" {
 const char* cpab_last_error_string(void);
 
 /* ABI version (major*100 + minor).  400: the transform_data entry points take
- * seed_grad. */
+ * seed_grad.  401: the deterministic mode (cpab_set_deterministic and the
+ * workspace sizes and cpab_interp_backward_ws that go with it). */
 int cpab_abi_version(void);
 
 /* A = B theta per theta: As[b, r] = sum_k vals[k] * theta[b, col_idx[k]] over
