@@ -1064,8 +1064,17 @@ int cpab_interp_backward_ws(int ndim, int64_t B, int64_t C, const int64_t* in_si
   CPAB_REQUIRE(data); CPAB_REQUIRE(grid); CPAB_REQUIRE(grad_out);
   CPAB_ALIGNED(workspace, 16);
   if (B == 0 || C == 0) return CPAB_OK;
-  int64_t plane = 1;
-  for (int k = 0; k < ndim; ++k) plane *= in_size[k];
+  int64_t plane = 1, nP = 1;
+  for (int k = 0; k < ndim; ++k) {
+    plane *= in_size[k];
+    nP *= out_size[k];
+  }
+  // the deterministic scatter indexes a batch row's points with 32-bit ints
+  // and takes one grid row per batch row
+  if (nP >= (1LL << 31) || B >= 65536)
+    return fail(CPAB_ERR_INVALID, "the deterministic grad_data takes fewer than 2^31 output "
+                "points per batch row and fewer than 65536 batch rows, got %lld and %lld",
+                (long long)nP, (long long)B);
   const DataWorkspace dw = data_workspace(0, B, C, plane);
   if (workspace == nullptr || workspace_bytes < dw.total)
     return fail(CPAB_ERR_INVALID,
