@@ -257,3 +257,26 @@ def test_interp_workspace_size_follows_the_mode():
         assert 2 * 3 * 720 * 8 <= n <= 2 * 3 * 720 * 8 + 4096
     finally:
         lib.cpab_set_deterministic(0)
+
+
+def test_deterministic_interp_limits():
+    _run_without_gpu("_check_deterministic_interp_limits")
+
+
+def _check_deterministic_interp_limits():
+    lib = _native.load_library()
+    p = ctypes.c_void_p(256)
+    lib.cpab_set_deterministic(1)
+    try:
+        ins = (ctypes.c_int64 * 2)(8, 8)
+        big = (ctypes.c_int64 * 2)(1 << 16, 1 << 15)   # 2^31 output points
+        rc = lib.cpab_interp_backward_ws(2, 1, 1, ins, big, p, p, p, None, p, p, 1 << 20, None)
+        assert rc == 1 and "2^31" in _err(lib)
+        small = (ctypes.c_int64 * 2)(2, 2)
+        rc = lib.cpab_interp_backward_ws(2, 70000, 1, ins, small, p, p, p, None, p, p, 1 << 30, None)
+        assert rc == 1 and "65536" in _err(lib)
+        # too small a workspace is rejected before anything is enqueued
+        rc = lib.cpab_interp_backward_ws(2, 2, 1, ins, small, p, p, p, None, p, p, 16, None)
+        assert rc == 1 and "workspace too small" in _err(lib)
+    finally:
+        lib.cpab_set_deterministic(0)
